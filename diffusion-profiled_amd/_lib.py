@@ -1,0 +1,104 @@
+"""ctypes binding of the C ABI in ``include/dpa_fp8.h`` (``lib/libdpa_fp8.so``).
+
+Every entry point takes raw device pointers, sizes and a ``hipStream_t``; this module only
+declares the signatures and turns non-zero status codes into ``RuntimeError``. There is no
+fallback: if the library is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_void_p
+
+from . import build as _build
+
+c_float_p = POINTER(c_float)
+
+# name -> (restype, argtypes); kept in the order of include/dpa_fp8.h
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "dpa_status_string": (c_char_p, [c_int]),
+    "dpa_abi_version": (c_int, []),
+    "dpa_quant_workspace_bytes": (c_int64, [c_int64]),
+    "dpa_quantize_fp8_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "dpa_quantize_fp8_delayed_bf16": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "dpa_conv2d_fwd_fp8": (
+        c_int,
+        [c_void_p] * 6 + [c_int] * 9 + [c_void_p],
+    ),
+    "dpa_conv2d_dgrad_workspace_bytes": (c_int64, [c_int] * 4),
+    "dpa_conv2d_dgrad_fp8": (
+        c_int,
+        [c_void_p] * 6 + [c_int64] + [c_int] * 9 + [c_void_p],
+    ),
+    "dpa_conv2d_dgrad_fp8_wt": (
+        c_int,
+        [c_void_p] * 5 + [c_int] * 9 + [c_void_p],
+    ),
+    "dpa_weight_transpose_fp8": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "dpa_conv2d_wgrad_workspace_bytes": (c_int64, [c_int] * 10),
+    "dpa_conv2d_wgrad_fp8": (
+        c_int,
+        [c_void_p] * 6 + [c_int64] + [c_int] * 10 + [c_void_p],
+    ),
+    "dpa_gemm_fp8": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_gn_silu_fwd_bf16": (
+        c_int,
+        [c_void_p] * 8 + [c_int] * 4 + [c_float, c_void_p],
+    ),
+    "dpa_gn_silu_bwd_workspace_bytes": (c_int64, [c_int] * 4),
+    "dpa_gn_silu_bwd_bf16": (
+        c_int,
+        [c_void_p] * 14 + [c_int64] + [c_int] * 4 + [c_void_p],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path():
+    return _build.LIB_PATH
+
+
+def load(build_if_missing: bool = True) -> ctypes.CDLL:
+    """Load (once) and return the library. Builds it only when no built library exists."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = _build.LIB_PATH
+        if not path.exists():
+            if not build_if_missing:
+                raise RuntimeError(f"FP8 HIP library not built: {path}")
+            _build.build_library()
+        lib = ctypes.CDLL(str(path))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return load().dpa_status_string(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed: {status_string(status)} (status {status})")
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point that returns a status code; raise on failure."""
+    check(getattr(load(), name)(*args), name)
+
+
+def query(name: str, *args) -> int:
+    """Call an entry point that returns a size."""
+    return int(getattr(load(), name)(*args))

@@ -1,0 +1,177 @@
+// Shared device/host helpers for the gfx950 FP8 path: bf16 and OCP-e4m3 conversions,
+// the per-tensor scale rule, MFMA wrappers and launch plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dpa_fp8.h"
+
+namespace dpa {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kFp8Max = 448.0f;  // torch.finfo(torch.float8_e4m3fn).max
+
+// ---------------------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------------------
+__host__ __device__ inline float bf16_bits_to_f32(uint32_t b16) {
+  uint32_t u = b16 << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> canonical quiet NaN of the same sign.
+__host__ __device__ inline uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// ---------------------------------------------------------------------------------------
+// Per-tensor scale: amax > 0 ? RN32(amax / 448) : 1  (fp8_kernels.py:100-101).
+// amax is carried as the bf16 bit pattern of |x| (max over integer patterns equals the max
+// over values for non-negative bf16, so the reduction is exact and order-free).
+// ---------------------------------------------------------------------------------------
+__host__ __device__ inline float scale_from_amax_bits(uint32_t amax_bf16_bits) {
+  float amax = bf16_bits_to_f32(amax_bf16_bits);
+  return amax > 0.0f ? amax / kFp8Max : 1.0f;
+}
+
+// ---------------------------------------------------------------------------------------
+// fp32 -> OCP e4m3 (float8_e4m3fn) with round-to-nearest-even, software version.
+// |v| > 464 and NaN -> 0x7f (NaN), like torch's CPU conversion; 448 < |v| <= 464 -> 448.
+// Used as the in-kernel reference of the GPU self-test and for documentation of the rule.
+// ---------------------------------------------------------------------------------------
+__host__ __device__ inline uint32_t e4m3_rne_soft(float v) {
+  uint32_t b;
+  __builtin_memcpy(&b, &v, 4);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t a = b & 0x7fffffffu;
+  if (a > 0x43e80000u) return sign | 0x7fu;  // > 464 (incl. inf/NaN)
+  if (a >= 0x3c800000u) {                    // normal e4m3: |v| >= 2^-6
+    const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+    return sign | ((r >> 20) - 0x3c0u);
+  }
+  // subnormal e4m3: multiples of 2^-9
+  const int e = (int)(a >> 23) - 127;
+  if (e < -127 + 1) return sign;  // fp32 zero / denormal rounds to 0
+  const uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+  const int s = 14 - e;  // >= 21 here
+  if (s >= 25) return sign;
+  uint32_t m = mant >> s;
+  const uint32_t rem = mant & ((1u << s) - 1u);
+  const uint32_t half = 1u << (s - 1);
+  if (rem > half || (rem == half && (m & 1u))) ++m;
+  return sign | m;
+}
+
+// Clamp in the reference kernel's order: max(-448, min(v, 448))  (fp8_kernels.py:119).
+// fminf/fmaxf follow IEEE minNum/maxNum, so a NaN quotient becomes +448.
+__device__ __forceinline__ float clamp_fp8(float v) {
+  return fmaxf(-kFp8Max, fminf(v, kFp8Max));
+}
+
+// Four clamped fp32 values -> four e4m3 bytes (RNE) with gfx950's v_cvt_pk_fp8_f32.
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+  return (uint32_t)r;
+}
+
+// q = e4m3(clamp(RN32(x / scale))) for the 2 bf16 halves of w -> 2 result floats.
+__device__ __forceinline__ float quant_div(float x, float scale) {
+  return clamp_fp8(x / scale);
+}
+
+// 8 bf16 (one uint4) -> 8 e4m3 bytes (one uint2).
+__device__ __forceinline__ uint2 quant8(uint4 v, float scale) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = quant_div(__uint_as_float(w[i] << 16), scale);
+    f[2 * i + 1] = quant_div(__uint_as_float(w[i] & 0xffff0000u), scale);
+  }
+  uint2 o;
+  o.x = pack4_e4m3(f[0], f[1], f[2], f[3]);
+  o.y = pack4_e4m3(f[4], f[5], f[6], f[7]);
+  return o;
+}
+
+// |bf16| magnitude max over the 8 bf16 of a uint4, as packed u16 pairs.
+__device__ __forceinline__ us2 absmax8(us2 acc, uint4 v) {
+  const uint32_t m = 0x7fff7fffu;
+  us2 a = __builtin_bit_cast(us2, v.x & m);
+  us2 b = __builtin_bit_cast(us2, v.y & m);
+  us2 c = __builtin_bit_cast(us2, v.z & m);
+  us2 d = __builtin_bit_cast(us2, v.w & m);
+  acc = __builtin_elementwise_max(acc, a);
+  acc = __builtin_elementwise_max(acc, b);
+  acc = __builtin_elementwise_max(acc, c);
+  acc = __builtin_elementwise_max(acc, d);
+  return acc;
+}
+
+// Wave-level max of a u32 (64 lanes).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    uint32_t o = __shfl_xor(v, off, 64);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------
+// MFMA: D(16x16 f32) += A(16x128 e4m3) * B(128x16 e4m3).
+// Lane l supplies row (l & 15) of A and column (l & 15) of B, 32 K-bytes each at K offset
+// 32 * (l >> 4); lane l receives D[4*(l>>4) + t][l & 15], t = 0..3.
+// The E8M0 block scales are fixed at 127 (2^0), which makes the scaled form a plain GEMM.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ v4f mfma16x16x128_e4m3(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// 16-byte streaming (non-temporal) global load/store.
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st_nt16(void* p, uint4 v) {
+  u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
+
+// Bytes of {hi:lo} selected by sel (v_perm_b32).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// ---------------------------------------------------------------------------------------
+// Host helpers
+// ---------------------------------------------------------------------------------------
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DPA_OK : (int)e;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace dpa

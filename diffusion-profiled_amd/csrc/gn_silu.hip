@@ -1,0 +1,407 @@
+// Fused GroupNorm (+FiLM) + SiLU, forward and backward, NHWC bf16 with fp32 statistics.
+//
+// Reference sites (diffusion/unet.py): F.silu(self.norm1(x)) at :151 and
+// self.dropout(F.silu((w + 1) * self.norm2(x) + b)) at :157-159, with nn.GroupNorm(32, C)
+// (:132-133, eps 1e-5, affine). Under autocast GroupNorm runs in fp32; the FP8 conv then
+// rounds its input to bf16 (diffusion/fp8_kernels.py:835), which is what `out` stores.
+//
+// Layout: one workgroup per (image n, 64-channel slab): 256 threads = 32 pixel lanes x 8
+// granules of 8 channels (16 B of bf16). Every group of the slab lies inside the slab
+// (64 % (C/G) == 0), so the statistics reduce inside the workgroup: 4-channel half-granule
+// partials -> wave shuffles over the 8 pixel lanes of a wave -> LDS over the 4 waves.
+// The kernels make two passes over their inputs (the second mostly from L2).
+#include "dpa_common.hpp"
+
+namespace dpa {
+
+constexpr int kGnThreads = 256;
+constexpr int kSlab = 64;  // channels per workgroup
+
+struct GnArgs {
+  const uint16_t* x;
+  const uint16_t* dout;
+  const float* gamma;
+  const float* beta;
+  const float* fs;  // film scale [N][C] or null
+  const float* fb;  // film shift [N][C]
+  uint16_t* out;
+  float* mean;
+  float* rstd;
+  float* part;  // bwd: [4][N][C] per-image channel sums
+  int N, HW, C, G, cpg;
+  float eps;
+};
+
+__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// Sum v over the 32 pixel lanes that share this thread's granule; result valid in all lanes
+// of LDS slot [granule]. red must hold 4 waves x 8 granules x nvals floats.
+template <int NV>
+__device__ __forceinline__ void slab_reduce(float (&v)[NV], float* red) {
+  const int gq = threadIdx.x & 7;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float s = v[k];
+    s += __shfl_xor(s, 8, 64);
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    v[k] = s;
+  }
+  if ((threadIdx.x & 63) < 8) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) red[(wave * 8 + gq) * NV + k] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    v[k] = red[(0 * 8 + gq) * NV + k] + red[(1 * 8 + gq) * NV + k] +
+           red[(2 * 8 + gq) * NV + k] + red[(3 * 8 + gq) * NV + k];
+  __syncthreads();
+}
+
+// Per-group value from half-granule (4-channel) sums hs[16] of the slab: group of this
+// thread's channel half h (0/1) = consecutive cpg/4 half-granules.
+__device__ __forceinline__ float group_sum(const float* hs, int half_idx, int cpg) {
+  const int hpg = cpg / 4;  // half-granules per group (1, 2, 4, ... 16)
+  const int g0 = (half_idx / hpg) * hpg;
+  float s = 0.f;
+  for (int i = 0; i < hpg; ++i) s += hs[g0 + i];
+  return s;
+}
+
+__global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p) {
+  __shared__ float red[4 * 8 * 2];
+  __shared__ float hs[16];
+  const int n = blockIdx.y;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;  // 0..31
+  const int ch = c0 + gq * 8;
+  const uint16_t* xb = p.x + (int64_t)n * p.HW * p.C + ch;
+
+  // pass 1: mean
+  float s[2] = {0.f, 0.f};
+  for (int px = pl; px < p.HW; px += 32) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
+    s[0] += (f[0] + f[1]) + (f[2] + f[3]);
+    s[1] += (f[4] + f[5]) + (f[6] + f[7]);
+  }
+  slab_reduce<2>(s, red);
+  if ((threadIdx.x >> 3) == 0) {
+    hs[2 * gq] = s[0];
+    hs[2 * gq + 1] = s[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)((int64_t)p.HW * p.cpg);
+  const float mu[2] = {group_sum(hs, 2 * gq, p.cpg) * inv_cnt,
+                       group_sum(hs, 2 * gq + 1, p.cpg) * inv_cnt};
+  __syncthreads();
+
+  // pass 2: biased variance around the mean
+  float q[2] = {0.f, 0.f};
+  for (int px = pl; px < p.HW; px += 32) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = f[e] - mu[e >> 2];
+      q[e >> 2] += d * d;
+    }
+  }
+  slab_reduce<2>(q, red);
+  if ((threadIdx.x >> 3) == 0) {
+    hs[2 * gq] = q[0];
+    hs[2 * gq + 1] = q[1];
+  }
+  __syncthreads();
+  float rs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float var = group_sum(hs, 2 * gq + h, p.cpg) * inv_cnt;
+    rs[h] = 1.0f / sqrtf(var + p.eps);
+  }
+  // statistics out: one writer per group
+  if (pl == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int cc = ch + 4 * h;
+      if (cc % p.cpg == 0) {
+        const int g = cc / p.cpg;
+        p.mean[n * p.G + g] = mu[h];
+        p.rstd[n * p.G + g] = rs[h];
+      }
+    }
+  }
+
+  // pass 3: normalise, affine, FiLM, SiLU, bf16
+  float a[8], b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float gm = p.gamma[ch + e];
+    a[e] = gm;
+    b[e] = p.beta[ch + e];
+  }
+  float fsc[8], fsh[8];
+  if (p.fs) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      fsc[e] = p.fs[(int64_t)n * p.C + ch + e];
+      fsh[e] = p.fb[(int64_t)n * p.C + ch + e];
+    }
+  }
+  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
+  for (int px = pl; px < p.HW; px += 32) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float z[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        float v = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
+        if (p.fs) v = fsc[ee] * v + fsh[ee];
+        z[k] = v / (1.0f + expf(-v));
+      }
+      o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(ob + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// Backward. With zp = film? fs*z + fb : z (z = GN output), u = silu(zp):
+//   g   = dout * sig(zp) * (1 + zp * (1 - sig(zp)))        (d u / d zp)
+//   dfs = sum_hw g * z,  dfb = sum_hw g;   gz = film? g * fs : g
+//   dgamma += sum gz * xhat, dbeta += sum gz;   gxh = gz * gamma
+//   dx = rstd * (gxh - mean_grp(gxh) - xhat * mean_grp(gxh * xhat))
+__global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p) {
+  __shared__ float red[4 * 8 * 32];
+  __shared__ float hs[2][16];
+  const int n = blockIdx.y;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const int64_t base = (int64_t)n * p.HW * p.C + ch;
+
+  float mu[2], rs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int g = (ch + 4 * h) / p.cpg;
+    mu[h] = p.mean[n * p.G + g];
+    rs[h] = p.rstd[n * p.G + g];
+  }
+  float gm[8], bt[8], fsc[8], fsh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    gm[e] = p.gamma[ch + e];
+    bt[e] = p.beta[ch + e];
+    fsc[e] = p.fs ? p.fs[(int64_t)n * p.C + ch + e] : 1.0f;
+    fsh[e] = p.fs ? p.fb[(int64_t)n * p.C + ch + e] : 0.0f;
+  }
+
+  // pass 1: per-channel sums of gz, gz*xhat, g*z, g
+  float acc[4][8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
+  for (int px = pl; px < p.HW; px += 32) {
+    float f[8], d[8];
+    unpack8(*reinterpret_cast<const uint4*>(p.x + base + (int64_t)px * p.C), f);
+    unpack8(*reinterpret_cast<const uint4*>(p.dout + base + (int64_t)px * p.C), d);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xh = (f[e] - mu[e >> 2]) * rs[e >> 2];
+      const float z = xh * gm[e] + bt[e];
+      const float zp = fsc[e] * z + fsh[e];
+      const float sg = 1.0f / (1.0f + expf(-zp));
+      const float g = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
+      const float gz = g * fsc[e];
+      acc[0][e] += gz;
+      acc[1][e] += gz * xh;
+      acc[2][e] += g * z;
+      acc[3][e] += g;
+    }
+  }
+  // reduce the 32 per-channel sums over pixel lanes
+  {
+    float* v = &acc[0][0];
+    float tmp[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) tmp[k] = v[k];
+    slab_reduce<32>(tmp, red);
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = tmp[k];
+  }
+  // per-image channel partials for dgamma/dbeta and the FiLM gradients
+  if (pl == 0) {
+    const int64_t nc = (int64_t)p.N * p.C;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t o = (int64_t)n * p.C + ch + e;
+      p.part[0 * nc + o] = acc[1][e];  // dgamma partial
+      p.part[1 * nc + o] = acc[0][e];  // dbeta partial
+      p.part[2 * nc + o] = acc[2][e];  // dfilm scale
+      p.part[3 * nc + o] = acc[3][e];  // dfilm shift
+    }
+    // group sums of gxh = gz*gamma and gxh*xhat, per 4-channel half
+    float h1[2] = {0.f, 0.f}, h2[2] = {0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      h1[e >> 2] += acc[0][e] * gm[e];
+      h2[e >> 2] += acc[1][e] * gm[e];
+    }
+    hs[0][2 * gq] = h1[0];
+    hs[0][2 * gq + 1] = h1[1];
+    hs[1][2 * gq] = h2[0];
+    hs[1][2 * gq + 1] = h2[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)((int64_t)p.HW * p.cpg);
+  float m1[2], m2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    m1[h] = group_sum(hs[0], 2 * gq + h, p.cpg) * inv_cnt;
+    m2[h] = group_sum(hs[1], 2 * gq + h, p.cpg) * inv_cnt;
+  }
+
+  // pass 2: dx
+  for (int px = pl; px < p.HW; px += 32) {
+    float f[8], d[8];
+    unpack8(*reinterpret_cast<const uint4*>(p.x + base + (int64_t)px * p.C), f);
+    unpack8(*reinterpret_cast<const uint4*>(p.dout + base + (int64_t)px * p.C), d);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float r2[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        const int h = ee >> 2;
+        const float xh = (f[ee] - mu[h]) * rs[h];
+        const float z = xh * gm[ee] + bt[ee];
+        const float zp = fsc[ee] * z + fsh[ee];
+        const float sg = 1.0f / (1.0f + expf(-zp));
+        const float g = d[ee] * (sg * (1.0f + zp * (1.0f - sg)));
+        const float gxh = g * fsc[ee] * gm[ee];
+        r2[k] = rs[h] * (gxh - m1[h] - xh * m2[h]);
+      }
+      o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(p.out + base + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c]; FiLM partials are the
+// per-image results already and are copied out.
+__global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __restrict__ part,
+                                                              float* __restrict__ dgamma,
+                                                              float* __restrict__ dbeta,
+                                                              float* __restrict__ dfs,
+                                                              float* __restrict__ dfb, int N,
+                                                              int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  const int64_t nc = (int64_t)N * C;
+  float sg = 0.f, sb = 0.f;
+  for (int n = 0; n < N; ++n) {
+    sg += part[(int64_t)n * C + c];
+    sb += part[nc + (int64_t)n * C + c];
+    if (dfs) {
+      dfs[(int64_t)n * C + c] = part[2 * nc + (int64_t)n * C + c];
+      dfb[(int64_t)n * C + c] = part[3 * nc + (int64_t)n * C + c];
+    }
+  }
+  dgamma[c] = sg;
+  dbeta[c] = sb;
+}
+
+static bool gn_shape_ok(int N, int HW, int C, int G) {
+  if (N <= 0 || HW <= 0 || C <= 0 || G <= 0) return false;
+  if (C % G != 0 || C % kSlab != 0) return false;
+  const int cpg = C / G;
+  return cpg >= 4 && kSlab % cpg == 0;
+}
+
+}  // namespace dpa
+
+using namespace dpa;
+
+extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                                    const float* film_scale, const float* film_shift, void* out,
+                                    float* mean, float* rstd, int N, int HW, int C, int G,
+                                    float eps, void* stream) {
+  if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
+  if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
+  if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(out, 16)) return DPA_ERR_ALIGN;
+  GnArgs a{};
+  a.x = (const uint16_t*)x;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.fs = film_scale;
+  a.fb = film_shift;
+  a.out = (uint16_t*)out;
+  a.mean = mean;
+  a.rstd = rstd;
+  a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = eps;
+  dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+  gn_silu_fwd_kernel<<<grid, kGnThreads, 0, (hipStream_t)stream>>>(a);
+  return launch_status();
+}
+
+extern "C" int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G) {
+  (void)HW;
+  (void)G;
+  return (int64_t)4 * N * C * 4;
+}
+
+extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                                    const float* beta, const float* film_scale,
+                                    const float* film_shift, const float* mean,
+                                    const float* rstd, void* dx, float* dgamma, float* dbeta,
+                                    float* dfilm_scale, float* dfilm_shift, void* workspace,
+                                    int64_t workspace_bytes, int N, int HW, int C, int G,
+                                    void* stream) {
+  if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
+    return DPA_ERR_NULL;
+  if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
+  if (film_scale && (!dfilm_scale || !dfilm_shift)) return DPA_ERR_NULL;
+  if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
+  if (!workspace || workspace_bytes < dpa_gn_silu_bwd_workspace_bytes(N, HW, C, G))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4))
+    return DPA_ERR_ALIGN;
+  GnArgs a{};
+  a.x = (const uint16_t*)x;
+  a.dout = (const uint16_t*)dout;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.fs = film_scale;
+  a.fb = film_shift;
+  a.out = (uint16_t*)dx;
+  a.mean = const_cast<float*>(mean);
+  a.rstd = const_cast<float*>(rstd);
+  a.part = (float*)workspace;
+  a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+  gn_silu_bwd_kernel<<<grid, kGnThreads, 0, s>>>(a);
+  int st = launch_status();
+  if (st != DPA_OK) return st;
+  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 256), 256, 0, s>>>(
+      (const float*)workspace, dgamma, dbeta, film_scale ? dfilm_scale : nullptr,
+      film_scale ? dfilm_shift : nullptr, N, C);
+  return launch_status();
+}

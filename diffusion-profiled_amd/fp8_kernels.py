@@ -1,0 +1,520 @@
+"""FP8 conv/GEMM operators on the gfx950 HIP library — drop-in for the reference's
+``diffusion/fp8_kernels.py`` (fattorib/diffusion-profiled).
+
+Same public names, argument meanings, return values and error behaviour as the reference
+(AssertionError for the launch-time checks, KeyError for shapes missing from the registry,
+NotImplementedError for a non-channels-last weight gradient). The Triton kernels are replaced
+by C-ABI calls into ``lib/libdpa_fp8.so``; every output and workspace is a fresh tensor from
+torch's caching allocator and every launch goes on torch's current stream, so the ops are
+safe inside ``torch.cuda.graph`` capture. There is no CPU or PyTorch fallback.
+
+Beyond the reference (no reference kernel exists for these; same FP8 recipe):
+``quantize_fp8_tensor`` (any rank), ``conv2d_fp8_*_general`` (stride 2 and 1x1),
+``linear_fp8`` / ``LinearFP8Function`` and ``DW_SPLIT_K`` defaults tuned for 256 CUs.
+"""
+from __future__ import annotations
+
+from typing import Any, cast
+
+import torch
+from torch.amp.autocast_mode import custom_bwd, custom_fwd
+
+from . import _lib
+
+# diffusion/fp8_kernels.py:11-12
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX_E4M3 = torch.finfo(torch.float8_e4m3fn).max
+
+# (input channels, output channels, input height, input width); diffusion/fp8_kernels.py:17-27
+SUPPORTED_UNET_SHAPES = (
+    (128, 128, 32, 32),
+    (128, 256, 32, 32),
+    (256, 256, 16, 16),
+    (512, 256, 16, 16),
+    (256, 256, 8, 8),
+    (512, 256, 8, 8),
+    (512, 128, 32, 32),
+    (256, 256, 32, 32),
+    (256, 256, 4, 4),
+)
+
+# Split-K for the weight gradient per registry shape. The reference's table
+# (diffusion/fp8_kernels.py:129-139) was tuned for 46 SMs; None lets the library choose one
+# round of workgroups over the MI355X's 256 CUs. The KeyError for unknown shapes is kept.
+DW_CONFIG_BY_SHAPE: dict[tuple[int, int, int, int], int | None] = {
+    shape: None for shape in SUPPORTED_UNET_SHAPES
+}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# --------------------------------------------------------------------------------------
+# checks (diffusion/fp8_kernels.py:471-515, :667-668)
+# --------------------------------------------------------------------------------------
+def torch_checks_conv(a: torch.Tensor, b: torch.Tensor, dtype: torch.dtype) -> None:
+    assert a.ndim == b.ndim == 4
+    assert a.is_cuda and b.is_cuda and a.device == b.device
+    assert a.is_contiguous() or a.is_contiguous(memory_format=torch.channels_last)
+    assert b.is_contiguous() or b.is_contiguous(memory_format=torch.channels_last)
+
+
+def fwd_shapes(x: torch.Tensor, weight: torch.Tensor, dtype: torch.dtype) -> tuple[int, int, int, int, int]:
+    torch_checks_conv(x, weight, dtype)
+    batch, cin, height, width = x.shape
+    cout, weight_cin, kh, kw = weight.shape
+    assert (weight_cin, kh, kw) == (cin, 3, 3)
+    assert (cin, cout, height, width) in SUPPORTED_UNET_SHAPES, f"{(cin, cout, height, width)=}"
+    return batch, cin, cout, height, width
+
+
+def xgrad_shapes(dy: torch.Tensor, weight: torch.Tensor, dtype: torch.dtype) -> tuple[int, int, int, int, int]:
+    torch_checks_conv(dy, weight, dtype)
+    batch, cout, height, width = dy.shape
+    weight_cout, cin, kh, kw = weight.shape
+    assert (weight_cout, kh, kw) == (cout, 3, 3)
+    assert (cin, cout, height, width) in SUPPORTED_UNET_SHAPES
+    return batch, cin, cout, height, width
+
+
+def wgrad_shapes(x: torch.Tensor, dy: torch.Tensor, dtype: torch.dtype) -> tuple[int, int, int, int, int]:
+    torch_checks_conv(x, dy, dtype)
+    batch, cin, height, width = x.shape
+    dy_batch, cout, dy_height, dy_width = dy.shape
+    assert (dy_batch, dy_height, dy_width) == (batch, height, width)
+    assert (cin, cout, height, width) in SUPPORTED_UNET_SHAPES
+    return batch, cin, cout, height, width
+
+
+def torch_checks_scale(scale: torch.Tensor, device: torch.device) -> None:
+    assert scale.device == device and scale.dtype == torch.float32 and scale.numel() == 1
+
+
+def _nhwc(t: torch.Tensor) -> torch.Tensor:
+    """Channels-last dense view of a 4-D tensor (copies only if the layout differs).
+
+    The reference kernels index C with unit stride without checking it, so a contiguous
+    (NCHW) FP8 operand silently produced garbage there; here it is converted instead."""
+    if t.is_contiguous(memory_format=torch.channels_last):
+        return t
+    return t.contiguous(memory_format=torch.channels_last)
+
+
+# --------------------------------------------------------------------------------------
+# quantization (diffusion/fp8_kernels.py:518-601)
+# --------------------------------------------------------------------------------------
+def _dense(t: torch.Tensor) -> bool:
+    return t.is_contiguous() or (t.ndim == 4 and t.is_contiguous(memory_format=torch.channels_last))
+
+
+def _quantize_impl(tensor: torch.Tensor, prev_scale: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
+    if not _dense(tensor):
+        tensor = tensor.contiguous()
+    n = tensor.numel()
+    quantized = torch.empty_like(tensor, dtype=FP8_DTYPE, memory_format=torch.preserve_format)
+    scale = torch.empty((), device=tensor.device, dtype=torch.float32)
+    ws_bytes = _lib.query("dpa_quant_workspace_bytes", n)
+    workspace = torch.empty(ws_bytes, device=tensor.device, dtype=torch.uint8)
+    if prev_scale is None:
+        _lib.call(
+            "dpa_quantize_fp8_bf16",
+            tensor.data_ptr(), n, quantized.data_ptr(), scale.data_ptr(),
+            workspace.data_ptr(), ws_bytes, _stream(tensor),
+        )
+    else:
+        torch_checks_scale(prev_scale, tensor.device)
+        _lib.call(
+            "dpa_quantize_fp8_delayed_bf16",
+            tensor.data_ptr(), n, prev_scale.data_ptr(), quantized.data_ptr(), scale.data_ptr(),
+            workspace.data_ptr(), ws_bytes, _stream(tensor),
+        )
+    return quantized, scale
+
+
+def quantize_fp8_delayed(tensor: torch.Tensor, prev_scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Tensorwise quantization from bfloat16 to fp8 with delay: cast with ``prev_scale`` and
+    return the scale of the current amax (diffusion/fp8_kernels.py:518-556)."""
+    assert tensor.dtype == torch.bfloat16 and tensor.is_cuda and tensor.ndim == 4, (
+        f"{tensor.dtype} {tensor.is_cuda} {tensor.ndim}"
+    )
+    return _quantize_impl(tensor, prev_scale)
+
+
+def quantize_fp8(tensor: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Current-scaling quantization (diffusion/fp8_kernels.py:559-601)."""
+    assert tensor.dtype == torch.bfloat16 and tensor.is_cuda and tensor.ndim == 4, (
+        f"{tensor.dtype} {tensor.is_cuda} {tensor.ndim}"
+    )
+    return _quantize_impl(tensor, None)
+
+
+def quantize_fp8_tensor(tensor: torch.Tensor, prev_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``quantize_fp8`` / ``quantize_fp8_delayed`` for a bf16 tensor of any rank."""
+    assert tensor.dtype == torch.bfloat16 and tensor.is_cuda, f"{tensor.dtype} {tensor.is_cuda}"
+    return _quantize_impl(tensor, prev_scale)
+
+
+# --------------------------------------------------------------------------------------
+# convolution (diffusion/fp8_kernels.py:604-819), general form first
+# --------------------------------------------------------------------------------------
+def _out_hw(h: int, w: int, k: int, stride: int, pad: int) -> tuple[int, int]:
+    return (h + 2 * pad - k) // stride + 1, (w + 2 * pad - k) // stride + 1
+
+
+def conv2d_fp8_fwd_general(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    x_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    stride: int = 1,
+    padding: int = 1,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """FP8 conv forward for 3x3 (pad 1, stride 1|2) and 1x1 (pad 0, stride 1); NCHW-logical,
+    channels-last bf16 output. ``bias`` (fp32 [Cout]) is added after dequantization."""
+    assert x.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE
+    torch_checks_scale(x_scale, x.device)
+    torch_checks_scale(weight_scale, x.device)
+    x = _nhwc(x)
+    weight = _nhwc(weight)
+    batch, cin, height, width = x.shape
+    cout, wcin, kh, kw = weight.shape
+    assert wcin == cin and kh == kw
+    oh, ow = _out_hw(height, width, kh, stride, padding)
+    y = torch.empty((batch, cout, oh, ow), device=x.device, dtype=torch.bfloat16,
+                    memory_format=torch.channels_last)
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == cout and bias.is_contiguous()
+    _lib.call(
+        "dpa_conv2d_fwd_fp8",
+        x.data_ptr(), weight.data_ptr(), x_scale.data_ptr(), weight_scale.data_ptr(),
+        _ptr(bias), y.data_ptr(), batch, height, width, cin, cout, kh, kw, stride, padding,
+        _stream(x),
+    )
+    return y
+
+
+def conv2d_fp8_dgrad_general(
+    dy: torch.Tensor,
+    weight: torch.Tensor,
+    dy_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+    input_hw: tuple[int, int],
+    stride: int = 1,
+    padding: int = 1,
+    weight_t: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """FP8 data gradient; ``input_hw`` is the forward input's (H, W). ``weight_t`` may carry
+    the weight already transposed to [Cin][R][S][Cout] bytes."""
+    assert dy.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE
+    torch_checks_scale(dy_scale, dy.device)
+    torch_checks_scale(weight_scale, dy.device)
+    dy = _nhwc(dy)
+    weight = _nhwc(weight)
+    batch, cout, _, _ = dy.shape
+    wcout, cin, kh, kw = weight.shape
+    assert wcout == cout and kh == kw
+    height, width = input_hw
+    dx = torch.empty((batch, cin, height, width), device=dy.device, dtype=torch.bfloat16,
+                     memory_format=torch.channels_last)
+    if weight_t is None:
+        ws_bytes = _lib.query("dpa_conv2d_dgrad_workspace_bytes", cin, cout, kh, kw)
+        workspace = torch.empty(ws_bytes, device=dy.device, dtype=torch.uint8)
+        _lib.call(
+            "dpa_conv2d_dgrad_fp8",
+            dy.data_ptr(), weight.data_ptr(), dy_scale.data_ptr(), weight_scale.data_ptr(),
+            dx.data_ptr(), workspace.data_ptr(), ws_bytes, batch, height, width, cin, cout,
+            kh, kw, stride, padding, _stream(dy),
+        )
+    else:
+        assert weight_t.numel() == weight.numel() and weight_t.is_contiguous()
+        _lib.call(
+            "dpa_conv2d_dgrad_fp8_wt",
+            dy.data_ptr(), weight_t.data_ptr(), dy_scale.data_ptr(), weight_scale.data_ptr(),
+            dx.data_ptr(), batch, height, width, cin, cout, kh, kw, stride, padding, _stream(dy),
+        )
+    return dx
+
+
+def weight_transpose_fp8(weight: torch.Tensor) -> torch.Tensor:
+    """[Cout][R][S][Cin] e4m3 bytes -> [Cin][R][S][Cout] (the data-gradient operand)."""
+    assert weight.dtype == FP8_DTYPE
+    weight = _nhwc(weight)
+    cout, cin, kh, kw = weight.shape
+    out = torch.empty((cin, kh, kw, cout), device=weight.device, dtype=FP8_DTYPE)
+    _lib.call("dpa_weight_transpose_fp8", weight.data_ptr(), out.data_ptr(), cout, kh, kw, cin,
+              _stream(weight))
+    return out
+
+
+def conv2d_fp8_wgrad_general(
+    x: torch.Tensor,
+    dy: torch.Tensor,
+    x_scale: torch.Tensor,
+    dy_scale: torch.Tensor,
+    kernel_size: int = 3,
+    stride: int = 1,
+    padding: int = 1,
+    split_k: int | None = None,
+) -> torch.Tensor:
+    """FP8 weight gradient -> bf16 (Cout, Cin, k, k) in channels-last memory."""
+    assert x.dtype == FP8_DTYPE and dy.dtype == FP8_DTYPE
+    torch_checks_scale(x_scale, x.device)
+    torch_checks_scale(dy_scale, x.device)
+    x = _nhwc(x)
+    dy = _nhwc(dy)
+    batch, cin, height, width = x.shape
+    _, cout, _, _ = dy.shape
+    sk = 0 if split_k is None else int(split_k)
+    ws_bytes = _lib.query("dpa_conv2d_wgrad_workspace_bytes", batch, height, width, cin, cout,
+                          kernel_size, kernel_size, stride, padding, sk)
+    if ws_bytes <= 0:
+        raise RuntimeError(f"dpa_conv2d_wgrad_fp8: unsupported shape {(batch, cin, cout, height, width, kernel_size, stride)}")
+    workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    dw = torch.empty((cout, cin, kernel_size, kernel_size), device=x.device, dtype=torch.bfloat16,
+                     memory_format=torch.channels_last)
+    _lib.call(
+        "dpa_conv2d_wgrad_fp8",
+        x.data_ptr(), dy.data_ptr(), x_scale.data_ptr(), dy_scale.data_ptr(), dw.data_ptr(),
+        workspace.data_ptr(), ws_bytes, batch, height, width, cin, cout, kernel_size,
+        kernel_size, stride, padding, sk, _stream(x),
+    )
+    return dw
+
+
+# ---- reference-named entry points (3x3, stride 1, pad 1, registry shapes) ----
+def conv2d_fwd_fp8_prequantized(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    x_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:604-639."""
+    fwd_shapes(x, weight, FP8_DTYPE)
+    return conv2d_fp8_fwd_general(x, weight, x_scale, weight_scale, stride=1, padding=1)
+
+
+def conv2d_fwd_fp8(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:642-650."""
+    x_fp8, x_scale = quantize_fp8(x)
+    weight_fp8, weight_scale = quantize_fp8(weight)
+    return conv2d_fwd_fp8_prequantized(x_fp8, weight_fp8, x_scale, weight_scale)
+
+
+def conv2d_fwd_fp8_delayed(x: torch.Tensor, weight: torch.Tensor, x_scale: torch.Tensor, w_scale: torch.Tensor):
+    """diffusion/fp8_kernels.py:653-664."""
+    x_fp8, _ = quantize_fp8_delayed(x, x_scale)
+    weight_fp8, _ = quantize_fp8_delayed(weight, w_scale)
+    return conv2d_fwd_fp8_prequantized(x_fp8, weight_fp8, x_scale, w_scale)
+
+
+def conv2d_bwd_input_fp8_prequantized(
+    dy: torch.Tensor,
+    weight: torch.Tensor,
+    dy_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:671-709."""
+    batch, cin, cout, height, width = xgrad_shapes(dy, weight, FP8_DTYPE)
+    torch_checks_scale(dy_scale, dy.device)
+    torch_checks_scale(weight_scale, dy.device)
+    return conv2d_fp8_dgrad_general(dy, weight, dy_scale, weight_scale, (height, width), 1, 1)
+
+
+def conv2d_bwd_input_fp8(dy: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:712-720."""
+    dy_fp8, dy_scale = quantize_fp8(dy)
+    weight_fp8, weight_scale = quantize_fp8(weight)
+    return conv2d_bwd_input_fp8_prequantized(dy_fp8, weight_fp8, dy_scale, weight_scale)
+
+
+def conv2d_bwd_weight_fp8_prequantized(
+    x: torch.Tensor,
+    dy: torch.Tensor,
+    x_scale: torch.Tensor,
+    dy_scale: torch.Tensor,
+    split_k: int | None = None,
+) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:723-808. Returns bf16 (Cout, Cin, 3, 3), channels-last."""
+    batch, cin, cout, height, width = wgrad_shapes(x, dy, FP8_DTYPE)
+    torch_checks_scale(x_scale, x.device)
+    torch_checks_scale(dy_scale, x.device)
+    if split_k is None:
+        split_k = DW_CONFIG_BY_SHAPE[(cin, cout, height, width)]
+    if not (x.is_contiguous(memory_format=torch.channels_last)
+            and dy.is_contiguous(memory_format=torch.channels_last)):
+        raise NotImplementedError
+    return conv2d_fp8_wgrad_general(x, dy, x_scale, dy_scale, 3, 1, 1, split_k)
+
+
+def conv2d_bwd_weight_fp8(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    """diffusion/fp8_kernels.py:811-819."""
+    x_fp8, x_scale = quantize_fp8(x)
+    dy_fp8, dy_scale = quantize_fp8(dy)
+    return conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale)
+
+
+# --------------------------------------------------------------------------------------
+# autograd boundary (diffusion/fp8_kernels.py:822-923)
+# --------------------------------------------------------------------------------------
+class Conv2dFP8Specialized(torch.autograd.Function):
+    """FP8 3x3/stride-1/pad-1 conv with e4m3 saved activations; current or delayed scaling.
+
+    Same inputs, saved tensors, outputs and in-place window update as the reference
+    (diffusion/fp8_kernels.py:823-913)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(
+        ctx: Any,
+        x: torch.Tensor,
+        weight: torch.Tensor,
+        hist_scales: tuple[torch.Tensor, torch.Tensor] | None = None,
+        dy_ptrs: tuple[torch.Tensor, torch.Tensor] | None = None,
+        do_delayed: bool = False,
+    ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        x = x.to(torch.bfloat16)
+        weight = weight.to(torch.bfloat16)
+
+        assert x.is_contiguous(memory_format=torch.channels_last)
+
+        ctx.do_delayed = do_delayed
+        if do_delayed:
+            assert hist_scales is not None
+            assert dy_ptrs is not None
+            x_scale, weight_scale = hist_scales
+            x_fp8, x_scale_curr = quantize_fp8_delayed(x, x_scale)
+            weight_fp8, weight_scale_curr = quantize_fp8_delayed(weight, weight_scale)
+
+            dy_amax_window, window_pos = dy_ptrs
+            dy_scale_hist = torch.max(dy_amax_window)
+
+            ctx.dy_window = dy_amax_window
+            ctx.window_pos = window_pos
+            ctx.save_for_backward(x_fp8, weight_fp8, x_scale, weight_scale, dy_scale_hist)
+        else:
+            x_fp8, x_scale = quantize_fp8(x)
+            weight_fp8, weight_scale = quantize_fp8(weight)
+            ctx.save_for_backward(x_fp8, weight_fp8, x_scale, weight_scale)
+
+        out = conv2d_fwd_fp8_prequantized(x_fp8, weight_fp8, x_scale, weight_scale)
+
+        if do_delayed:
+            ctx.mark_non_differentiable(x_scale_curr, weight_scale_curr)
+            return out, x_scale_curr, weight_scale_curr
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, *grad_outputs: Any) -> Any:
+        dy = cast(torch.Tensor, grad_outputs[0])
+        dy = dy.contiguous(memory_format=torch.channels_last)
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+
+        if ctx.do_delayed:
+            x_fp8, weight_fp8, x_scale, weight_scale, dy_scale = ctx.saved_tensors
+            dy_fp8, dy_scale_curr = quantize_fp8_delayed(dy, dy_scale)
+            window_idx = ctx.window_pos.unsqueeze(0)
+            ctx.dy_window.scatter_(0, window_idx, dy_scale_curr.unsqueeze(0))
+        else:
+            x_fp8, weight_fp8, x_scale, weight_scale = ctx.saved_tensors
+            dy_fp8, dy_scale = quantize_fp8(dy)
+
+        assert dy_fp8.is_contiguous(memory_format=torch.channels_last)
+        assert weight_fp8.is_contiguous(memory_format=torch.channels_last)
+        assert x_fp8.is_contiguous(memory_format=torch.channels_last)
+
+        dx = conv2d_bwd_input_fp8_prequantized(dy_fp8, weight_fp8, dy_scale, weight_scale)
+        dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale)
+        return dx, dw, None, None, None
+
+
+def triton_conv2d_fp8(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    hist_scales: tuple[torch.Tensor, torch.Tensor] | None = None,
+    dy_ptrs: tuple[torch.Tensor, torch.Tensor] | None = None,
+    do_delayed: bool = False,
+) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Reference-named entry point (diffusion/fp8_kernels.py:916-923); runs the HIP kernels."""
+    return Conv2dFP8Specialized.apply(x, weight, hist_scales, dy_ptrs, do_delayed)
+
+
+hip_conv2d_fp8 = triton_conv2d_fp8
+
+
+# --------------------------------------------------------------------------------------
+# generalised conv (stride 2, 1x1) and the FP8 linear: same recipe, no reference kernel
+# --------------------------------------------------------------------------------------
+class Conv2dFP8General(torch.autograd.Function):
+    """Current-scaling FP8 conv for any supported (k, stride, pad); saves e4m3 x and w."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, stride: int, padding: int) -> torch.Tensor:
+        x = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        weight = weight.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        x_fp8, x_scale = quantize_fp8(x)
+        w_fp8, w_scale = quantize_fp8(weight)
+        ctx.save_for_backward(x_fp8, w_fp8, x_scale, w_scale)
+        ctx.stride, ctx.padding = stride, padding
+        ctx.input_hw = (x.shape[2], x.shape[3])
+        return conv2d_fp8_fwd_general(x_fp8, w_fp8, x_scale, w_scale, stride, padding)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor) -> Any:
+        x_fp8, w_fp8, x_scale, w_scale = ctx.saved_tensors
+        dy = dy.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        dy_fp8, dy_scale = quantize_fp8(dy)
+        k = w_fp8.shape[2]
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = conv2d_fp8_dgrad_general(dy_fp8, w_fp8, dy_scale, w_scale, ctx.input_hw,
+                                          ctx.stride, ctx.padding)
+        dw = conv2d_fp8_wgrad_general(x_fp8, dy_fp8, x_scale, dy_scale, k, ctx.stride, ctx.padding)
+        return dx, dw, None, None
+
+
+def conv2d_fp8(x: torch.Tensor, weight: torch.Tensor, stride: int = 1, padding: int = 1) -> torch.Tensor:
+    return Conv2dFP8General.apply(x, weight, stride, padding)
+
+
+def linear_fp8_prequantized(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    a_scale: torch.Tensor,
+    b_scale: torch.Tensor,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """c[M, N] = bf16(a[M, K] @ b[N, K]^T * a_scale * b_scale [+ bias]); e4m3 inputs."""
+    assert a.dtype == FP8_DTYPE and b.dtype == FP8_DTYPE and a.is_cuda and b.is_cuda
+    assert a.ndim == 2 and b.ndim == 2 and a.shape[1] == b.shape[1]
+    torch_checks_scale(a_scale, a.device)
+    torch_checks_scale(b_scale, a.device)
+    a = a.contiguous()
+    b = b.contiguous()
+    m, k = a.shape
+    n = b.shape[0]
+    c = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.numel() == n and bias.is_contiguous()
+    _lib.call("dpa_gemm_fp8", a.data_ptr(), b.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(),
+              _ptr(bias), c.data_ptr(), m, n, k, _stream(a))
+    return c
+
+
+def linear_fp8(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Forward-only FP8 linear with current scaling: bf16 x[..., K] and weight[N, K]."""
+    lead = x.shape[:-1]
+    x2 = x.to(torch.bfloat16).reshape(-1, x.shape[-1])
+    xq, xs = quantize_fp8_tensor(x2)
+    wq, wsc = quantize_fp8_tensor(weight.to(torch.bfloat16))
+    y = linear_fp8_prequantized(xq, wq, xs, wsc, bias)
+    return y.reshape(*lead, weight.shape[0])

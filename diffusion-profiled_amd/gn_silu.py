@@ -1,0 +1,109 @@
+"""Fused GroupNorm(+FiLM)+SiLU on the HIP library, as an autograd Function.
+
+Replaces the two Inductor-fused chains of the reference ResidualBlock
+(diffusion/unet.py:151 ``F.silu(self.norm1(x))`` and :157-159
+``F.silu((w + 1) * self.norm2(x) + b)``). The output is bf16, which is exactly what the FP8
+conv consumes after its ``x.to(torch.bfloat16)`` (diffusion/fp8_kernels.py:835).
+"""
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _lib
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def supported(c: int, groups: int) -> bool:
+    """Shapes the fused kernel implements (all GroupNorms of the reference U-Net)."""
+    if c % groups != 0 or c % 64 != 0:
+        return False
+    cpg = c // groups
+    return cpg >= 4 and 64 % cpg == 0
+
+
+def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
+    """Returns (out bf16 channels-last, mean [N*G], rstd [N*G])."""
+    n, c, h, w = x.shape
+    x = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    out = torch.empty_like(x, memory_format=torch.channels_last)
+    mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
+    rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
+    gamma = gamma.float().contiguous()
+    beta = beta.float().contiguous()
+    fs = fb = None
+    if film_scale is not None:
+        fs = film_scale.float().reshape(n, c).contiguous()
+        fb = film_shift.float().reshape(n, c).contiguous()
+    _lib.call(
+        "dpa_gn_silu_fwd_bf16",
+        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+        None if fs is None else fs.data_ptr(), None if fb is None else fb.data_ptr(),
+        out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), n, h * w, c, groups, float(eps),
+        _stream(x),
+    )
+    return out, mean, rstd
+
+
+def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None):
+    """Returns (dx bf16, dgamma, dbeta, dfilm_scale [N,C] | None, dfilm_shift | None)."""
+    n, c, h, w = x.shape
+    x = x.contiguous(memory_format=torch.channels_last)
+    dout = dout.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    dx = torch.empty_like(x, memory_format=torch.channels_last)
+    dgamma = torch.empty(c, device=x.device, dtype=torch.float32)
+    dbeta = torch.empty(c, device=x.device, dtype=torch.float32)
+    fs = fb = dfs = dfb = None
+    if film_scale is not None:
+        fs = film_scale.float().reshape(n, c).contiguous()
+        fb = film_shift.float().reshape(n, c).contiguous()
+        dfs = torch.empty((n, c), device=x.device, dtype=torch.float32)
+        dfb = torch.empty((n, c), device=x.device, dtype=torch.float32)
+    ws_bytes = _lib.query("dpa_gn_silu_bwd_workspace_bytes", n, h * w, c, groups)
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    _lib.call(
+        "dpa_gn_silu_bwd_bf16",
+        x.data_ptr(), dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+        beta.float().contiguous().data_ptr(), p(fs), p(fb), mean.data_ptr(), rstd.data_ptr(),
+        dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs), p(dfb), ws.data_ptr(),
+        ws_bytes, n, h * w, c, groups, _stream(x),
+    )
+    return dx, dgamma, dbeta, dfs, dfb
+
+
+class GroupNormSiLU(torch.autograd.Function):
+    """silu(GroupNorm(x)) or silu(film_scale * GroupNorm(x) + film_shift), bf16 out.
+
+    x: bf16 [N, C, H, W] (any memory format; used channels-last). gamma/beta: fp32 [C].
+    film_scale/film_shift: [N, C, 1, 1] or None (the reference's ``w + 1`` and ``b``)."""
+
+    @staticmethod
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_scale=None, film_shift=None):
+        xb = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps, film_scale, film_shift)
+        ctx.groups = groups
+        ctx.has_film = film_scale is not None
+        ctx.x_dtype = x.dtype
+        ctx.film_dtypes = (film_scale.dtype, film_shift.dtype) if ctx.has_film else None
+        ctx.save_for_backward(xb, gamma, beta, mean, rstd, film_scale, film_shift)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout):
+        xb, gamma, beta, mean, rstd, fs, fb = ctx.saved_tensors
+        dx, dgamma, dbeta, dfs, dfb = gn_silu_bwd(xb, dout, gamma, beta, mean, rstd, ctx.groups, fs, fb)
+        n, c = xb.shape[0], xb.shape[1]
+        gfs = gfb = None
+        if ctx.has_film:
+            gfs = dfs.reshape(fs.shape).to(ctx.film_dtypes[0])
+            gfb = dfb.reshape(fb.shape).to(ctx.film_dtypes[1])
+        return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, gfs, gfb
+
+
+def group_norm_silu(x, gamma, beta, groups: int, eps: float = 1e-5, film_scale=None, film_shift=None):
+    return GroupNormSiLU.apply(x, gamma, beta, groups, eps, film_scale, film_shift)

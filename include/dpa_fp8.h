@@ -1,0 +1,166 @@
+/*
+ * dpa_fp8.h — C ABI of the MI355X (gfx950) FP8 conv/GEMM path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, explicit sizes and a hipStream_t passed as void*;
+ *   - launches asynchronously on that stream and never synchronises the host;
+ *   - allocates nothing: outputs and workspaces are owned by the caller;
+ *   - returns DPA_OK (0), a negative DPA_E* code when a precondition fails (nothing is
+ *     launched), or a positive hipError_t when a launch fails.
+ *
+ * Tensor conventions (all dense, no padding between rows):
+ *   activations  NHWC    ([N][H][W][C], C contiguous)  — the reference's channels_last
+ *   conv weights OHWI    ([Cout][R][S][Cin])          — channels_last of (Cout, Cin, R, S)
+ *   e4m3         OCP float8_e4m3fn bytes (bias 7, max 448, 0x7f/0xff = NaN)
+ *   bf16         IEEE bfloat16 bits, round-to-nearest-even
+ *   scales       one fp32 value in device memory ("0-dim tensor")
+ *
+ * Reference interfaces replaced (fattorib/diffusion-profiled, diffusion/fp8_kernels.py):
+ *   dpa_quantize_fp8_bf16          <- quantize_fp8                        :559-601 (K1+K2+K3)
+ *   dpa_quantize_fp8_delayed_bf16  <- quantize_fp8_delayed                :518-556 (K4+K2)
+ *   dpa_conv2d_fwd_fp8             <- conv2d_fwd_fp8_prequantized         :604-639 (K5)
+ *   dpa_conv2d_dgrad_fp8           <- conv2d_bwd_input_fp8_prequantized   :671-709 (K6)
+ *   dpa_conv2d_wgrad_fp8           <- conv2d_bwd_weight_fp8_prequantized  :723-808 (K7+K8+K9)
+ *   dpa_gemm_fp8                   <- no reference kernel; the FP8 recipe applied to the
+ *                                     nn.Linear sites of diffusion/unet.py:171-172
+ *   dpa_gn_silu_fwd_bf16 / _bwd    <- nn.GroupNorm + F.silu (+ FiLM) of diffusion/unet.py:151,
+ *                                     :157-159 (Inductor-fused in the reference)
+ */
+#ifndef DPA_FP8_H
+#define DPA_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DPA_OK 0
+#define DPA_ERR_NULL (-1)        /* a required pointer is NULL */
+#define DPA_ERR_SIZE (-2)        /* a size is negative, zero where not allowed, or too large */
+#define DPA_ERR_ALIGN (-3)       /* a pointer lacks the alignment the kernel needs */
+#define DPA_ERR_SHAPE (-4)       /* shape combination the kernels do not implement */
+#define DPA_ERR_WORKSPACE (-5)   /* workspace missing or smaller than *_workspace_bytes() */
+
+/* Human-readable text for a status code (static storage). */
+const char* dpa_status_string(int status);
+
+/* ABI version of this library; bumped when a signature changes. */
+int dpa_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Per-tensor absmax scaling and e4m3 cast.
+ *   scale = amax > 0 ? RN32(amax / 448) : 1            (fp8_kernels.py:90-102)
+ *   q[i]  = e4m3_RNE( max(-448, min(RN32(f32(x[i]) / scale), 448)) )   (:105-120)
+ * Bit-exact: q and scale are identical to the CPU restatement for every bf16 input.
+ * x and q have the same (dense) memory order; they are treated as flat arrays of n items.
+ * ---------------------------------------------------------------------------------------- */
+
+/* Bytes of workspace the two quantize entry points need for n elements. */
+int64_t dpa_quant_workspace_bytes(int64_t n);
+
+/* Current scaling: scale_out <- scale(amax(x)); q <- cast(x, scale_out).
+ * Replaces quantize_fp8 (diffusion/fp8_kernels.py:559-601). Two launches. */
+int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* scale_out,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Delayed scaling: q <- cast(x, *prev_scale); cur_scale_out <- scale(amax(x)).
+ * One read of x. Replaces quantize_fp8_delayed (diffusion/fp8_kernels.py:518-556). */
+int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const float* prev_scale, void* q,
+                                  float* cur_scale_out, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * FP8 implicit-GEMM convolution, NHWC activations, OHWI weights, fp32 accumulation,
+ * fused dequant epilogue:  out = bf16_RNE( RN32(acc * RN32(sa * sb)) [+ bias[c]] ).
+ * Supported: R = S = 3 with pad 1 and stride 1 or 2;  R = S = 1 with pad 0, stride 1.
+ * Cin and Cout must be multiples of 128 (the MFMA K depth and output tile).
+ * Output size P = (H + 2*pad - R) / stride + 1, Q likewise.
+ * ---------------------------------------------------------------------------------------- */
+
+/* y[N,P,Q,Cout] = conv(xq[N,H,W,Cin], wq[Cout,R,S,Cin]).
+ * Replaces conv2d_fwd_fp8_prequantized (diffusion/fp8_kernels.py:604-639) and its kernel
+ * conv2d_fwd_fp8_kernel (:142-247). bias may be NULL (the reference has none). */
+int dpa_conv2d_fwd_fp8(const void* xq, const void* wq, const float* x_scale,
+                       const float* w_scale, const float* bias, void* y, int N, int H, int W,
+                       int Cin, int Cout, int R, int S, int stride, int pad, void* stream);
+
+/* Bytes of workspace dpa_conv2d_dgrad_fp8 needs (the transposed weight, Cout*R*S*Cin). */
+int64_t dpa_conv2d_dgrad_workspace_bytes(int Cin, int Cout, int R, int S);
+
+/* dx[N,H,W,Cin] = conv_transpose(dyq[N,P,Q,Cout], wq[Cout,R,S,Cin]); H, W are the INPUT
+ * spatial sizes of the forward conv. Replaces conv2d_bwd_input_fp8_prequantized
+ * (diffusion/fp8_kernels.py:671-709) and conv2d_dx_fp8_kernel (:250-318).
+ * The workspace receives wq transposed to [Cin][R][S][Cout]. */
+int dpa_conv2d_dgrad_fp8(const void* dyq, const void* wq, const float* dy_scale,
+                         const float* w_scale, void* dx, void* workspace,
+                         int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout,
+                         int R, int S, int stride, int pad, void* stream);
+
+/* Same as dpa_conv2d_dgrad_fp8 but takes the weight already transposed to [Cin][R][S][Cout]
+ * (as written by dpa_weight_transpose_fp8), so a caller can reuse it across calls. */
+int dpa_conv2d_dgrad_fp8_wt(const void* dyq, const void* wq_t, const float* dy_scale,
+                            const float* w_scale, void* dx, int N, int H, int W, int Cin,
+                            int Cout, int R, int S, int stride, int pad, void* stream);
+
+/* wq_t[Cin][R][S][Cout] = wq[Cout][R][S][Cin] (e4m3 bytes). */
+int dpa_weight_transpose_fp8(const void* wq, void* wq_t, int Cout, int R, int S, int Cin,
+                             void* stream);
+
+/* Bytes of workspace dpa_conv2d_wgrad_fp8 needs for the given split count
+ * (split_k <= 0 selects the library's default for the shape). */
+int64_t dpa_conv2d_wgrad_workspace_bytes(int N, int H, int W, int Cin, int Cout, int R,
+                                         int S, int stride, int pad, int split_k);
+
+/* dw[Cout,R,S,Cin] = bf16( RN32(sum_splits partial) * RN32(sx * sdy) ),
+ * partial[s][co][(r,s,ci)] = sum over output pixels of split s of
+ *                            dyq[pix,co] * xq[shifted pix, ci].
+ * Splits are summed in index order (deterministic). Replaces
+ * conv2d_bwd_weight_fp8_prequantized (diffusion/fp8_kernels.py:723-808), i.e. K7+K8+K9. */
+int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float* x_scale,
+                         const float* dy_scale, void* dw, void* workspace,
+                         int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout,
+                         int R, int S, int stride, int pad, int split_k, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * FP8 GEMM (the FP8 linear): c[M,N] = bf16( RN32(a[M,K] . b[N,K]^T * RN32(sa*sb)) [+ bias] )
+ * a and b are row-major with K contiguous (b is nn.Linear's weight layout).
+ * K and N must be multiples of 128. No reference kernel exists (see header comment).
+ * ---------------------------------------------------------------------------------------- */
+int dpa_gemm_fp8(const void* a, const void* b, const float* a_scale, const float* b_scale,
+                 const float* bias, void* c, int M, int N, int K, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Fused GroupNorm + optional FiLM + SiLU on NHWC bf16, fp32 statistics (biased variance).
+ *   z   = gamma[c] * (x - mean[n,g]) * rstd[n,g] + beta[c]
+ *   z'  = film_scale ? film_scale[n,c] * z + film_shift[n,c] : z
+ *   out = bf16_RNE( z' * sigmoid(z') )
+ * Mirrors F.silu(nn.GroupNorm(G, C)(x)) (diffusion/unet.py:151) and
+ * F.silu((w + 1) * nn.GroupNorm(G, C)(x) + b) (diffusion/unet.py:157-159), with
+ * film_scale = (w + 1) and film_shift = b given as fp32 [N, C].
+ * mean/rstd [N*G] fp32 are written for the backward pass.
+ * Requires C % 64 == 0 and 64 % (C / G) == 0 (every GroupNorm of the reference U-Net).
+ * ---------------------------------------------------------------------------------------- */
+int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                         const float* film_scale, const float* film_shift, void* out,
+                         float* mean, float* rstd, int N, int HW, int C, int G, float eps,
+                         void* stream);
+
+/* Bytes of workspace dpa_gn_silu_bwd_bf16 needs (per-image channel partial sums). */
+int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G);
+
+/* Backward of dpa_gn_silu_fwd_bf16 given dout (bf16, same layout as out). Writes dx (bf16)
+ * and overwrites dgamma, dbeta [C] and, when film_scale is given, dfilm_scale and
+ * dfilm_shift [N, C] (all fp32). Per-channel sums over the batch are reduced in image
+ * order (deterministic). */
+int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                         const float* beta, const float* film_scale, const float* film_shift,
+                         const float* mean, const float* rstd, void* dx, float* dgamma,
+                         float* dbeta, float* dfilm_scale, float* dfilm_shift, void* workspace,
+                         int64_t workspace_bytes, int N, int HW, int C, int G, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DPA_FP8_H */
