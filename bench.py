@@ -1,0 +1,322 @@
+"""Benchmark of the MI355X FP8 conv path (one GPU).
+
+A step is one pass of the hot path over one batch: the FP8 3x3 conv of BASELINE config 2
+(NHWC [128,32,32,128] -> 128, stride 1, pad 1) forward + data gradient + weight gradient,
+including the per-tensor e4m3 quantization of x, w and dy — exactly what
+Conv2dFP8Specialized does per layer in the reference (diffusion/fp8_kernels.py:826-913).
+
+    python bench.py [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3s2|cfg3k1]
+
+Prints ONE JSON line. `value` is TFLOP/s of algorithmic conv work (3 x 2*M*N*K per step)
+with inputs resident in HBM. `roofline` is for the dominant kernel, timed with HIP events on
+the stream the kernels are launched on (torch's current stream). `cpu_baseline` times the
+oracle's CPU path (the reference recipe on torch CPU: e4m3 round trip + fp32 conv) on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "FP8 conv/GEMM TFLOP/s (% of MFMA peak); U-Net train steps/s at batch 128"
+PEAK_FP8_TFLOPS = 5000.0  # MI355X dense FP8 MFMA
+PEAK_HBM_GBS = 8000.0
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1"])
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def seeded(shape, seed, std=1.0, kaiming=False):
+    g = torch.Generator().manual_seed(seed)
+    if kaiming:
+        import math
+
+        fan_in = 1
+        for d in shape[1:]:
+            fan_in *= d
+        b = 1.0 / math.sqrt(fan_in)
+        return (torch.rand(shape, generator=g) * 2 * b - b).to(torch.bfloat16)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+class ConvWorkload:
+    """One FP8 conv layer fwd + dgrad + wgrad with current scaling."""
+
+    def __init__(self, K, n, cin, cout, h, w, k, stride, pad, name):
+        self.K = K
+        self.n, self.cin, self.cout, self.h, self.w, self.k = n, cin, cout, h, w, k
+        self.stride, self.pad = stride, pad
+        self.p = (h + 2 * pad - k) // stride + 1
+        self.q = (w + 2 * pad - k) // stride + 1
+        self.name = name
+        cl = torch.channels_last
+        self.x = seeded((n, cin, h, w), 0).cuda().contiguous(memory_format=cl)
+        self.wt = seeded((cout, cin, k, k), 1, kaiming=True).cuda().contiguous(memory_format=cl)
+        self.dy = seeded((n, cout, self.p, self.q), 2, std=1e-2).cuda().contiguous(memory_format=cl)
+        self.flop = 2.0 * n * self.p * self.q * cout * cin * k * k  # per GEMM (fwd/dgrad/wgrad)
+        # algorithmic bytes (e4m3 operands, bf16 outputs)
+        self.bytes = {
+            "fwd": n * h * w * cin + cout * k * k * cin + 2 * n * self.p * self.q * cout,
+            "dgrad": n * self.p * self.q * cout + cout * k * k * cin + 2 * n * h * w * cin,
+            "wgrad": n * h * w * cin + n * self.p * self.q * cout + 2 * cout * k * k * cin,
+        }
+        self.quant_bytes = 3 * (n * h * w * cin + cout * k * k * cin + n * self.p * self.q * cout)
+
+    def quantize(self):
+        K = self.K
+        self.xq, self.xs = K.quantize_fp8(self.x)
+        self.wq, self.ws = K.quantize_fp8(self.wt)
+        self.dyq, self.dys = K.quantize_fp8(self.dy)
+
+    def fwd(self):
+        return self.K.conv2d_fp8_fwd_general(self.xq, self.wq, self.xs, self.ws, self.stride, self.pad)
+
+    def dgrad(self):
+        return self.K.conv2d_fp8_dgrad_general(self.dyq, self.wq, self.dys, self.ws, (self.h, self.w),
+                                               self.stride, self.pad)
+
+    def wgrad(self):
+        return self.K.conv2d_fp8_wgrad_general(self.xq, self.dyq, self.xs, self.dys, self.k,
+                                               self.stride, self.pad)
+
+    def step(self):
+        self.quantize()
+        self.fwd()
+        self.dgrad()
+        self.wgrad()
+
+    def parts(self):
+        return {"quantize": self.quantize, "fwd": self.fwd, "dgrad": self.dgrad, "wgrad": self.wgrad}
+
+    def step_flop(self):
+        return 3 * self.flop
+
+    def config(self):
+        return {
+            "workload": self.name,
+            "batch": self.n, "cin": self.cin, "cout": self.cout, "h": self.h, "w": self.w,
+            "kernel": self.k, "stride": self.stride, "pad": self.pad,
+            "layout": "NHWC activations, OHWI weights, e4m3 per-tensor current scaling",
+            "step": "quantize x,w,dy + conv fwd + dgrad + wgrad",
+        }
+
+
+class GemmWorkload:
+    """cfg1: FP8 linear forward X[32768,256] . W[768,256]^T with current scaling."""
+
+    def __init__(self, K):
+        self.K = K
+        self.m, self.nn, self.kk = 32768, 768, 256
+        self.x = seeded((self.m, self.kk), 0).cuda()
+        self.wt = seeded((self.nn, self.kk), 1, kaiming=True).cuda()
+        self.flop = 2.0 * self.m * self.nn * self.kk
+        self.bytes = {"fwd": self.m * self.kk + self.nn * self.kk + 2 * self.m * self.nn}
+        self.quant_bytes = 3 * (self.m * self.kk + self.nn * self.kk)
+        self.name = "cfg1: FP8 linear fwd X[32768,256] x W[768,256]^T -> bf16, incl. e4m3 quantization"
+
+    def quantize(self):
+        self.xq, self.xs = self.K.quantize_fp8_tensor(self.x)
+        self.wq, self.ws = self.K.quantize_fp8_tensor(self.wt)
+
+    def fwd(self):
+        return self.K.linear_fp8_prequantized(self.xq, self.wq, self.xs, self.ws)
+
+    def step(self):
+        self.quantize()
+        self.fwd()
+
+    def parts(self):
+        return {"quantize": self.quantize, "fwd": self.fwd}
+
+    def step_flop(self):
+        return self.flop
+
+    def config(self):
+        return {"workload": self.name, "m": self.m, "n": self.nn, "k": self.kk}
+
+
+def make_workload(K, name):
+    if name == "cfg1":
+        return GemmWorkload(K)
+    if name == "cfg2":
+        return ConvWorkload(K, 128, 128, 128, 32, 32, 3, 1, 1,
+                            "cfg2: FP8 3x3 conv s1 p1, NHWC [128,32,32,128] -> 128, fwd+dgrad+wgrad incl. e4m3 quantization")
+    if name == "cfg3":
+        return ConvWorkload(K, 128, 256, 256, 16, 16, 3, 1, 1,
+                            "cfg3: FP8 3x3 conv s1 p1, NHWC [128,16,16,256] -> 256, fwd+dgrad+wgrad incl. quantization")
+    if name == "cfg3s2":
+        return ConvWorkload(K, 128, 256, 256, 16, 16, 3, 2, 1,
+                            "cfg3: FP8 3x3 conv stride 2, [128,16,16,256] -> [128,8,8,256], fwd+dgrad+wgrad")
+    if name == "cfg3k1":
+        return ConvWorkload(K, 128, 128, 256, 32, 32, 1, 1, 0,
+                            "cfg3: FP8 1x1 conv 128 -> 256 @ 32x32, fwd+dgrad+wgrad")
+    raise ValueError(name)
+
+
+def time_part(fn, reps):
+    """Average device time of fn() over reps launches, HIP events on torch's current stream
+    (the stream every kernel of this library is launched on)."""
+    s = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record(s)
+    for _ in range(reps):
+        fn()
+    end.record(s)
+    end.synchronize()
+    return start.elapsed_time(end) / reps * 1e3  # microseconds
+
+
+def cpu_baseline(wl, seconds):
+    """The reference recipe on torch CPU (e4m3 round trip, fp32 conv/dgrad/wgrad) on a bounded
+    sample of the workload: the first `b` images, b grown until the run takes ~seconds."""
+    from oracle import fp8_oracle  # noqa: F401  (the CPU restatement of the recipe)
+    import torch.nn.functional as F
+
+    threads = torch.get_num_threads()
+
+    def q(t):
+        t = t.float()
+        amax = t.abs().max()
+        s = amax / 448.0 if amax > 0 else torch.tensor(1.0)
+        return (t / s).clamp(-448, 448).to(torch.float8_e4m3fn).float(), s
+
+    if isinstance(wl, GemmWorkload):
+        rows = 1024
+        x = wl.x[:rows].cpu()
+        w = wl.wt.cpu()
+        done = 0
+        t0 = time.perf_counter()
+        while True:
+            xq, xs = q(x)
+            wq, ws = q(w)
+            _ = ((xq @ wq.T) * (xs * ws)).to(torch.bfloat16)
+            done += 1
+            if time.perf_counter() - t0 > seconds:
+                break
+        dt = (time.perf_counter() - t0) / done
+        flop = 2.0 * rows * wl.nn * wl.kk
+        return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"{rows} of {wl.m} rows, {done} reps, {dt * 1e3:.1f} ms/rep"}
+    b = 1
+    x = wl.x[:b].cpu().float()
+    w = wl.wt.cpu()
+    dy = wl.dy[:b].cpu()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        xq, xs = q(x)
+        wq, ws = q(w)
+        dq, ds = q(dy)
+        y = (F.conv2d(xq, wq, stride=wl.stride, padding=wl.pad) * (xs * ws)).to(torch.bfloat16)
+        dx = (torch.nn.grad.conv2d_input(xq.shape, wq, dq, stride=wl.stride, padding=wl.pad) * (ds * ws)).to(torch.bfloat16)
+        dw = (torch.nn.grad.conv2d_weight(xq, wq.shape, dq, stride=wl.stride, padding=wl.pad) * (xs * ds)).to(torch.bfloat16)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > seconds:
+            break
+    dt = el / reps
+    flop = 3 * wl.flop * b / wl.n
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{b} of {wl.n} images (fwd+dgrad+wgrad incl. e4m3 round trip), {reps} reps, "
+                      f"{dt * 1e3:.0f} ms/rep; torch CPU fp32"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is not "
+                                   "measured (see DESIGN.md for how the path would shard)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    K = importlib.import_module("diffusion-profiled_amd.fp8_kernels")
+    importlib.import_module("diffusion-profiled_amd._lib").load()
+    wl = make_workload(K, args.workload)
+
+    # per-part device times (HIP events on the launch stream)
+    wl.quantize()
+    parts = {}
+    for name, fn in wl.parts().items():
+        parts[name] = time_part(fn, args.kernel_reps)
+
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+
+    tflops = wl.step_flop() / dt / 1e12
+    gemm_parts = {k: v for k, v in parts.items() if k != "quantize"}
+    dominant = max(gemm_parts, key=gemm_parts.get)
+    dom_us = gemm_parts[dominant]
+    achieved = wl.flop / (dom_us * 1e-6) / 1e12
+    traffic = None
+    if os.path.exists(PROFILE_TRAFFIC):
+        try:
+            traffic = json.load(open(PROFILE_TRAFFIC)).get(args.workload, {}).get(dominant)
+        except Exception:
+            traffic = None
+    kernels = {}
+    for k, us in parts.items():
+        if k == "quantize":
+            kernels[k] = {"us": round(us, 2), "GB/s": round(wl.quant_bytes / (us * 1e-6) / 1e9, 1)}
+        else:
+            kernels[k] = {"us": round(us, 2), "TFLOP/s": round(wl.flop / (us * 1e-6) / 1e12, 1),
+                          "frac_fp8_peak": round(wl.flop / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded N(0,1) activations, Kaiming-uniform weights, N(0,1e-2) grad_out)",
+        "config": wl.config(),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dominant,
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": wl.bytes.get(dominant),
+        },
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
