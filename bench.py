@@ -8,8 +8,10 @@ Conv2dFP8Specialized does per layer in the reference (diffusion/fp8_kernels.py:8
     python bench.py [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3s2|cfg3k1]
 
 Prints ONE JSON line. `value` is TFLOP/s of algorithmic conv work (3 x 2*M*N*K per step)
-with inputs resident in HBM. `roofline` is for the dominant kernel, timed with HIP events on
-the stream the kernels are launched on (torch's current stream). `cpu_baseline` times the
+with inputs resident in HBM; the step is captured once as a HIP graph and replayed K times
+(wall clock around the replays, synchronised on both sides). `roofline` is for the dominant
+kernel: HIP events around a graph replay of many calls, recorded on the replay stream (the
+stream every kernel of the library is launched on). `cpu_baseline` times the
 oracle's CPU path (the reference recipe on torch CPU: e4m3 round trip + fp32 conv) on a
 bounded sample of the same workload.
 """
@@ -172,17 +174,34 @@ def make_workload(K, name):
     raise ValueError(name)
 
 
+def capture(fn, reps):
+    """A HIP graph (torch.cuda.CUDAGraph) of reps back-to-back calls of fn on a side stream;
+    replaying it launches the kernels with no host work in between."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm: allocator pools, library load
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
 def time_part(fn, reps):
-    """Average device time of fn() over reps launches, HIP events on torch's current stream
-    (the stream every kernel of this library is launched on)."""
+    """Average device time per call of fn: HIP events around a graph replay of reps calls,
+    recorded on the stream the replay (and so every kernel of this library) runs on."""
+    g = capture(fn, reps)
+    g.replay()
+    torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    fn()
-    torch.cuda.synchronize()
     start.record(s)
-    for _ in range(reps):
-        fn()
+    g.replay()
     end.record(s)
     end.synchronize()
     return start.elapsed_time(end) / reps * 1e3  # microseconds
@@ -260,12 +279,14 @@ def main():
     for name, fn in wl.parts().items():
         parts[name] = time_part(fn, args.kernel_reps)
 
+    # the step as one HIP graph (one replay = one step), timed over K replays
+    g = capture(wl.step, 1)
     for _ in range(args.warmup):
-        wl.step()
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        wl.step()
+        g.replay()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
 

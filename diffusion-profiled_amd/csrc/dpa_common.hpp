@@ -157,9 +157,41 @@ __device__ __forceinline__ void st_nt16(void* p, uint4 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
 }
 
+// Two fp32 -> packed bf16 pair (round to nearest even) with gfx950's v_cvt_pk_bf16_f32.
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const v2bf r = __builtin_convertvector((v2f){a, b}, v2bf);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // Bytes of {hi:lo} selected by sel (v_perm_b32).
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// ---------------------------------------------------------------------------------------
+// Integer division by a launch-time constant without the ~40-instruction runtime divide.
+// ---------------------------------------------------------------------------------------
+// x / d for 0 <= x < 2^31 via a precomputed (magic, shift) pair (Granlund-Montgomery).
+struct FastDiv {
+  uint32_t magic, shift, d;
+};
+__host__ __device__ inline uint32_t fdiv(uint32_t x, const FastDiv& f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return (__umulhi(x, f.magic) + x) >> f.shift;
+#else
+  return (uint32_t)((((uint64_t)x * f.magic) >> 32) + x) >> f.shift;
+#endif
+}
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.shift = s;
+  f.magic = (uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1);
+  return f;
 }
 
 // ---------------------------------------------------------------------------------------

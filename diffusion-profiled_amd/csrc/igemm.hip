@@ -6,26 +6,43 @@
 //
 // One kernel serves every case. The GEMM is
 //   out[pix, co] = sum_{tap, c} act[pix shifted by tap, c] * wgt[co, tap, c]
-// where the tap list (<= 9 entries) says, per tap, the input-pixel offset and which weight
-// tap to use. Forward convs (stride 1 or 2, 3x3 or 1x1) use the natural tap list; the data
-// gradient is the same kernel on dy with the weight transposed to [Cin][R][S][Cout] and
-// mirrored offsets; stride-2 dgrad runs once per output parity class with only the taps
-// that class touches; the linear is the 1x1 case with H = W = 1.
+// over a tap grid (ty, tx) in [0, ny) x [0, nx) whose input offset and weight tap are linear
+// in (ty, tx). Forward convs (stride 1 or 2, 3x3 or 1x1) use the natural grid; the data
+// gradient is the same kernel on dy with the weight transposed to [Cin][R][S][Cout] and a
+// mirrored grid; stride-2 dgrad runs once per output parity class with only the taps that
+// class touches; the linear is the 1x1 case with H = W = 1.
 //
-// Tile: 128 output pixels x 128 output channels per workgroup of 4 waves (2 x 2), each
-// wave 64 x 64 = 4 x 4 MFMA 16x16x128 tiles. K advances 128 channels (one tap) per step.
-// Operands are staged global -> registers -> LDS (double-buffered, one barrier per step);
-// LDS rows are 128 B with the 16-B granules XOR-swizzled by (row & 7).
-// Epilogue: out = bf16(RN32(acc * RN32(sa * sb)) [+ bias]) with 8-byte stores.
+// Schedule: persistent. One workgroup of 8 waves (4 x 2, two per SIMD) per CU walks its
+// output tiles of 256 pixels x 128 channels (a contiguous run per XCD, so neighbouring
+// tiles share halo rows in that XCD's L2) as one continuous stream of K-steps (128 input
+// channels of one tap per step). Operands reach LDS by DMA (global_load_lds, 16 B per lane)
+// through a 3-stage ring, issued three steps ahead, also across tile boundaries. Each wave
+// owns a 64 x 64 output tile (4 x 4 MFMA 16x16x128); step k runs its 16 MFMAs on fragments
+// read during step k-1 while it reads step k+1's fragments, so LDS reads, DMA and MFMA of
+// neighbouring steps overlap. LDS rows are 128 B with 16-B granules XOR-swizzled by
+// ((row ^ (row >> 3)) & 7), conflict-free for the 16-row fragment reads.
+// Epilogue per finished tile, per wave, while the next tile's DMA is in flight:
+//   out = bf16(RN32(acc * RN32(sa * sb)) [+ bias]), staged through the wave's private 2 KB
+// LDS slot so every pixel's 64 channels leave as one 128-B run.
 #include "dpa_common.hpp"
 
 namespace dpa {
 
-constexpr int kIgThreads = 256;
-constexpr int kBM = 128;  // output pixels per workgroup
-constexpr int kBN = 128;  // output channels per workgroup
-constexpr int kBK = 128;  // K bytes per step (MFMA depth)
-constexpr int kMaxTaps = 9;
+constexpr int kIgThreads = 512;  // 8 waves: 2 per SIMD
+constexpr int kWaves = kIgThreads / 64;
+constexpr int kWavesM = 4;
+constexpr int kWTM = 64, kWTN = 64;  // wave tile
+constexpr int kBM = 256;             // output pixels per tile
+constexpr int kBN = 128;             // output channels per tile
+constexpr int kBK = 128;             // K bytes per step (MFMA depth)
+constexpr int kStageBytes = (kBM + kBN) * kBK;         // 48 KB: A tile then B tile
+constexpr int kALoads = kBM * kBK / 16 / kIgThreads;  // 16-B DMA per thread per stage: 4
+constexpr int kBLoads = kBN * kBK / 16 / kIgThreads;  // 2
+constexpr int kLoadsPerStage = kALoads + kBLoads;     // per wave (one per instruction)
+constexpr int kARowsPerWave = kBM / kWaves;           // 32
+constexpr int kBRowsPerWave = kBN / kWaves;           // 16
+constexpr int kSlotBytes = 16 * kWTN * 2;             // 16 pixels x 64 channels of bf16
+constexpr int kMaxTapDim = 3;
 
 struct IgemmArgs {
   const uint8_t* act;  // [N][Hi][Wi][C]
@@ -34,169 +51,272 @@ struct IgemmArgs {
   const float* sa;
   const float* sb;
   const float* bias;  // [Cout] or null
-  int N, Hi, Wi, C, Cout, T;
+  int Hi, Wi, C, Cout, T;
   int Pg, Qg;  // output grid enumerated by this launch
   int Ho, Wo;
   int oy_step, oy_off, ox_step, ox_off;  // out pixel = (i*oy_step + oy_off, j*ox_step + ox_off)
-  int iy_step, ix_step;                  // in pixel  = (i*iy_step + tap_dy, j*ix_step + tap_dx)
+  int iy_step, ix_step;                  // in pixel  = (i*iy_step + dy, j*ix_step + dx)
   int M;                                 // N * Pg * Qg
-  int ntaps;
-  int tap_dy[kMaxTaps], tap_dx[kMaxTaps], tap_w[kMaxTaps];
+  int tiles_n, tiles, tiles_per_xcd, wg_per_xcd;
+  // tap grid: tap (ty, tx), ty < ny, tx < nx: input offset (dy0 + ty*dys, dx0 + tx*dxs),
+  // weight tap w0 + ty*wys + tx*wxs
+  int ny, nx, dy0, dys, dx0, dxs, w0, wys, wxs;
+  int kc_per_tap, nk;  // K-steps per tap (C / 128) and per tile
+  FastDiv divQ, divP, divKC, divNX, divNK, divTN;
 };
 
-__device__ __forceinline__ int swz(int row, int granule) { return granule ^ (row & 7); }
+// 16 zero bytes: the DMA source for padding taps and rows past M.
+__device__ __attribute__((aligned(64))) uint8_t g_zero16[64];
+constexpr int64_t kMaxOperandBytes = 0x7fffffff;  // 32-bit offsets
 
-__global__ __launch_bounds__(kIgThreads) void igemm_fp8_kernel(const IgemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(kBM + kBN) * kBK];
+// Three pipeline stages and the per-wave epilogue slots: 3 x 48 KB + 8 x 2 KB = 160 KB.
+__shared__ __attribute__((aligned(1024))) uint8_t ig_st[3][kStageBytes];
+__shared__ __attribute__((aligned(1024))) uint8_t ig_slot[kWaves][kSlotBytes];
 
+// LDS rows are 128 B = 8 granules of 16 B; granule g of row r lives at (g ^ swz(r)). Measured
+// on gfx950 (SQ_LDS_BANK_CONFLICT): this swizzle makes the 16-row, one-granule fragment
+// reads of ds_read_b128 conflict-free, where (r & 7) or ((r >> 1) & 7) cost 2 passes.
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// 16-B-per-lane global -> LDS DMA (lane i lands at lds + 16 i). Issued through inline asm so
+// the compiler does not guard later LDS reads with conservative vmcnt(0) waits: all waits for
+// these DMAs are the explicit in-order vmcnt counts of the pipeline below (in-order counting
+// keeps every compiler-inserted wait conservative, hence correct).
+__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(lds));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "m0");
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt | lgkmcnt | vmcnt[5:4]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+#ifdef DPA_IG_PROBE
+__device__ unsigned long long g_ig_probe[4096 * 16];
+#define IG_STAMP(slot)                                                                   \
+  do {                                                                                   \
+    if (threadIdx.x == 0 && blockIdx.x < 4096)                                           \
+      g_ig_probe[blockIdx.x * 16 + (slot)] = __builtin_readcyclecounter();               \
+  } while (0)
+#else
+#define IG_STAMP(slot) \
+  do {                 \
+  } while (0)
+#endif
+
+// m -> (n, i, j) of the launch grid [N, Pg, Qg]
+__device__ __forceinline__ void decode_pixel(const IgemmArgs& p, int m, int& n, int& i, int& j) {
+  const uint32_t t = fdiv((uint32_t)m, p.divQ);
+  j = m - (int)t * p.Qg;
+  const uint32_t nn = fdiv(t, p.divP);
+  i = (int)t - (int)nn * p.Pg;
+  n = (int)nn;
+}
+
+__device__ __forceinline__ int out_offset(const IgemmArgs& p, int m) {
+  int n, ii, jj;
+  decode_pixel(p, m, n, ii, jj);
+  return ((n * p.Ho + ii * p.oy_step + p.oy_off) * p.Wo + jj * p.ox_step + p.ox_off) * p.Cout;
+}
+
+__device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
+  const int s = swz(row);
+  const uint4 lo = *reinterpret_cast<const uint4*>(base + row * kBK + (((2 * q) ^ s) * 16));
+  const uint4 hi = *reinterpret_cast<const uint4*>(base + row * kBK + (((2 * q + 1) ^ s) * 16));
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+__global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArgs p) {
+  IG_STAMP(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave & 1;   // pixel half
-  const int wn = wave >> 1;  // channel half
+  const int wm = wave % kWavesM;  // pixel quarter (64 rows)
+  const int wn = wave / kWavesM;  // channel half (64 cols)
+  const int frow = lane & 15, fq = lane >> 4;
 
-  const int m0 = blockIdx.x * kBM;
-  const int n0 = blockIdx.y * kBN;
+  // this workgroup's tiles: XCD x owns tiles [x*tiles_per_xcd, +tiles_per_xcd); its
+  // wg_per_xcd workgroups take them round-robin
+  const int xcd = blockIdx.x & 7;
+  const int wi = blockIdx.x >> 3;
+  const int t_begin = xcd * p.tiles_per_xcd + wi;
+  int t_end = (xcd + 1) * p.tiles_per_xcd;
+  if (t_end > p.tiles) t_end = p.tiles;
+  if (t_begin >= t_end) return;
+  const int nt = (t_end - t_begin + p.wg_per_xcd - 1) / p.wg_per_xcd;
+  const int nk = p.nk;
+  const int total = nt * nk;
+  const float scale = p.sa[0] * p.sb[0];
 
-  // ---- per-thread load assignment: granule g of rows r0 + 32*i ----
-  const int g = tid & 7;
-  const int r0 = tid >> 3;
-  constexpr int kRowsPerThread = kBM / 32;  // A and B both 128 rows
-  int a_base[kRowsPerThread];               // n * Hi (or -1 if pixel out of range)
-  int a_iy[kRowsPerThread], a_ix[kRowsPerThread];
+  // ---- DMA side: row metadata of the tile being loaded ----
+  int a_off[kALoads], a_mask[kALoads], b_off[kBLoads];
+  int dma_tile = -1;
+  auto set_dma_tile = [&](int j) __attribute__((always_inline)) {
+    const int tile = t_begin + j * p.wg_per_xcd;
+    const int tm = (int)fdiv((uint32_t)tile, p.divTN);
+    const int tn = tile - tm * p.tiles_n;
+    const int m0 = tm * kBM, n0 = tn * kBN;
 #pragma unroll
-  for (int i = 0; i < kRowsPerThread; ++i) {
-    const int m = m0 + r0 + 32 * i;
-    if (m < p.M) {
-      const int j = m % p.Qg;
-      const int t = m / p.Qg;
-      const int ii = t % p.Pg;
-      const int n = t / p.Pg;
-      a_base[i] = n * p.Hi;
-      a_iy[i] = ii * p.iy_step;
-      a_ix[i] = j * p.ix_step;
-    } else {
-      a_base[i] = -1;
-      a_iy[i] = 0;
-      a_ix[i] = 0;
-    }
-  }
-
-  const int kc_per_tap = p.C / kBK;
-  const int nk = p.ntaps * kc_per_tap;
-  const int64_t wrow = (int64_t)p.T * p.C;
-
-  uint4 ra[kRowsPerThread], rb[kRowsPerThread];
-
-  auto load_step = [&](int k) {
-    const int t = k / kc_per_tap;
-    const int c0 = (k - t * kc_per_tap) * kBK + g * 16;
-    const int dy = p.tap_dy[t], dx = p.tap_dx[t];
+    for (int r = 0; r < kALoads; ++r) {
+      const int row = wave * kARowsPerWave + 8 * r + (lane >> 3);
+      const int g = (lane & 7) ^ swz(row);
+      const int m = m0 + row;
+      int off = 0, mask = 0;
+      if (m < p.M) {
+        int n, ii, jj;
+        decode_pixel(p, m, n, ii, jj);
+        const int iy0 = ii * p.iy_step, ix0 = jj * p.ix_step;
+        off = ((n * p.Hi + iy0) * p.Wi + ix0) * p.C + g * 16;
 #pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-      const int iy = a_iy[i] + dy, ix = a_ix[i] + dx;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (a_base[i] >= 0 && iy >= 0 && iy < p.Hi && ix >= 0 && ix < p.Wi) {
-        const int64_t off = ((int64_t)(a_base[i] + iy) * p.Wi + ix) * p.C + c0;
-        v = *reinterpret_cast<const uint4*>(p.act + off);
+        for (int ty = 0; ty < kMaxTapDim; ++ty) {
+#pragma unroll
+          for (int tx = 0; tx < kMaxTapDim; ++tx) {
+            const int iy = iy0 + p.dy0 + ty * p.dys, ix = ix0 + p.dx0 + tx * p.dxs;
+            const bool in = (ty < p.ny) & (tx < p.nx) & ((unsigned)iy < (unsigned)p.Hi) &
+                            ((unsigned)ix < (unsigned)p.Wi);
+            mask |= (int)in << (ty * p.nx + tx);
+          }
+        }
       }
-      ra[i] = v;
+      a_off[r] = off;
+      a_mask[r] = mask;
     }
-    const int64_t woff = (int64_t)p.tap_w[t] * p.C + c0;
 #pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-      const int co = n0 + r0 + 32 * i;
-      rb[i] = *reinterpret_cast<const uint4*>(p.wgt + (int64_t)co * wrow + woff);
+    for (int r = 0; r < kBLoads; ++r) {
+      const int row = wave * kBRowsPerWave + 8 * r + (lane >> 3);
+      b_off[r] = (n0 + row) * p.T * p.C + ((lane & 7) ^ swz(row)) * 16;
+    }
+  };
+  // DMA of global step s (tile s / nk, K-step s % nk) into stage buffer st. Steps past the
+  // end load the zero page, so every step issues the same number of DMAs and the wait
+  // counts stay compile-time constants.
+  auto issue = [&](uint8_t* st, int s) __attribute__((always_inline)) {
+    const bool live = s < total;
+    const int ss = live ? s : 0;
+    const int j = (int)fdiv((uint32_t)ss, p.divNK);
+    const int k = ss - j * nk;
+    if (live && j != dma_tile) {
+      set_dma_tile(j);
+      dma_tile = j;
+    }
+    const int t = (int)fdiv((uint32_t)k, p.divKC);
+    const int c0 = (k - t * p.kc_per_tap) * kBK;
+    const int ty = (int)fdiv((uint32_t)t, p.divNX);
+    const int tx = t - ty * p.nx;
+    const int ad = ((p.dy0 + ty * p.dys) * p.Wi + p.dx0 + tx * p.dxs) * p.C + c0;
+    const int wd = (p.w0 + ty * p.wys + tx * p.wxs) * p.C + c0;
+#pragma unroll
+    for (int r = 0; r < kALoads; ++r) {
+      const bool ok = live & ((a_mask[r] >> t) & 1);
+      const uint8_t* real = p.act + (uint32_t)(a_off[r] + ad);
+      // 8 rows of the A tile: 1 KB, lane i -> row +i/8, granule slot i%8
+      dma16(ok ? real : (const uint8_t*)g_zero16, st + (wave * kARowsPerWave + 8 * r) * kBK);
+    }
+#pragma unroll
+    for (int r = 0; r < kBLoads; ++r) {
+      const uint8_t* real = p.wgt + (uint32_t)(b_off[r] + wd);
+      dma16(live ? real : (const uint8_t*)g_zero16,
+            st + kBM * kBK + (wave * kBRowsPerWave + 8 * r) * kBK);
     }
   };
 
-  auto store_step = [&](int buf) {
-    uint8_t* sa = smem[buf];
-    uint8_t* sb = smem[buf] + kBM * kBK;
-#pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-      const int row = r0 + 32 * i;
-      *reinterpret_cast<uint4*>(sa + row * kBK + swz(row, g) * 16) = ra[i];
-      *reinterpret_cast<uint4*>(sb + row * kBK + swz(row, g) * 16) = rb[i];
-    }
-  };
-
+  // ---- compute side ----
   v4f acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8i fa[4], fb[4];
 
-  const int frow = lane & 15;
-  const int fq = lane >> 4;
-
-  load_step(0);
-  store_step(0);
-  __syncthreads();
-
-  for (int k = 0; k < nk; ++k) {
-    const int buf = k & 1;
-    if (k + 1 < nk) load_step(k + 1);
-
-    const uint8_t* sa = smem[buf];
-    const uint8_t* sb = smem[buf] + kBM * kBK;
-    v8i af[4], bf[4];
+  // finished tile j: scale, bias, bf16 -> wave slot -> 128-B runs per pixel
+  auto epilogue = [&](int j) __attribute__((always_inline)) {
+    const int tile = t_begin + j * p.wg_per_xcd;
+    const int tm = (int)fdiv((uint32_t)tile, p.divTN);
+    const int tn = tile - tm * p.tiles_n;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+    uint8_t* slot = ig_slot[wave];
+    const int c0 = n0 + wn * kWTN;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 64 + i * 16 + frow;
-      const uint4 lo = *reinterpret_cast<const uint4*>(sa + row * kBK + swz(row, 2 * fq) * 16);
-      const uint4 hi =
-          *reinterpret_cast<const uint4*>(sa + row * kBK + swz(row, 2 * fq + 1) * 16);
-      af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                  (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
+    for (int pj = 0; pj < 4; ++pj) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wn * 64 + i * 16 + frow;
-      const uint4 lo = *reinterpret_cast<const uint4*>(sb + row * kBK + swz(row, 2 * fq) * 16);
-      const uint4 hi =
-          *reinterpret_cast<const uint4*>(sb + row * kBK + swz(row, 2 * fq + 1) * 16);
-      bf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                  (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-    // D rows = output channels (weight operand), D cols = pixels (activation operand)
+      for (int ci = 0; ci < 4; ++ci) {
+        float v[4];
 #pragma unroll
-    for (int ci = 0; ci < 4; ++ci)
+        for (int e = 0; e < 4; ++e) v[e] = acc[ci][pj][e] * scale;
+        if (p.bias) {
 #pragma unroll
-      for (int pj = 0; pj < 4; ++pj) acc[ci][pj] = mfma16x16x128_e4m3(bf[ci], af[pj], acc[ci][pj]);
-
-    if (k + 1 < nk) store_step(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue ----
-  const float scale = p.sa[0] * p.sb[0];
-#pragma unroll
-  for (int pj = 0; pj < 4; ++pj) {
-    const int m = m0 + wm * 64 + pj * 16 + frow;
-    if (m >= p.M) continue;
-    const int j = m % p.Qg;
-    const int t = m / p.Qg;
-    const int ii = t % p.Pg;
-    const int n = t / p.Pg;
-    const int oy = ii * p.oy_step + p.oy_off;
-    const int ox = j * p.ox_step + p.ox_off;
-    uint16_t* orow = p.out + (((int64_t)n * p.Ho + oy) * p.Wo + ox) * p.Cout;
-#pragma unroll
-    for (int ci = 0; ci < 4; ++ci) {
-      const int co = n0 + wn * 64 + ci * 16 + 4 * fq;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = acc[ci][pj][e] * scale;
-        if (p.bias) v[e] = v[e] + p.bias[co + e];
+          for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[c0 + ci * 16 + 4 * fq + e];
+        }
+        const int g = 2 * ci + (fq >> 1);  // 16-B granule of channels ci*16 + 4*fq
+        uint2 o;
+        o.x = pack_bf16x2(v[0], v[1]);
+        o.y = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(slot + frow * 128 + ((g ^ (frow & 7)) * 16) + (fq & 1) * 8) = o;
       }
-      uint2 o;
-      o.x = f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16);
-      o.y = f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16);
-      *reinterpret_cast<uint2*>(orow + co) = o;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int c = lane + 64 * rr;
+        const int r = c >> 3, g = c & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((g ^ (r & 7)) * 16));
+        const int m = m0 + wm * kWTM + pj * 16 + r;
+        if (m < p.M) *reinterpret_cast<uint4*>(p.out + out_offset(p, m) + c0 + g * 8) = v;
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
+  };
+
+  IG_STAMP(1);
+  issue(ig_st[0], 0);
+  issue(ig_st[1], 1);
+  issue(ig_st[2], 2);
+  IG_STAMP(2);
+  wait_vmcnt<2 * kLoadsPerStage>();
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fb[i] = ld_frag(ig_st[0] + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fa[i] = ld_frag(ig_st[0], wm * kWTM + i * 16 + frow, fq);
+
+  // Step s on stage buffer cur = s % 3: wait until stage s+1 has landed (its DMA was issued
+  // two steps earlier), barrier (every wave finished reading stage s), then the 16 MFMAs on
+  // stage s's fragments with stage s+1's fragments read in between, and queue the DMA of
+  // stage s+3 into buffer cur.
+  int cur = 0, kstep = 0;
+  for (int s = 0; s < total; ++s) {
+    const int nx = cur == 2 ? 0 : cur + 1;
+    wait_vmcnt<kLoadsPerStage>();
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    const uint8_t* nxt = ig_st[nx];
+#pragma unroll
+    for (int pj = 0; pj < 4; ++pj) {
+#pragma unroll
+      for (int ci = 0; ci < 4; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
+      fa[pj] = ld_frag(nxt, wm * kWTM + pj * 16 + frow, fq);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
+    }
+    issue(ig_st[cur], s + 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fb[i] = ld_frag(nxt + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
+    if (++kstep == nk) {
+      kstep = 0;
+      epilogue((int)fdiv((uint32_t)s, p.divNK));
+    }
+    cur = nx;
+    if (s == 0) IG_STAMP(3);
   }
+  wait_vmcnt<0>();  // trailing zero-page DMAs land before the workgroup retires
+  IG_STAMP(4);
 }
 
 // wt[ci][r][s][co] = w[co][r][s][ci] (e4m3 bytes): 32x32 byte tiles through LDS.
@@ -218,10 +338,48 @@ __global__ __launch_bounds__(256) void weight_transpose_kernel(const uint8_t* __
   }
 }
 
-static int launch_igemm(IgemmArgs& a, hipStream_t s) {
+static int g_num_cus = 0;
+
+static int num_cus() {
+  if (g_num_cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      g_num_cus = n;
+    else
+      g_num_cus = 256;
+  }
+  return g_num_cus;
+}
+
+// act geometry (N, Hi, Wi, C), output geometry, tap grid already in `a`
+static int launch_igemm(IgemmArgs& a, int N, hipStream_t s) {
   if (a.M <= 0) return DPA_OK;
-  dim3 grid((unsigned)ceil_div(a.M, kBM), (unsigned)(a.Cout / kBN));
-  igemm_fp8_kernel<<<grid, kIgThreads, 0, s>>>(a);
+  const int64_t act_bytes = (int64_t)N * a.Hi * a.Wi * a.C;
+  const int64_t wgt_bytes = (int64_t)a.Cout * a.T * a.C;
+  const int64_t out_elems = (int64_t)N * a.Ho * a.Wo * a.Cout;
+  if (act_bytes > kMaxOperandBytes || wgt_bytes > kMaxOperandBytes || out_elems > kMaxOperandBytes)
+    return DPA_ERR_SIZE;
+  const int tiles_m = (int)ceil_div(a.M, kBM);
+  a.tiles_n = a.Cout / kBN;
+  a.tiles = tiles_m * a.tiles_n;
+  a.tiles_per_xcd = (int)ceil_div(a.tiles, 8);
+  // one workgroup per CU (160 KB of LDS each), never more than there are tiles
+  int grid = num_cus();
+  grid = (grid / 8) * 8;
+  if (grid < 8) grid = 8;
+  const int max_grid = a.tiles_per_xcd * 8;
+  if (grid > max_grid) grid = max_grid;
+  a.wg_per_xcd = grid / 8;
+  a.kc_per_tap = a.C / kBK;
+  a.nk = a.ny * a.nx * a.kc_per_tap;
+  a.divQ = make_fastdiv((uint32_t)a.Qg);
+  a.divP = make_fastdiv((uint32_t)a.Pg);
+  a.divKC = make_fastdiv((uint32_t)a.kc_per_tap);
+  a.divNX = make_fastdiv((uint32_t)a.nx);
+  a.divNK = make_fastdiv((uint32_t)a.nk);
+  a.divTN = make_fastdiv((uint32_t)a.tiles_n);
+  igemm_fp8_kernel<<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   return launch_status();
 }
 
@@ -251,24 +409,22 @@ static int conv_fwd(const void* xq, const void* wq, const float* xs, const float
   fill_common(a, xq, wq, y, xs, ws, bias);
   const int P = (H + 2 * pad - R) / stride + 1;
   const int Q = (W + 2 * pad - S) / stride + 1;
-  a.N = N; a.Hi = H; a.Wi = W; a.C = Cin; a.Cout = Cout; a.T = R * S;
+  a.Hi = H; a.Wi = W; a.C = Cin; a.Cout = Cout; a.T = R * S;
   a.Pg = P; a.Qg = Q; a.Ho = P; a.Wo = Q;
   a.oy_step = 1; a.oy_off = 0; a.ox_step = 1; a.ox_off = 0;
   a.iy_step = stride; a.ix_step = stride;
   a.M = N * P * Q;
-  a.ntaps = R * S;
-  for (int r = 0; r < R; ++r)
-    for (int c = 0; c < S; ++c) {
-      const int t = r * S + c;
-      a.tap_dy[t] = r - pad;
-      a.tap_dx[t] = c - pad;
-      a.tap_w[t] = t;
-    }
-  return launch_igemm(a, s);
+  // tap (r, s): input offset (r - pad, s - pad), weight tap r*S + s
+  a.ny = R; a.nx = S;
+  a.dy0 = -pad; a.dys = 1; a.dx0 = -pad; a.dxs = 1;
+  a.w0 = 0; a.wys = S; a.wxs = 1;
+  return launch_igemm(a, N, s);
 }
 
 // dx[n, h, w, ci] = sum_{r,s,co} dy[n, (h+pad-r)/st, (w+pad-s)/st, co] * w[co, r, s, ci]
-// over the (r, s) for which the division is exact and in range.
+// over the (r, s) for which the division is exact and in range: one launch per output
+// parity class (ay, ax); within a class the usable r (and s) form an arithmetic progression
+// of step `stride`, so the class's taps are again a linear grid.
 static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const float* ws,
                       void* dx, int N, int H, int W, int Cin, int Cout, int R, int S,
                       int stride, int pad, hipStream_t s) {
@@ -278,33 +434,22 @@ static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const f
     for (int ax = 0; ax < stride; ++ax) {
       IgemmArgs a{};
       fill_common(a, dyq, wt, dx, dys, ws, nullptr);
-      a.N = N; a.Hi = P; a.Wi = Q; a.C = Cout; a.Cout = Cin; a.T = R * S;
+      a.Hi = P; a.Wi = Q; a.C = Cout; a.Cout = Cin; a.T = R * S;
       a.Pg = (H - ay + stride - 1) / stride;
       a.Qg = (W - ax + stride - 1) / stride;
       a.Ho = H; a.Wo = W;
       a.oy_step = stride; a.oy_off = ay; a.ox_step = stride; a.ox_off = ax;
       a.iy_step = 1; a.ix_step = 1;
       a.M = N * a.Pg * a.Qg;
-      int nt = 0;
-      for (int r = 0; r < R; ++r) {
-        const int ey = ay + pad - r;
-        if (((ey % stride) + stride) % stride != 0) continue;
-        for (int c = 0; c < S; ++c) {
-          const int ex = ax + pad - c;
-          if (((ex % stride) + stride) % stride != 0) continue;
-          // floor division of the exact multiples
-          a.tap_dy[nt] = ey >= 0 ? ey / stride : -((-ey) / stride);
-          a.tap_dx[nt] = ex >= 0 ? ex / stride : -((-ex) / stride);
-          a.tap_w[nt] = r * S + c;
-          ++nt;
-        }
-      }
-      a.ntaps = nt;
-      if (nt == 0 || a.M == 0) {
-        // no tap reaches this class (cannot happen for the supported shapes)
-        return DPA_ERR_SHAPE;
-      }
-      int st = launch_igemm(a, s);
+      // first r with (ay + pad - r) divisible by stride, then every stride-th
+      const int r0 = (ay + pad) % stride, s0 = (ax + pad) % stride;
+      a.ny = (R - r0 + stride - 1) / stride;
+      a.nx = (S - s0 + stride - 1) / stride;
+      if (a.ny <= 0 || a.nx <= 0 || a.M == 0) return DPA_ERR_SHAPE;
+      a.dy0 = (ay + pad - r0) / stride; a.dys = -1;
+      a.dx0 = (ax + pad - s0) / stride; a.dxs = -1;
+      a.w0 = r0 * S + s0; a.wys = stride * S; a.wxs = stride;
+      int st = launch_igemm(a, N, s);
       if (st != DPA_OK) return st;
     }
   return DPA_OK;

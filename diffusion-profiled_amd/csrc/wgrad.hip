@@ -6,118 +6,139 @@
 //   conv2d_dw_reduce_fp8_kernel :446-468  -> wgrad_reduce_kernel
 //   conv2d_bwd_weight_fp8_prequantized :723-808 -> dpa_conv2d_wgrad_fp8
 //
-// GEMM view: D[ci][co] (per tap) = sum over output pixels of x[shifted pix][ci] * dy[pix][co].
-// The reduction runs over pixels, which is the strided dimension of both NHWC operands, so
-// each K-step loads a 128-pixel x 128-channel block of each operand with 16-B row loads and
-// transposes it in registers (4x4 byte blocks, v_perm_b32) while writing it to LDS as
-// [channel][pixel]; the MFMA then reads 32 contiguous pixels per lane. No transposed copy
-// of dy or x ever touches HBM.
+// GEMM view, per tap: D[ci][co] = sum over output pixels of x[shifted pix][ci] * dy[pix][co].
+// The reduction runs over pixels, the strided dimension of both NHWC operands. Each K-step
+// DMAs a 128-pixel x 128-channel block of each operand into LDS in its natural layout
+// (global_load_lds, 16 B per lane; padding taps read a zero page), and the MFMA fragments are
+// formed with ds_read_b64_tr_b8: a 16-lane group pointing at an 8-pixel x 16-channel block
+// receives, in lane j, the 8 pixels of channel j. No transposed copy touches HBM or VALU.
 //
 // Workgroup tile: 128 input channels x 128 output channels of one tap; 4 waves (2 x 2) of
-// 64 x 64. The pixel range is split over gridDim.z (split-K); every split writes an fp32
-// partial tile, and the reduce kernel sums splits in index order, scales and casts to bf16.
+// 64 x 64. Pixels are split over workgroups (split-K), ordered so the workgroups that read
+// one pixel range (all taps and channel tiles) share an XCD and its L2. Every split writes
+// an fp32 partial tile (through LDS, as contiguous 512-B rows); the reduce kernel sums the
+// splits in index order, scales by RN32(sx * sdy) and rounds to bf16.
 #include "dpa_common.hpp"
 
 namespace dpa {
 
 constexpr int kWgThreads = 256;
-constexpr int kWgTile = 128;  // channels per tile side and pixels per K-step
+constexpr int kWgTile = 128;                       // channels per tile side, pixels per K-step
+constexpr int kWgOperandBytes = kWgTile * kWgTile;  // 16 KB
+constexpr int kWgStageBytes = 2 * kWgOperandBytes;  // x block then dy block
+constexpr int kWgLoads = kWgOperandBytes / 16 / kWgThreads;  // 4 DMA per operand per thread
+constexpr int kWgPPitch = kWgTile * 4 + 16;  // fp32 partial-tile row pitch in LDS (bytes)
 
-// LDS row swizzle: rows are 128 B = 8 granules of 16 B.
-__device__ __forceinline__ int wswz(int row) { return (row ^ (row >> 4)) & 7; }
+__shared__ __attribute__((aligned(1024))) uint8_t wg_smem[3 * kWgStageBytes];
+static_assert(kWgTile * kWgPPitch <= 3 * kWgStageBytes, "partial tile must fit in LDS");
+
+__device__ __attribute__((aligned(64))) uint8_t wg_zero16[64];
+
+// Row r (a pixel, 128 B) keeps its 16-B granule g at g ^ wswz(r): conflict-free for the
+// transpose reads (8 rows per 16-lane group, 4 groups at row offsets of 32).
+__device__ __forceinline__ int wswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
+
+#define WG_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
 struct WgradArgs {
   const uint8_t* x;   // [N][H][W][Cin]
   const uint8_t* dy;  // [N][P][Q][Cout]
   float* partial;     // [splits][Cout][T*Cin]
   int N, H, W, Cin, Cout, R, S, stride, pad, P, Q;
-  int npix;           // N*P*Q
-  int nchunks;        // ceil(npix / 128)
-  int splits;
+  int npix, nchunks, splits;
+  int ci_tiles, co_tiles, taps;
+  int total, per_xcd;
+  FastDiv divQ, divP;
 };
 
-// 4 rows (pixels) x 16 bytes (channels) -> 16 dwords, dword j = bytes j of the 4 rows.
-__device__ __forceinline__ void transpose4x16(const uint4 (&r)[4], uint32_t (&o)[16]) {
-  const uint32_t a[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
-  const uint32_t b[4] = {r[1].x, r[1].y, r[1].z, r[1].w};
-  const uint32_t c[4] = {r[2].x, r[2].y, r[2].z, r[2].w};
-  const uint32_t d[4] = {r[3].x, r[3].y, r[3].z, r[3].w};
+template <int ST>
+__device__ __forceinline__ void wg_issue(const WgradArgs& p, int chunk, int ci0, int co0, int kr,
+                                         int ks, int wave, int lane) {
+  uint8_t* st = wg_smem + ST * kWgStageBytes;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t lo01 = perm_b32(b[k], a[k], 0x05010400u);  // a0 b0 a1 b1
-    const uint32_t hi01 = perm_b32(b[k], a[k], 0x07030602u);  // a2 b2 a3 b3
-    const uint32_t lo23 = perm_b32(d[k], c[k], 0x05010400u);  // c0 d0 c1 d1
-    const uint32_t hi23 = perm_b32(d[k], c[k], 0x07030602u);  // c2 d2 c3 d3
-    o[4 * k + 0] = perm_b32(lo23, lo01, 0x05040100u);         // a0 b0 c0 d0
-    o[4 * k + 1] = perm_b32(lo23, lo01, 0x07060302u);         // a1 b1 c1 d1
-    o[4 * k + 2] = perm_b32(hi23, hi01, 0x05040100u);         // a2 b2 c2 d2
-    o[4 * k + 3] = perm_b32(hi23, hi01, 0x07060302u);         // a3 b3 c3 d3
+  for (int j = 0; j < kWgLoads; ++j) {
+    const int row = wave * 32 + 8 * j + (lane >> 3);
+    const int g = (lane & 7) ^ wswz(row);
+    const int pix = chunk * kWgTile + row;
+    const uint8_t* xs = wg_zero16;
+    const uint8_t* ds = wg_zero16;
+    if (pix < p.npix) {
+      ds = p.dy + (uint32_t)(pix * p.Cout + co0 + g * 16);
+      const uint32_t t = fdiv((uint32_t)pix, p.divQ);
+      const int q = pix - (int)t * p.Q;
+      const uint32_t n = fdiv(t, p.divP);
+      const int pp = (int)t - (int)n * p.P;
+      const int ih = pp * p.stride + kr - p.pad;
+      const int iw = q * p.stride + ks - p.pad;
+      if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
+        xs = p.x + (uint32_t)((((int)n * p.H + ih) * p.W + iw) * p.Cin + ci0 + g * 16);
+    }
+    __builtin_amdgcn_global_load_lds(xs, WG_LDS(st + (wave * 32 + 8 * j) * kWgTile), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ds, WG_LDS(st + kWgOperandBytes + (wave * 32 + 8 * j) * kWgTile),
+                                     16, 0, 0);
   }
 }
 
-__global__ __launch_bounds__(kWgThreads) void wgrad_partial_kernel(const WgradArgs p) {
-  // [buf][operand x|dy][128 rows (channels)][128 B (pixels)]
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kWgTile * kWgTile];
+typedef int v2i __attribute__((ext_vector_type(2)));
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+// 32 pixels (K) x 1 channel per lane: lane l -> channel row (l & 15) of the 16-channel
+// group starting at granule G, pixels [32*(l>>4), +32), via four 8-pixel transpose reads.
+__device__ __forceinline__ v8i ld_frag_tr(const uint8_t* base, int G, int lane) {
+  const int k = lane & 15, q = lane >> 4;
+  v8i f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int row = 32 * q + 8 * s + (k >> 1);
+    const uint8_t* a = base + row * kWgTile + ((G ^ wswz(row)) * 16) + 8 * (k & 1);
+    const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (v2i __attribute__((address_space(3)))*)(a));
+    f[2 * s] = v.x;
+    f[2 * s + 1] = v.y;
+  }
+  return f;
+}
+
+template <int ST>
+__device__ __forceinline__ void wg_step(const WgradArgs& p, int c, int c_end, int ci0, int co0,
+                                        int kr, int ks, int wave, int lane, int wc, int wo,
+                                        v4f (&acc)[4][4]) {
+  __syncthreads();  // this stage's DMA landed (the fence waits for it) and is visible to all
+  const uint8_t* sx = wg_smem + ST * kWgStageBytes;
+  const uint8_t* sd = sx + kWgOperandBytes;
+  v8i xf[4], df[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xf[i] = ld_frag_tr(sx, wc * 4 + i, lane);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) df[i] = ld_frag_tr(sd, wo * 4 + i, lane);
+  if (c + 2 < c_end) wg_issue<(ST + 2) % 3>(p, c + 2, ci0, co0, kr, ks, wave, lane);
+  // D rows = input channels, D cols = output channels
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xf[i], df[j], acc[i][j]);
+}
+
+__global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const WgradArgs p) {
+  // XCD-aware order: logical workgroup index = split-major, so the workgroups reading one
+  // pixel range are consecutive and land on the same XCD (hardware deals round-robin).
+  const int logical = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+  if (logical >= p.total) return;
+  const int per_split = p.ci_tiles * p.co_tiles * p.taps;
+  const int split = logical / per_split;
+  int rem = logical - split * per_split;
+  const int tap = rem / (p.ci_tiles * p.co_tiles);
+  rem -= tap * (p.ci_tiles * p.co_tiles);
+  const int ci0 = (rem % p.ci_tiles) * kWgTile;
+  const int co0 = (rem / p.ci_tiles) * kWgTile;
+  const int kr = tap / p.S, ks = tap - (tap / p.S) * p.S;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int wc = wave & 1;   // input-channel half (D rows)
   const int wo = wave >> 1;  // output-channel half (D cols)
 
-  const int ci_tiles = p.Cin / kWgTile;
-  const int ci0 = (blockIdx.x % ci_tiles) * kWgTile;
-  const int co0 = (blockIdx.x / ci_tiles) * kWgTile;
-  const int tap = blockIdx.y;
-  const int kr = tap / p.S, ks = tap % p.S;
-  const int split = blockIdx.z;
-
-  // pixel chunks [c_begin, c_end) of this split
   const int c_begin = (int)(((int64_t)p.nchunks * split) / p.splits);
   const int c_end = (int)(((int64_t)p.nchunks * (split + 1)) / p.splits);
-
-  // load assignment: pixel quad pq (4 pixels), channel granule cg (16 channels)
-  const int pq = tid >> 3;  // 0..31
-  const int cg = tid & 7;   // 0..7
-
-  uint4 rx[4], rd[4];
-  auto load_step = [&](int chunk) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pix = chunk * kWgTile + pq * 4 + e;
-      uint4 vx = {0u, 0u, 0u, 0u}, vd = {0u, 0u, 0u, 0u};
-      if (pix < p.npix) {
-        vd = *reinterpret_cast<const uint4*>(p.dy + (int64_t)pix * p.Cout + co0 + cg * 16);
-        const int q = pix % p.Q;
-        const int t = pix / p.Q;
-        const int pp = t % p.P;
-        const int n = t / p.P;
-        const int ih = pp * p.stride + kr - p.pad;
-        const int iw = q * p.stride + ks - p.pad;
-        if (ih >= 0 && ih < p.H && iw >= 0 && iw < p.W)
-          vx = *reinterpret_cast<const uint4*>(
-              p.x + (((int64_t)n * p.H + ih) * p.W + iw) * p.Cin + ci0 + cg * 16);
-      }
-      rx[e] = vx;
-      rd[e] = vd;
-    }
-  };
-  auto store_step = [&](int buf) {
-    uint32_t tx[16], td[16];
-    transpose4x16(rx, tx);
-    transpose4x16(rd, td);
-    uint8_t* sx = smem[buf][0];
-    uint8_t* sd = smem[buf][1];
-    const int gr = pq >> 2;        // granule within the 128-pixel row
-    const int wi = (pq & 3) * 4;   // byte within granule
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int row = cg * 16 + j;
-      const int off = row * kWgTile + ((gr ^ wswz(row)) * 16) + wi;
-      *reinterpret_cast<uint32_t*>(sx + off) = tx[j];
-      *reinterpret_cast<uint32_t*>(sd + off) = td[j];
-    }
-  };
 
   v4f acc[4][4];
 #pragma unroll
@@ -125,63 +146,37 @@ __global__ __launch_bounds__(kWgThreads) void wgrad_partial_kernel(const WgradAr
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int frow = lane & 15;
-  const int fq = lane >> 4;
-
-  if (c_begin < c_end) {
-    load_step(c_begin);
-    store_step(0);
+  if (c_begin < c_end) wg_issue<0>(p, c_begin, ci0, co0, kr, ks, wave, lane);
+  if (c_begin + 1 < c_end) wg_issue<1>(p, c_begin + 1, ci0, co0, kr, ks, wave, lane);
+  for (int c = c_begin; c < c_end; c += 3) {
+    wg_step<0>(p, c, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
+    if (c + 1 < c_end) wg_step<1>(p, c + 1, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
+    if (c + 2 < c_end) wg_step<2>(p, c + 2, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
   }
+
+  // partial[split][co][tap*Cin + ci]: stage [co][ci] fp32 in LDS, then 512-B row stores
   __syncthreads();
-
-  for (int c = c_begin; c < c_end; ++c) {
-    const int buf = (c - c_begin) & 1;
-    if (c + 1 < c_end) load_step(c + 1);
-
-    const uint8_t* sx = smem[buf][0];
-    const uint8_t* sd = smem[buf][1];
-    v8i xf[4], df[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wc * 64 + i * 16 + frow;
-      const int sw = wswz(row);
-      const uint4 lo = *reinterpret_cast<const uint4*>(sx + row * kWgTile + ((2 * fq) ^ sw) * 16);
-      const uint4 hi =
-          *reinterpret_cast<const uint4*>(sx + row * kWgTile + ((2 * fq + 1) ^ sw) * 16);
-      xf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                  (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wo * 64 + i * 16 + frow;
-      const int sw = wswz(row);
-      const uint4 lo = *reinterpret_cast<const uint4*>(sd + row * kWgTile + ((2 * fq) ^ sw) * 16);
-      const uint4 hi =
-          *reinterpret_cast<const uint4*>(sd + row * kWgTile + ((2 * fq + 1) ^ sw) * 16);
-      df[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                  (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-    // D rows = input channels, D cols = output channels
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xf[i], df[j], acc[i][j]);
-
-    if (c + 1 < c_end) store_step(buf ^ 1);
-    __syncthreads();
-  }
-
-  // partial[split][co][tap*Cin + ci]: lane holds 4 consecutive ci for one co -> float4
-  const int64_t kk = (int64_t)p.R * p.S * p.Cin;
-  float* base = p.partial + (int64_t)split * p.Cout * kk + (int64_t)tap * p.Cin;
+  const int frow = lane & 15, fq = lane >> 4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int co = co0 + wo * 64 + j * 16 + frow;
+    const int co = wo * 64 + j * 16 + frow;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ci = ci0 + wc * 64 + i * 16 + 4 * fq;
-      *reinterpret_cast<v4f*>(base + (int64_t)co * kk + ci) = acc[i][j];
+      const int ci = wc * 64 + i * 16 + 4 * fq;
+      *reinterpret_cast<v4f*>(wg_smem + co * kWgPPitch + ci * 4) = acc[i][j];
     }
+  }
+  __syncthreads();
+  const int64_t kk = (int64_t)p.taps * p.Cin;
+  float* base = p.partial + (int64_t)split * p.Cout * kk + (int64_t)tap * p.Cin + ci0;
+  constexpr int kChunks = kWgTile * 4 / 16;            // 32 x 16 B per co row
+  constexpr int kRowsPerPass = kWgThreads / kChunks;  // 8
+  const int ch = threadIdx.x % kChunks;
+#pragma unroll 4
+  for (int r0 = 0; r0 < kWgTile; r0 += kRowsPerPass) {
+    const int co = r0 + threadIdx.x / kChunks;
+    *reinterpret_cast<v4f*>(base + (int64_t)(co0 + co) * kk + ch * 4) =
+        *reinterpret_cast<const v4f*>(wg_smem + co * kWgPPitch + ch * 16);
   }
 }
 
@@ -214,16 +209,6 @@ static bool wgrad_shape_ok(int N, int H, int W, int Cin, int Cout, int R, int S,
   return k3 || k1;
 }
 
-static int default_splits(int tiles, int nchunks) {
-  // one round of workgroups over the 256 CUs, at least 4 K-steps per split
-  int s = 256 / (tiles > 0 ? tiles : 1);
-  if (s < 1) s = 1;
-  int maxs = nchunks / 4;
-  if (maxs < 1) maxs = 1;
-  if (s > maxs) s = maxs;
-  return s;
-}
-
 struct WgradPlan {
   int P, Q, npix, nchunks, tiles, splits;
 };
@@ -236,7 +221,16 @@ static WgradPlan plan_wgrad(int N, int H, int W, int Cin, int Cout, int R, int S
   pl.npix = N * pl.P * pl.Q;
   pl.nchunks = (int)ceil_div(pl.npix, kWgTile);
   pl.tiles = (Cin / kWgTile) * (Cout / kWgTile) * R * S;
-  pl.splits = split_k > 0 ? split_k : default_splits(pl.tiles, pl.nchunks);
+  if (split_k > 0) {
+    pl.splits = split_k;
+  } else {
+    // one round of workgroups over the 256 CUs, at least 4 K-steps per split
+    int s = 256 / pl.tiles;
+    if (s < 1) s = 1;
+    int maxs = pl.nchunks / 4;
+    if (maxs < 1) maxs = 1;
+    pl.splits = s < maxs ? s : maxs;
+  }
   if (pl.splits > pl.nchunks) pl.splits = pl.nchunks;
   return pl;
 }
@@ -266,6 +260,9 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   if (!workspace || workspace_bytes < need) return DPA_ERR_WORKSPACE;
   if (!aligned(xq, 16) || !aligned(dyq, 16) || !aligned(workspace, 16) || !aligned(dw, 8))
     return DPA_ERR_ALIGN;
+  // 32-bit byte offsets inside the kernel
+  if ((int64_t)N * H * W * Cin > 0x7fffffff || (int64_t)pl.npix * Cout > 0x7fffffff)
+    return DPA_ERR_SIZE;
   hipStream_t s = (hipStream_t)stream;
   WgradArgs a{};
   a.x = (const uint8_t*)xq;
@@ -274,9 +271,14 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   a.N = N; a.H = H; a.W = W; a.Cin = Cin; a.Cout = Cout; a.R = R; a.S = S;
   a.stride = stride; a.pad = pad; a.P = pl.P; a.Q = pl.Q;
   a.npix = pl.npix; a.nchunks = pl.nchunks; a.splits = pl.splits;
-  dim3 grid((unsigned)((Cin / kWgTile) * (Cout / kWgTile)), (unsigned)(R * S),
-            (unsigned)pl.splits);
-  wgrad_partial_kernel<<<grid, kWgThreads, 0, s>>>(a);
+  a.ci_tiles = Cin / kWgTile;
+  a.co_tiles = Cout / kWgTile;
+  a.taps = R * S;
+  a.total = pl.tiles * pl.splits;
+  a.per_xcd = (int)ceil_div(a.total, 8);
+  a.divQ = make_fastdiv((uint32_t)pl.Q);
+  a.divP = make_fastdiv((uint32_t)pl.P);
+  wgrad_partial_kernel<<<(unsigned)(a.per_xcd * 8), kWgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
   const int64_t total = (int64_t)Cout * R * S * Cin;
