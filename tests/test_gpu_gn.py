@@ -1,0 +1,150 @@
+"""GPU parity of the fused GroupNorm(+FiLM)+SiLU forward/backward against the float64 oracle.
+
+The reference runs GroupNorm and SiLU in float32 under autocast (diffusion/unet.py:151,
+:157-159) and the FP8 conv then rounds the result to bf16 (diffusion/fp8_kernels.py:835). The
+fused kernel emits that bf16 directly. Against the float64 oracle, a float32 evaluation may
+land on the other side of a bf16 rounding boundary, so the forward bar is one bf16 ulp, with
+almost every element bit-identical. Gradients are float32 reductions: normwise 1e-4 for the
+parameter gradients and the conv tolerance (one bf16 ulp + noise) for dx.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import assert_bf16_close, dpa_mod, nhwc_bits, randn_bf16
+from oracle import fp8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GROUPS = 32
+
+
+@pytest.fixture(scope="module")
+def G():
+    return dpa_mod("gn_silu")
+
+
+def cl(t):
+    return t.cuda().contiguous(memory_format=torch.channels_last)
+
+
+def params(c, n, seed, film):
+    g = torch.Generator().manual_seed(seed)
+    gamma = 1.0 + 0.1 * torch.randn(c, generator=g)
+    beta = 0.1 * torch.randn(c, generator=g)
+    fs = fb = None
+    if film:
+        fs = 1.0 + 0.2 * torch.randn(n, c, generator=g)   # the reference's (w + 1)
+        fb = 0.2 * torch.randn(n, c, generator=g)
+    return gamma, beta, fs, fb
+
+
+def assert_fwd_close(got_bits, ref_bits, what):
+    g = O.bf16_bits_to_f32(got_bits).astype(np.float64)
+    r = O.bf16_bits_to_f32(ref_bits).astype(np.float64)
+    assert np.isfinite(g).all(), what
+    # one bf16 ulp of the reference (at most 2^-7 |r|) plus float32 noise near zero
+    bad = np.abs(g - r) > 2.0**-7 * np.abs(r) + 1e-6
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond 1 bf16 ulp"
+    exact = float(np.mean(got_bits == ref_bits))
+    assert exact > 0.995, f"{what}: only {exact:.4f} bit-identical"
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+
+
+CASES = [
+    # (n, c, h, w, film): the reference U-Net's GroupNorm sites at reduced batch
+    (2, 128, 32, 32, False),
+    (2, 256, 16, 16, True),
+    (2, 512, 8, 8, False),
+    (3, 256, 4, 4, True),
+    (2, 256, 7, 9, True),    # ragged pixel count
+    (1, 128, 5, 3, False),
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,film", CASES, ids=lambda v: str(v))
+def test_gn_silu_fwd_bwd_vs_oracle(G, n, c, h, w, film):
+    if not G.supported(c, GROUPS):
+        pytest.skip(f"C={c}, G={GROUPS} outside the fused kernel's shapes")
+    seed = n * 1000 + c + h
+    x = randn_bf16((n, c, h, w), seed=seed, std=2.0)
+    x = (x.float() + 0.5).to(torch.bfloat16)      # non-zero group means
+    dout = randn_bf16((n, c, h, w), seed=seed + 1, std=1e-2)
+    gamma, beta, fs, fb = params(c, n, seed + 2, film)
+    fs_d = None if fs is None else fs.cuda()[:, :, None, None]
+    fb_d = None if fb is None else fb.cuda()[:, :, None, None]
+
+    out, mean, rstd = G.gn_silu_fwd(cl(x), gamma.cuda(), beta.cuda(), GROUPS, 1e-5, fs_d, fb_d)
+    dx, dgamma, dbeta, dfs, dfb = G.gn_silu_bwd(
+        cl(x), cl(dout), gamma.cuda(), beta.cuda(), mean, rstd, GROUPS, fs_d, fb_d)
+    torch.cuda.synchronize()
+
+    xb = nhwc_bits(x)
+    npf = None if fs is None else fs.numpy()
+    npb = None if fb is None else fb.numpy()
+    ref = O.gn_silu_fwd(xb, gamma.numpy(), beta.numpy(), GROUPS, 1e-5, npf, npb)
+    assert out.is_contiguous(memory_format=torch.channels_last) and out.dtype == torch.bfloat16
+    assert_fwd_close(nhwc_bits(out.cpu()), ref, f"fwd {(n, c, h, w, film)}")
+
+    # group statistics
+    xg = O.bf16_bits_to_f32(xb).astype(np.float64).reshape(n, h * w, GROUPS, c // GROUPS)
+    m_ref = xg.mean(axis=(1, 3))
+    v_ref = xg.var(axis=(1, 3))
+    assert rel(mean.cpu().numpy().reshape(n, GROUPS), m_ref) < 1e-5
+    assert rel(rstd.cpu().numpy().reshape(n, GROUPS), 1 / np.sqrt(v_ref + 1e-5)) < 1e-5
+
+    rdx, rdg, rdb, rdfs, rdfb = O.gn_silu_bwd(xb, nhwc_bits(dout), gamma.numpy(), beta.numpy(),
+                                             GROUPS, 1e-5, npf, npb)
+    assert_bf16_close(nhwc_bits(dx.cpu()), O.f32_to_bf16_bits(rdx.astype(np.float32)),
+                      f"dx {(n, c, h, w, film)}")
+    assert rel(dgamma.cpu().numpy(), rdg) < 1e-4
+    assert rel(dbeta.cpu().numpy(), rdb) < 1e-4
+    if film:
+        assert rel(dfs.cpu().numpy(), rdfs) < 1e-4
+        assert rel(dfb.cpu().numpy(), rdfb) < 1e-4
+    else:
+        assert dfs is None and dfb is None
+
+
+def test_gn_silu_cfg4_full_size_vs_torch_fp32(G):
+    """cfg4's norm2 site at full size ([128,256,16,16] with FiLM) through the autograd
+    Function, against torch float32 GroupNorm+SiLU on the GPU."""
+    n, c, h, w = 128, 256, 16, 16
+    x = cl(randn_bf16((n, c, h, w), seed=0))
+    gamma, beta, fs, fb = params(c, n, 3, True)
+    gamma, beta = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    fs = fs.cuda()[:, :, None, None].requires_grad_()
+    fb = fb.cuda()[:, :, None, None].requires_grad_()
+    dout = cl(randn_bf16((n, c, h, w), seed=1, std=1e-2))
+
+    xa = x.clone().requires_grad_()
+    out = G.group_norm_silu(xa, gamma, beta, GROUPS, 1e-5, fs, fb)
+    out.backward(dout)
+
+    xr = x.float().clone().requires_grad_()
+    gr, br = gamma.detach().clone().requires_grad_(), beta.detach().clone().requires_grad_()
+    fsr, fbr = fs.detach().clone().requires_grad_(), fb.detach().clone().requires_grad_()
+    ref = F.silu(fsr * F.group_norm(xr, GROUPS, gr, br, 1e-5) + fbr)
+    ref.backward(dout.float())
+    torch.cuda.synchronize()
+
+    def nerr(a, b):
+        a, b = a.detach().float(), b.detach().float()
+        return float((a - b).norm() / b.norm())
+
+    assert out.dtype == torch.bfloat16
+    assert nerr(out, ref) < 2**-8
+    assert nerr(xa.grad, xr.grad) < 1e-2
+    assert xa.grad.dtype == torch.bfloat16
+    for got, want in ((gamma.grad, gr.grad), (beta.grad, br.grad), (fs.grad, fsr.grad),
+                      (fb.grad, fbr.grad)):
+        assert got.shape == want.shape
+        assert nerr(got, want) < 1e-3
