@@ -5,7 +5,7 @@ A step is one pass of the hot path over one batch: the FP8 3x3 conv of BASELINE 
 including the per-tensor e4m3 quantization of x, w and dy — exactly what
 Conv2dFP8Specialized does per layer in the reference (diffusion/fp8_kernels.py:826-913).
 
-    python bench.py [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3s2|cfg3k1]
+    python bench.py [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3|cfg3s2|cfg3k1|cfg4|cfg5]
 
 Prints ONE JSON line. `value` is TFLOP/s of algorithmic conv work (3 x 2*M*N*K per step)
 with inputs resident in HBM; the step is captured once as a HIP graph and replayed K times
@@ -13,7 +13,12 @@ with inputs resident in HBM; the step is captured once as a HIP graph and replay
 kernel: HIP events around a graph replay of many calls, recorded on the replay stream (the
 stream every kernel of the library is launched on). `cpu_baseline` times the
 oracle's CPU path (the reference recipe on torch CPU: e4m3 round trip + fp32 conv) on a
-bounded sample of the same workload.
+bounded sample of the same workload. The default run also measures the graph-captured U-Net
+training step at batch 128 (`unet_train_step`, the second half of the metric).
+
+cfg4 (one ResidualBlock fwd+bwd at 16x16/256/batch 128) and cfg5 (the full training step:
+forward, backward, clip, AdamW, EMA) are model-level workloads; their `value` is TFLOP/s of
+FP8 GEMM work (cfg4) and training steps/s (cfg5).
 """
 from __future__ import annotations
 
@@ -40,7 +45,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="cfg2", choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1"])
+    ap.add_argument("--workload", default="cfg2",
+                    choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1", "cfg4", "cfg5"])
+    ap.add_argument("--no-unet", action="store_true", help="skip the U-Net step in the cfg2 line")
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -154,6 +161,149 @@ class GemmWorkload:
 
     def config(self):
         return {"workload": self.name, "m": self.m, "n": self.nn, "k": self.kk}
+
+
+def fp8_gemm_flops(model, batch, res=32):
+    """Forward FLOPs (2*M*N*K) of every FP8 GEMM site of a U-Net (3x3 and 1x1 convs,
+    linears) at the given batch, from one shape-tracing forward on the CPU with FP8 off."""
+    import copy
+
+    U = importlib.import_module("diffusion-profiled_amd.unet")
+    cfg = copy.deepcopy(model.config)
+    cfg.fp8_convs_enabled = cfg.fp8_linears = False
+    probe = U.UNet(cfg)
+    total = [0.0]
+
+    def conv_hook(mod, inp, out):
+        w = mod.conv.weight if isinstance(mod, U.Conv2dFP8) else mod.weight
+        total[0] += 2.0 * out.shape[0] * out.shape[2] * out.shape[3] * w.shape[0] * w[0].numel()
+
+    def lin_hook(mod, inp, out):
+        total[0] += 2.0 * out.numel() * mod.in_features
+
+    for m in probe.modules():
+        if isinstance(m, (U.Conv2dFP8, U.Conv1x1FP8)):
+            m.register_forward_hook(conv_hook)
+        elif isinstance(m, U.LinearFP8):
+            m.register_forward_hook(lin_hook)
+    with torch.no_grad():
+        probe(torch.zeros(1, cfg.in_channels, res, res), torch.zeros(1, dtype=torch.long))
+    return total[0] * batch
+
+
+class ResBlockWorkload:
+    """cfg4: one ResidualBlock (GN+SiLU -> FP8 3x3 -> FiLM -> GN+SiLU -> dropout 0.1 -> FP8
+    3x3 -> residual) at [128,256,16,16], forward + backward under bf16 autocast."""
+
+    def __init__(self):
+        U = importlib.import_module("diffusion-profiled_amd.unet")
+        cfg = U.cfg5_config(fp8_scaling_type="current", p_drop=0.1)
+        torch.manual_seed(0)
+        self.blk = U.ResidualBlock(cfg, 256, 256, p_drop=0.1).cuda().to(memory_format=torch.channels_last)
+        import math
+
+        torch.nn.init.kaiming_uniform_(self.blk.conv_2.conv.weight, a=math.sqrt(5))
+        cl = torch.channels_last
+        self.x = seeded((128, 256, 16, 16), 0).cuda().contiguous(memory_format=cl).requires_grad_()
+        g = torch.Generator().manual_seed(3)
+        self.temb = torch.randn((128, 512), generator=g).to(torch.bfloat16).cuda().requires_grad_()
+        self.dout = seeded((128, 256, 16, 16), 2, std=1e-2).cuda().contiguous(memory_format=cl)
+        self.flop = 2.0 * 128 * 16 * 16 * 256 * 256 * 9      # one conv GEMM
+        self.name = ("cfg4: ResidualBlock 256->256 @16x16, batch 128, fused GN+SiLU(+FiLM), FP8 3x3 "
+                     "convs, dropout 0.1, fwd+bwd")
+
+    def step(self):
+        for p in self.blk.parameters():
+            p.grad = None
+        self.x.grad = None
+        self.temb.grad = None
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = self.blk(self.x, self.temb)
+        out.backward(self.dout)
+
+    def step_flop(self):
+        return 6 * self.flop
+
+    def config(self):
+        return {"workload": self.name, "batch": 128, "channels": 256, "h": 16, "w": 16}
+
+
+class UNetStepWorkload:
+    """cfg5: the full DDPM U-Net training step at batch 128 (forward, eps-MSE, backward,
+    clip_grad_norm, AdamW, EMA), captured as one HIP graph (the reference's
+    prepare_cuda_graph, train.py:104-149)."""
+
+    def __init__(self, batch=128):
+        U = importlib.import_module("diffusion-profiled_amd.unet")
+        T = importlib.import_module("diffusion-profiled_amd.trainer")
+        self.batch = batch
+        self.state = T.TrainState(U.cfg5_config(), batch=batch, lr=2e-4, seed=0)
+        g = torch.Generator().manual_seed(4)
+        self.state.set_batch((torch.rand((batch, 3, 32, 32), generator=g) * 2 - 1).cuda())
+        self.fwd_flop = fp8_gemm_flops(self.state.model, batch)
+        self.name = ("cfg5: DDPM U-Net train step, ch 128, mults (1,2,2,2), 2 ResBlocks/level, "
+                     "attention at 16x16 and 8x8 + mid, 33.57M params, batch 128, FP8 convs+linears "
+                     "(delayed scaling), AdamW lr 2e-4, EMA, one HIP graph")
+
+    def capture(self):
+        self.state.capture(warmup=3)
+
+    def step(self):
+        self.state.replay()
+
+    def step_flop(self):
+        return 3 * self.fwd_flop
+
+    def config(self):
+        return {"workload": self.name, "batch": self.batch, "image": [3, 32, 32],
+                "params": sum(p.numel() for p in self.state.model.parameters())}
+
+
+def time_graph_steps(g_replay, steps, warmup):
+    for _ in range(warmup):
+        g_replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g_replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def unet_step_summary(steps, warmup):
+    wl = UNetStepWorkload()
+    wl.capture()
+    dt = time_graph_steps(wl.step, steps, warmup)
+    loss = float(wl.state.loss_acc) / max(1, steps + warmup)
+    return wl, dt, {
+        "steps_per_s": round(1.0 / dt, 3),
+        "ms_per_step": round(dt * 1e3, 3),
+        "fp8_gemm_tflops": round(wl.step_flop() / dt / 1e12, 2),
+        "fp8_gemm_tflop_per_step": round(wl.step_flop() / 1e12, 4),
+        "mean_loss": round(loss, 5),
+        "config": wl.config(),
+    }
+
+
+def model_main(args):
+    base = {
+        "metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8e4m3 GEMMs (fp32 accumulate), bf16 activations, fp32 master weights",
+        "data": "synthetic (seeded images U[-1,1] / N(0,1) activations; random-init weights)",
+        "higher_is_better": True,
+    }
+    if args.workload == "cfg5":
+        wl, dt, summ = unet_step_summary(args.steps, args.warmup)
+        out = dict(base, value=summ["steps_per_s"], unit="steps/s", ms_per_step=summ["ms_per_step"],
+                   config=wl.config(), unet_train_step=summ, roofline=None)
+    else:
+        wl = ResBlockWorkload()
+        g = capture(wl.step, 1)
+        dt = time_graph_steps(g.replay, args.steps, args.warmup)
+        out = dict(base, value=round(wl.step_flop() / dt / 1e12, 2), unit="TFLOP/s",
+                   ms_per_step=round(dt * 1e3, 4), config=wl.config(), roofline=None)
+    print(json.dumps(out), flush=True)
 
 
 def make_workload(K, name):
@@ -271,6 +421,8 @@ def main():
         sys.exit(2)
     K = importlib.import_module("diffusion-profiled_amd.fp8_kernels")
     importlib.import_module("diffusion-profiled_amd._lib").load()
+    if args.workload in ("cfg4", "cfg5"):
+        return model_main(args)
     wl = make_workload(K, args.workload)
 
     # per-part device times (HIP events on the launch stream)
@@ -334,6 +486,9 @@ def main():
         },
         "kernels": kernels,
     }
+    if args.workload == "cfg2" and not args.no_unet:
+        del g
+        _, _, out["unet_train_step"] = unet_step_summary(20, 3)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -379,7 +379,9 @@ class Conv2dFP8Specialized(torch.autograd.Function):
         do_delayed: bool = False,
     ) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         x = x.to(torch.bfloat16)
-        weight = weight.to(torch.bfloat16)
+        # the reference relies on the model having been converted to channels-last; a
+        # contiguous (OIHW) parameter is converted here instead of producing wrong results
+        weight = weight.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
 
         assert x.is_contiguous(memory_format=torch.channels_last)
 
@@ -518,3 +520,111 @@ def linear_fp8(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None 
     wq, wsc = quantize_fp8_tensor(weight.to(torch.bfloat16))
     y = linear_fp8_prequantized(xq, wq, xs, wsc, bias)
     return y.reshape(*lead, weight.shape[0])
+
+
+def linear_fp8_dgrad_prequantized(
+    dy: torch.Tensor,
+    weight: torch.Tensor,
+    dy_scale: torch.Tensor,
+    weight_scale: torch.Tensor,
+) -> torch.Tensor:
+    """dx[M, K] = bf16(dy[M, N] @ weight[N, K] * dy_scale * weight_scale); e4m3 inputs.
+
+    Runs the 1x1 data-gradient kernel on M one-pixel images."""
+    assert dy.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE and dy.ndim == weight.ndim == 2
+    assert dy.shape[1] == weight.shape[0]
+    torch_checks_scale(dy_scale, dy.device)
+    torch_checks_scale(weight_scale, dy.device)
+    dy = dy.contiguous()
+    weight = weight.contiguous()
+    m, n = dy.shape
+    k = weight.shape[1]
+    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    ws_bytes = _lib.query("dpa_conv2d_dgrad_workspace_bytes", k, n, 1, 1)
+    workspace = torch.empty(ws_bytes, device=dy.device, dtype=torch.uint8)
+    _lib.call(
+        "dpa_conv2d_dgrad_fp8",
+        dy.data_ptr(), weight.data_ptr(), dy_scale.data_ptr(), weight_scale.data_ptr(),
+        dx.data_ptr(), workspace.data_ptr(), ws_bytes, m, 1, 1, k, n, 1, 1, 1, 0, _stream(dy),
+    )
+    return dx
+
+
+def linear_fp8_wgrad_prequantized(
+    x: torch.Tensor,
+    dy: torch.Tensor,
+    x_scale: torch.Tensor,
+    dy_scale: torch.Tensor,
+) -> torch.Tensor:
+    """dw[N, K] = bf16(dy[M, N]^T @ x[M, K] * x_scale * dy_scale); e4m3 inputs.
+
+    Runs the 1x1 weight-gradient kernel on M one-pixel images."""
+    assert x.dtype == FP8_DTYPE and dy.dtype == FP8_DTYPE and x.ndim == dy.ndim == 2
+    assert x.shape[0] == dy.shape[0]
+    torch_checks_scale(x_scale, x.device)
+    torch_checks_scale(dy_scale, x.device)
+    x = x.contiguous()
+    dy = dy.contiguous()
+    m, k = x.shape
+    n = dy.shape[1]
+    ws_bytes = _lib.query("dpa_conv2d_wgrad_workspace_bytes", m, 1, 1, k, n, 1, 1, 1, 0, 0)
+    if ws_bytes <= 0:
+        raise RuntimeError(f"dpa_conv2d_wgrad_fp8: unsupported linear shape {(m, k, n)}")
+    workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    dw = torch.empty((n, k), device=x.device, dtype=torch.bfloat16)
+    _lib.call(
+        "dpa_conv2d_wgrad_fp8",
+        x.data_ptr(), dy.data_ptr(), x_scale.data_ptr(), dy_scale.data_ptr(), dw.data_ptr(),
+        workspace.data_ptr(), ws_bytes, m, 1, 1, k, n, 1, 1, 1, 0, 0, _stream(x),
+    )
+    return dw
+
+
+def linear_fp8_supported(in_features: int, out_features: int) -> bool:
+    """Feature counts the FP8 GEMM and its gradients implement (multiples of 128)."""
+    return in_features % 128 == 0 and out_features % 128 == 0 and in_features > 0
+
+
+class LinearFP8Function(torch.autograd.Function):
+    """y = x @ weight^T (+ bias) with current per-tensor e4m3 scaling of x, weight and dy.
+
+    Same recipe as the conv (diffusion/fp8_kernels.py:822-913) applied to the U-Net's
+    nn.Linear sites (diffusion/unet.py:101, :171-172, :189, :199): bf16 inputs, e4m3 saved
+    operands, bf16 output and gradients (autograd casts them to the parameter dtype)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None):
+        lead = x.shape[:-1]
+        n, k = weight.shape
+        assert x.shape[-1] == k
+        x2 = x.to(torch.bfloat16).reshape(-1, k).contiguous()
+        w = weight.to(torch.bfloat16).contiguous()
+        xq, xs = quantize_fp8_tensor(x2)
+        wq, wsc = quantize_fp8_tensor(w)
+        b32 = None if bias is None else bias.detach().float().contiguous()
+        y = linear_fp8_prequantized(xq, wq, xs, wsc, b32)
+        ctx.save_for_backward(xq, wq, xs, wsc)
+        ctx.lead = lead
+        ctx.has_bias = bias is not None
+        return y.reshape(*lead, n)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor):
+        xq, wq, xs, wsc = ctx.saved_tensors
+        n, k = wq.shape
+        dy2 = dy.to(torch.bfloat16).reshape(-1, n).contiguous()
+        dyq, dys = quantize_fp8_tensor(dy2)
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = linear_fp8_dgrad_prequantized(dyq, wq, dys, wsc).reshape(*ctx.lead, k)
+        if ctx.needs_input_grad[1]:
+            dw = linear_fp8_wgrad_prequantized(xq, dyq, xs, dys)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy2.float().sum(0)
+        return dx, dw, db
+
+
+def linear_fp8_autograd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    return LinearFP8Function.apply(x, weight, bias)

@@ -1,0 +1,111 @@
+"""Graph-captured single-GPU training step (train.py:104-149 of the reference).
+
+``prepare_cuda_graph`` keeps the reference's signature and order: three warm-up iterations on
+a side stream (which also lets every FP8 op and library kernel initialise outside the
+capture), then one capture of zero_grad / autocast forward / loss accumulation / backward /
+clip_grad_norm_ / AdamW / EMA. Replaying the returned graph is one training step. Every FP8
+launch goes to torch's current stream, which is the capture stream inside the graph, and all
+of their buffers come from torch's allocator (the graph's private pool).
+
+``TrainState`` bundles model, optimizer, diffusion wrapper, EMA and the static input buffers
+so a benchmark or test can build the reference's training setup in one call.
+"""
+from __future__ import annotations
+
+import torch
+
+from .ddpm import DiffusionWrapper, EWMAWrapper
+from .unet import UNet, UNetConfig
+
+
+def _one_step(ddpm: DiffusionWrapper, model: torch.nn.Module, ema_ddpm: DiffusionWrapper,
+              static_batch: torch.Tensor, optimizer: torch.optim.Optimizer,
+              loss_acc: torch.Tensor | None, static_t: torch.Tensor | None,
+              static_eps: torch.Tensor | None, max_norm: float) -> torch.Tensor:
+    optimizer.zero_grad(set_to_none=True)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        loss = ddpm.forward_batch(static_batch, static_t, static_eps)
+    if loss_acc is not None:
+        loss_acc.add_(loss.detach())
+    loss.backward()
+    torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=max_norm)
+    optimizer.step()
+    ema_ddpm.model.update(ddpm.model)
+    return loss
+
+
+def prepare_cuda_graph(ddpm: DiffusionWrapper, model: torch.nn.Module, ema_ddpm: DiffusionWrapper,
+                       static_batch: torch.Tensor, optimizer: torch.optim.Optimizer,
+                       loss_acc: torch.Tensor, static_t: torch.Tensor | None = None,
+                       static_eps: torch.Tensor | None = None, warmup: int = 3,
+                       max_norm: float = 1.0) -> torch.cuda.CUDAGraph:
+    """train.py:104-149. ``static_t`` / ``static_eps`` (optional) fix the timesteps and noise
+    instead of drawing them inside the graph."""
+    model.train()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            _one_step(ddpm, model, ema_ddpm, static_batch, optimizer, None, static_t, static_eps,
+                      max_norm)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    g = torch.cuda.CUDAGraph()
+    optimizer.zero_grad(set_to_none=True)
+    with torch.cuda.graph(g):
+        _one_step(ddpm, model, ema_ddpm, static_batch, optimizer, loss_acc, static_t, static_eps,
+                  max_norm)
+    return g
+
+
+class TrainState:
+    """Model + AdamW + DDPM + EMA with static input buffers (the reference's train.py setup:
+    channels-last model, fused capturable AdamW, EMA beta 0.9999)."""
+
+    def __init__(self, config: UNetConfig, batch: int, lr: float = 2e-4, max_t: int = 1000,
+                 schedule_type: str = "linear", ema_beta: float = 0.9999, device: str = "cuda",
+                 seed: int = 0, fixed_noise: bool = False):
+        torch.manual_seed(seed)
+        model = UNet(config).to(memory_format=torch.channels_last)
+        self.model = model.to(device)
+        self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=lr, fused=True,
+                                           capturable=True)
+        self.ddpm = DiffusionWrapper(self.model, schedule_type=schedule_type, max_t=max_t,
+                                     in_dim=config.in_resolution, device=device)
+        self.ema_ddpm = DiffusionWrapper(EWMAWrapper(self.model, beta=ema_beta),
+                                         schedule_type=schedule_type, max_t=max_t,
+                                         in_dim=config.in_resolution, device=device)
+        shape = (batch, config.in_channels, config.in_resolution, config.in_resolution)
+        self.static_batch = torch.empty(shape, device=device).contiguous(
+            memory_format=torch.channels_last)
+        self.static_t = torch.zeros(batch, dtype=torch.long, device=device) if fixed_noise else None
+        self.static_eps = (torch.zeros(shape, device=device).contiguous(
+            memory_format=torch.channels_last) if fixed_noise else None)
+        self.loss_acc = torch.zeros((), device=device)
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def set_batch(self, images: torch.Tensor, t: torch.Tensor | None = None,
+                  eps: torch.Tensor | None = None) -> None:
+        self.static_batch.copy_(images)
+        if t is not None:
+            assert self.static_t is not None
+            self.static_t.copy_(t)
+        if eps is not None:
+            assert self.static_eps is not None
+            self.static_eps.copy_(eps)
+
+    def eager_step(self) -> torch.Tensor:
+        self.model.train()
+        return _one_step(self.ddpm, self.model, self.ema_ddpm, self.static_batch, self.optimizer,
+                         self.loss_acc, self.static_t, self.static_eps, 1.0)
+
+    def capture(self, warmup: int = 3) -> torch.cuda.CUDAGraph:
+        self.graph = prepare_cuda_graph(self.ddpm, self.model, self.ema_ddpm, self.static_batch,
+                                        self.optimizer, self.loss_acc, self.static_t,
+                                        self.static_eps, warmup=warmup)
+        return self.graph
+
+    def replay(self) -> None:
+        assert self.graph is not None, "capture() first"
+        self.graph.replay()

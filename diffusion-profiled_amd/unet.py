@@ -1,0 +1,394 @@
+"""The DDPM U-Net of fattorib/diffusion-profiled on the gfx950 FP8 path.
+
+Module tree, parameter and buffer names, initialisation and forward arithmetic follow
+diffusion/unet.py, so a reference ``state_dict`` loads unchanged (and vice versa). What runs
+underneath differs:
+
+* ``Conv2dFP8`` (diffusion/unet.py:32-94): registry shapes go through ``triton_conv2d_fp8``
+  (the HIP kernels) with the same current/delayed scaling and window state machine; with
+  ``UNetConfig.fp8_all_convs`` the other 3x3 convs whose channels are multiples of 128 use
+  the general FP8 conv (current scaling) instead of the bf16 fallback.
+* GroupNorm + SiLU (diffusion/unet.py:151, :157-159, :380-384) and the FiLM ``(w + 1) * h + b``
+  run as one fused HIP kernel each way (``gn_silu``).
+* With ``UNetConfig.fp8_linears`` the bias-free linears (time MLP, FiLM projection, qkv, out)
+  and the 1x1 skip convs use the FP8 GEMM with current scaling.
+* Attention (diffusion/unet.py:181-203) is written out with batched products on dense
+  operands (no transposed views) and a float32 softmax.
+
+The torch ops around them (LayerNorm, interpolate, concat, the 3->128 and 128->3 convs whose
+channel counts the FP8 kernels do not take) stay in PyTorch-ROCm, as in the reference.
+"""
+from __future__ import annotations
+
+import math
+from collections import deque
+from dataclasses import asdict, dataclass
+from functools import partial
+from typing import Any
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import fp8_kernels as K
+from .gn_silu import group_norm_silu, supported as gn_supported
+
+
+@dataclass
+class UNetConfig:
+    """diffusion/unet.py:13-28, plus three switches for the fused/FP8 sites of this build."""
+
+    in_channels: int
+    base_hidden: int
+    scales: list[int]
+    n_heads: int
+    p_drop: float
+    attn_resolutions: list[int]
+    in_resolution: int
+    n_resblocks: int
+    fp8_convs_enabled: bool = False
+    fp8_scaling_type: str = "current"
+    fp8_amax_history: int = 1024
+    fp8_all_convs: bool = False
+    fp8_linears: bool = False
+    fused_gn_silu: bool = True
+
+    def as_dict(self):
+        return asdict(self)
+
+
+def _on_gpu(x: torch.Tensor) -> bool:
+    return x.is_cuda
+
+
+class Conv2dFP8(nn.Module):
+    """3x3 / stride 1 / pad 1 conv, FP8 when the shape allows (diffusion/unet.py:32-94)."""
+
+    def __init__(
+        self,
+        in_channels: int,
+        out_channels: int,
+        fp8_convs_enabled: bool,
+        scaling_type: str = "current",
+        amax_history: int | None = None,
+        fp8_all_convs: bool = False,
+    ):
+        super().__init__()
+        self.conv = nn.Conv2d(in_channels, out_channels, (3, 3), stride=1, padding=1, bias=False)
+        self.scaling_type = scaling_type
+        self.fp8_convs_enabled = fp8_convs_enabled
+        self.fp8_all_convs = fp8_all_convs
+        assert self.scaling_type in ["current", "delayed"]
+        if scaling_type == "delayed":
+            assert amax_history is not None
+            self.amax_history = amax_history
+            self.register_buffer("amax_window_weights", torch.zeros(amax_history))
+            self.register_buffer("amax_window_acts", torch.zeros(amax_history))
+            self.register_buffer("amax_window_dy", torch.zeros(amax_history))
+            self.register_buffer("window_pos", torch.zeros((), dtype=torch.long))
+
+    def conv_fp8(self, x: torch.Tensor, weight: torch.Tensor) -> bool:
+        """diffusion/unet.py:58-60: FP8 iff enabled and the shape is in the registry."""
+        shape = (x.shape[1], weight.shape[0], x.shape[2], x.shape[3])
+        return self.fp8_convs_enabled and shape in K.SUPPORTED_UNET_SHAPES
+
+    def conv_fp8_general(self, x: torch.Tensor, weight: torch.Tensor) -> bool:
+        return (self.fp8_convs_enabled and self.fp8_all_convs and x.shape[1] % 128 == 0
+                and weight.shape[0] % 128 == 0)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.conv_fp8(x, self.conv.weight):
+            x = x.contiguous(memory_format=torch.channels_last)
+            if self.scaling_type == "current":
+                return K.triton_conv2d_fp8(x, self.conv.weight)
+            with torch.no_grad():
+                x_scale_hist = torch.max(self.amax_window_acts)
+                w_scale_hist = torch.max(self.amax_window_weights)
+            out, x_scale_curr, w_scale_curr = K.triton_conv2d_fp8(
+                x, self.conv.weight, (x_scale_hist, w_scale_hist),
+                (self.amax_window_dy, self.window_pos), do_delayed=True,
+            )
+            with torch.no_grad():
+                window_idx = self.window_pos.unsqueeze(0)
+                self.amax_window_weights.scatter_(0, window_idx, w_scale_curr.detach().unsqueeze(0))
+                self.amax_window_acts.scatter_(0, window_idx, x_scale_curr.detach().unsqueeze(0))
+                self.window_pos.add_(1).remainder_(self.amax_history)
+            return out
+        if self.conv_fp8_general(x, self.conv.weight):
+            return K.conv2d_fp8(x, self.conv.weight, 1, 1)
+        return self.conv(x)
+
+
+class Conv1x1FP8(nn.Conv2d):
+    """The bias-free 1x1 skip projection (diffusion/unet.py:137-139) with an FP8 path; the
+    parameter is the nn.Conv2d ``weight`` so checkpoints are unchanged."""
+
+    def __init__(self, in_channels: int, out_channels: int, fp8: bool):
+        super().__init__(in_channels, out_channels, (1, 1), bias=False)
+        self.fp8 = fp8
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fp8 and _on_gpu(x) and self.in_channels % 128 == 0 and self.out_channels % 128 == 0:
+            return K.conv2d_fp8(x, self.weight, 1, 0)
+        return super().forward(x)
+
+
+class LinearFP8(nn.Linear):
+    """nn.Linear with the FP8 GEMM (forward and both gradients) when enabled and shaped for it."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, fp8: bool = False):
+        super().__init__(in_features, out_features, bias=bias)
+        self.fp8 = fp8
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fp8 and _on_gpu(x) and K.linear_fp8_supported(self.in_features, self.out_features):
+            return K.LinearFP8Function.apply(x, self.weight, self.bias)
+        return super().forward(x)
+
+
+def norm_silu(norm: nn.GroupNorm, x: torch.Tensor, fused: bool, film_scale=None, film_shift=None):
+    """silu(norm(x)) or silu(film_scale * norm(x) + film_shift); bf16 from the fused kernel."""
+    if fused and _on_gpu(x) and gn_supported(x.shape[1], norm.num_groups):
+        return group_norm_silu(x, norm.weight, norm.bias, norm.num_groups, norm.eps,
+                               film_scale, film_shift)
+    # autocast runs GroupNorm in float32 (diffusion/unet.py:151, :157); so does this path
+    h = norm(x.float() if x.dtype in (torch.bfloat16, torch.float16) else x)
+    if film_scale is not None:
+        h = film_scale * h + film_shift
+    return F.silu(h)
+
+
+class TimeEmbed(nn.Module):
+    """diffusion/unet.py:97-104."""
+
+    def __init__(self, embed_channels: int, channels: int, fp8: bool = False):
+        super().__init__()
+        self.mlp = LinearFP8(embed_channels, channels, bias=False, fp8=fp8)
+
+    def forward(self, t: torch.Tensor):
+        return self.mlp(t)[:, :, None, None]
+
+
+class ResidualBlock(nn.Module):
+    """diffusion/unet.py:107-161."""
+
+    def __init__(self, config: UNetConfig, in_chann: int, out_chann: int, p_drop: float = 0.0):
+        super().__init__()
+        conv = partial(Conv2dFP8, fp8_convs_enabled=config.fp8_convs_enabled,
+                       scaling_type=config.fp8_scaling_type, amax_history=config.fp8_amax_history,
+                       fp8_all_convs=config.fp8_all_convs)
+        self.conv_1 = conv(in_chann, out_chann)
+        self.conv_2 = conv(out_chann, out_chann)
+        self.norm1 = nn.GroupNorm(32, in_chann)
+        self.norm2 = nn.GroupNorm(32, out_chann)
+        self.t_embed_wb = TimeEmbed(4 * config.base_hidden, 2 * out_chann, fp8=config.fp8_linears)
+        self.skip_connection: nn.Module = nn.Identity()
+        if in_chann != out_chann:
+            self.skip_connection = Conv1x1FP8(in_chann, out_chann, fp8=config.fp8_linears)
+        self.dropout = nn.Dropout(p_drop)
+        self.fused = config.fused_gn_silu
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        torch.nn.init.zeros_(self.conv_2.conv.weight)
+
+    def forward(self, x: torch.Tensor, t: torch.Tensor):
+        resid = x
+        x = self.conv_1(norm_silu(self.norm1, x, self.fused))
+        wb = self.t_embed_wb(t)
+        w, b = torch.chunk(wb, chunks=2, dim=1)
+        h = norm_silu(self.norm2, x, self.fused, w + 1, b)
+        x = self.conv_2(self.dropout(h))
+        return (self.skip_connection(resid) + x) / math.sqrt(2.0)
+
+
+class _Attention(torch.autograd.Function):
+    """softmax(q k^T / sqrt(d)) v over [B*heads, L, d] with dense batched products only.
+
+    Every right operand handed to bmm is a contiguous tensor (the transposes are
+    materialised), and the softmax and its gradient run in float32."""
+
+    @staticmethod
+    def forward(ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        scale = 1.0 / math.sqrt(q.shape[-1])
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        s = torch.bmm(q, k.transpose(1, 2).contiguous()).float() * scale
+        p = torch.softmax(s, dim=-1)
+        pl = p.to(q.dtype)
+        o = torch.bmm(pl, v)
+        ctx.save_for_backward(q, k, v, pl)
+        ctx.scale = scale
+        return o
+
+    @staticmethod
+    def backward(ctx: Any, do: torch.Tensor):
+        q, k, v, pl = ctx.saved_tensors
+        do = do.to(q.dtype).contiguous()
+        dv = torch.bmm(pl.transpose(1, 2).contiguous(), do)
+        dp = torch.bmm(do, v.transpose(1, 2).contiguous()).float()
+        p = pl.float()
+        ds = (p * (dp - (dp * p).sum(-1, keepdim=True)) * ctx.scale).to(q.dtype)
+        dq = torch.bmm(ds, k)
+        dk = torch.bmm(ds.transpose(1, 2).contiguous(), q)
+        return dq, dk, dv
+
+
+class CHWAttention(nn.Module):
+    """diffusion/unet.py:164-203."""
+
+    def __init__(self, config: UNetConfig, hidden_size: int):
+        super().__init__()
+        self.config = config
+        self.nh = config.n_heads
+        self.qkv = LinearFP8(hidden_size, 3 * hidden_size, bias=False, fp8=config.fp8_linears)
+        self.out = LinearFP8(hidden_size, hidden_size, bias=False, fp8=config.fp8_linears)
+        self.norm = nn.LayerNorm(hidden_size)
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        torch.nn.init.zeros_(self.out.weight)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        resid = x
+        b, c, h, w = x.shape
+        seq = x.permute(0, 2, 3, 1).reshape(b, h * w, c)           # b (h w) c
+        seq = self.norm(seq)
+        qkv = self.qkv(seq)
+        q, k, v = torch.chunk(qkv, chunks=3, dim=-1)
+        hd = c // self.nh
+
+        def heads(t):                                              # b l (nh hd) -> (b nh) l hd
+            return t.reshape(b, h * w, self.nh, hd).transpose(1, 2).reshape(b * self.nh, h * w, hd)
+
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else q.dtype
+        o = _Attention.apply(heads(q).to(dt), heads(k).to(dt), heads(v).to(dt))
+        o = o.reshape(b, self.nh, h * w, hd).transpose(1, 2).reshape(b, h * w, c)
+        o = self.out(o)
+        out = o.reshape(b, h, w, c).permute(0, 3, 1, 2) + resid
+        return out / math.sqrt(2.0)
+
+
+class Stage(nn.Module):
+    """diffusion/unet.py:206-242."""
+
+    def __init__(self, config: UNetConfig, in_channels: int, hidden_channels: int,
+                 out_channels: int, attention: bool = False, num_blocks: int = 2):
+        super().__init__()
+        self.num_blocks = num_blocks
+        self.blocks = nn.ModuleList()
+        self.attns = nn.ModuleList()
+        self.blocks.append(ResidualBlock(config, in_channels, hidden_channels, p_drop=config.p_drop))
+        self.attns.append(CHWAttention(config, hidden_channels) if attention else nn.Identity())
+        for _ in range(num_blocks - 2):
+            self.blocks.append(ResidualBlock(config, hidden_channels, hidden_channels, p_drop=config.p_drop))
+            self.attns.append(CHWAttention(config, hidden_channels) if attention else nn.Identity())
+        self.blocks.append(ResidualBlock(config, hidden_channels, out_channels, p_drop=config.p_drop))
+        self.attns.append(CHWAttention(config, out_channels) if attention else nn.Identity())
+
+    def forward(self, x: torch.Tensor, t: torch.Tensor):
+        for block, attn in zip(self.blocks, self.attns):
+            x = block(x, t)
+            x = attn(x)
+        return x
+
+
+class _OutHead(nn.Sequential):
+    """GroupNorm(32) + SiLU + 3x3 conv to image channels (diffusion/unet.py:306-310); the
+    first two run as the fused kernel. Indices 0/1/2 keep the reference's state_dict keys."""
+
+    def __init__(self, channs: int, out_channels: int, fused: bool):
+        super().__init__(nn.GroupNorm(32, channs), nn.SiLU(),
+                         nn.Conv2d(channs, out_channels, kernel_size=(3, 3), padding=1, bias=False))
+        self.fused = fused
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self[2](norm_silu(self[0], x, self.fused))
+
+
+class UNet(nn.Module):
+    """diffusion/unet.py:245-388."""
+
+    def __init__(self, config: UNetConfig):
+        super().__init__()
+        self.config = config
+        self.base_channs = config.base_hidden
+        channs_1 = config.scales[0] * self.base_channs
+        self.conv_in = nn.Conv2d(config.in_channels, channs_1, kernel_size=(3, 3), padding=1, bias=False)
+
+        down_stages: deque = deque()
+        up_stages: deque = deque()
+        res = config.in_resolution
+        for i in range(0, len(config.scales) - 1):
+            chann_curr = self.base_channs * config.scales[i]
+            chann_next = self.base_channs * config.scales[i + 1]
+            do_attn = res in config.attn_resolutions
+            down_stages.append(Stage(config, chann_curr, chann_curr, chann_next, attention=do_attn,
+                                     num_blocks=config.n_resblocks))
+            up_stages.appendleft(Stage(config, chann_next + chann_next, chann_curr, chann_curr,
+                                       attention=do_attn, num_blocks=config.n_resblocks + 1))
+            res = res // 2
+
+        mid_stage = config.scales[-1] * self.base_channs
+        down_stages.append(Stage(config, mid_stage, mid_stage, mid_stage, num_blocks=config.n_resblocks))
+        up_stages.appendleft(Stage(config, mid_stage + mid_stage, mid_stage, mid_stage,
+                                   num_blocks=config.n_resblocks + 1))
+        # attention=True in the middle whatever attn_resolutions says, as in the reference
+        self.mid = Stage(config, mid_stage, mid_stage, mid_stage, attention=True,
+                         num_blocks=config.n_resblocks)
+        self.down_stages = nn.ModuleList(list(down_stages))
+        self.up_stages = nn.ModuleList(list(up_stages))
+
+        self.out = _OutHead(channs_1, self.config.in_channels, config.fused_gn_silu)
+        fp8_lin = config.fp8_linears
+        self.time_embed = nn.Sequential(
+            LinearFP8(self.base_channs, 4 * self.config.base_hidden, bias=False, fp8=fp8_lin),
+            nn.SiLU(),
+            LinearFP8(4 * self.config.base_hidden, 4 * self.config.base_hidden, bias=False, fp8=fp8_lin),
+            nn.SiLU(),
+        )
+        self.reset_parameters()
+        self.downsample = partial(F.interpolate, scale_factor=0.5, mode="nearest")
+        self.upsample = partial(F.interpolate, scale_factor=2.0, mode="nearest")
+        half = self.base_channs // 2
+        freqs = torch.exp(-torch.arange(half, dtype=torch.float32) * (math.log(10000.0) / half))
+        self.register_buffer("freqs", freqs, persistent=False)
+
+    def _timestep(self, t: torch.Tensor):
+        emb = t[:, None].float() * self.freqs[None]
+        emb = torch.cat([emb.sin(), emb.cos()], dim=1)
+        if self.base_channs % 2 == 1:
+            emb = F.pad(emb, (0, 1))
+        return emb
+
+    def reset_parameters(self):
+        assert isinstance(self.out[-1], nn.Conv2d)
+        torch.nn.init.zeros_(self.out[-1].weight)
+
+    def forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+        t_emb = self.time_embed(self._timestep(t))
+        act = self.conv_in(x)
+        hs = []
+        for i, stage in enumerate(self.down_stages):
+            act = stage(self.downsample(act) if i > 0 else act, t_emb)
+            hs.append(act)
+        act = self.mid(act, t_emb)
+        for i, stage in enumerate(self.up_stages):
+            h = hs.pop()
+            up = self.upsample(act) if i > 0 else act
+            act = stage(torch.concat([up, h], dim=1), t_emb)
+        return self.out(act)
+
+
+def cfg5_config(**overrides) -> UNetConfig:
+    """The benchmark U-Net as the reference trains and profiles it (train.py:220-233,
+    extra/profile_cuda_graph.py:121-133): ch 128, mults (1,2,2,2), 2 ResBlocks per level,
+    attention at 16x16 and 8x8 plus the middle stage, dropout 0.2, delayed scaling; here
+    every conv and linear whose channel counts are multiples of 128 runs in FP8."""
+    kw: dict[str, Any] = dict(
+        in_channels=3, base_hidden=128, scales=[1, 2, 2, 2], n_heads=4, p_drop=0.2,
+        attn_resolutions=[16, 8], in_resolution=32, n_resblocks=2, fp8_convs_enabled=True,
+        fp8_scaling_type="delayed", fp8_amax_history=1024, fp8_all_convs=True, fp8_linears=True,
+        fused_gn_silu=True,
+    )
+    kw.update(overrides)
+    return UNetConfig(**kw)

@@ -1,0 +1,246 @@
+"""GPU tests of the module level: the FP8 linear with both gradients, the delayed-scaling
+Conv2dFP8 module against the oracle's state machine, a ResidualBlock (cfg4) against the
+fake-quant emulation, and the graph-captured U-Net training step against eager steps.
+"""
+from __future__ import annotations
+
+import math
+import types
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import assert_bf16_close, bits, dpa_mod, kaiming_uniform_bf16, nhwc_bits, randn_bf16
+from fakequant import emulate
+from oracle import fp8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+K = dpa_mod("fp8_kernels")
+U = dpa_mod("unet")
+T = dpa_mod("trainer")
+
+
+def f32(t):
+    return np.float32(t.item())
+
+
+def nerr(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def test_linear_fp8_forward_and_gradients_vs_oracle():
+    """LinearFP8Function at cfg1's feature sizes (256 -> 768) with ragged rows: y, dx, dw
+    against the exact oracle on the operands the function quantized."""
+    m, k, n = 1000, 256, 768
+    x = randn_bf16((m, k), seed=0).cuda().requires_grad_()
+    w = kaiming_uniform_bf16((n, k), seed=1).float().cuda().requires_grad_()
+    dy = randn_bf16((m, n), seed=2, std=1e-2).cuda()
+    y = K.LinearFP8Function.apply(x, w, None)
+    y.backward(dy)
+    torch.cuda.synchronize()
+    xq, xs = O.quantize_fp8(bits(x.detach().cpu()))
+    wq, ws = O.quantize_fp8(bits(w.detach().to(torch.bfloat16).cpu()))
+    dyq, dys = O.quantize_fp8(bits(dy.cpu()))
+    assert y.dtype == torch.bfloat16 and x.grad.dtype == torch.bfloat16 and w.grad.dtype == torch.float32
+    assert_bf16_close(bits(y.detach().cpu()), O.gemm(xq, wq, xs, ws), "linear fwd")
+    assert_bf16_close(bits(x.grad.cpu()), O.gemm(dyq, np.ascontiguousarray(wq.T), dys, ws), "linear dx")
+    assert_bf16_close(bits(w.grad.to(torch.bfloat16).cpu()),
+                      O.gemm(np.ascontiguousarray(dyq.T), np.ascontiguousarray(xq.T), dys, xs),
+                      "linear dw")
+
+
+def test_conv_module_delayed_scaling_vs_oracle():
+    """Conv2dFP8 in delayed mode (diffusion/unet.py:69-91): after each fwd+bwd the three
+    windows and window_pos equal the oracle's state machine bit for bit, and from the second
+    step on y, dx, dw match the oracle conv run with the historical scales."""
+    torch.manual_seed(0)
+    mod = U.Conv2dFP8(128, 128, True, "delayed", amax_history=4).cuda()
+    st = O.DelayedScaling(history=4)
+    wb = bits(mod.conv.weight.detach().to(torch.bfloat16).permute(0, 2, 3, 1).contiguous().cpu())
+    for step in range(6):
+        x = randn_bf16((2, 128, 32, 32), seed=10 + step, std=0.5 + step)
+        dy = randn_bf16((2, 128, 32, 32), seed=20 + step, std=1e-2 * (step + 1))
+        xd = x.cuda().contiguous(memory_format=torch.channels_last).requires_grad_()
+        mod.conv.weight.grad = None
+        y = mod(xd)
+        y.backward(dy.cuda().contiguous(memory_format=torch.channels_last))
+        torch.cuda.synchronize()
+        xq, wq, xs_h, ws_h, _, _ = st.forward(nhwc_bits(x), wb)
+        dyq, dys_h, _ = st.backward(nhwc_bits(dy))
+        np.testing.assert_array_equal(mod.amax_window_acts.cpu().numpy(), st.win_acts)
+        np.testing.assert_array_equal(mod.amax_window_weights.cpu().numpy(), st.win_weights)
+        np.testing.assert_array_equal(mod.amax_window_dy.cpu().numpy(), st.win_dy)
+        assert int(mod.window_pos) == st.pos
+        if step == 0:
+            continue            # empty history: scale 0, outside the reference's contract
+        assert_bf16_close(nhwc_bits(y.detach().cpu()), O.conv2d_fwd(xq, wq, xs_h, ws_h), f"y {step}")
+        assert_bf16_close(nhwc_bits(xd.grad.cpu()), O.conv2d_dgrad(dyq, wq, dys_h, ws_h, (32, 32)),
+                          f"dx {step}")
+        dw = mod.conv.weight.grad.to(torch.bfloat16).permute(0, 2, 3, 1).contiguous().cpu()
+        assert_bf16_close(bits(dw), O.conv2d_wgrad(xq, dyq, xs_h, dys_h), f"dw {step}")
+
+
+def _cfg(**kw):
+    base = dict(fp8_scaling_type="current", p_drop=0.0)
+    base.update(kw)
+    return U.cfg5_config(**base)
+
+
+def test_resblock_cfg4_vs_fakequant_emulation():
+    """cfg4's block (GN+SiLU -> FP8 3x3 -> FiLM from the 512-d time embedding -> GN+SiLU ->
+    FP8 3x3 -> residual / sqrt 2) at 16x16, 256 channels, batch 8, plus a 128 -> 256 block
+    with the FP8 1x1 skip: output and gradients against the fake-quant emulation."""
+    for cin, cout, hw in ((256, 256, 16), (128, 256, 32)):
+        torch.manual_seed(cin)
+        blk = U.ResidualBlock(_cfg(), cin, cout).cuda().to(memory_format=torch.channels_last)
+        torch.nn.init.kaiming_uniform_(blk.conv_2.conv.weight, a=math.sqrt(5))   # not the zero init
+        with torch.no_grad():
+            blk.norm1.weight.uniform_(0.5, 1.5)
+            blk.norm2.bias.uniform_(-0.2, 0.2)
+        em = emulate(blk)
+        x = randn_bf16((8, cin, hw, hw), seed=1)
+        t = randn_bf16((8, 512), seed=2)
+        dout = randn_bf16((8, cout, hw, hw), seed=3, std=1e-2)
+
+        xg = x.cuda().contiguous(memory_format=torch.channels_last).requires_grad_()
+        tg = t.cuda().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = blk(xg, tg)
+        out.backward(dout.cuda().contiguous(memory_format=torch.channels_last))
+
+        xc = x.clone().requires_grad_()
+        tc = t.clone().requires_grad_()
+        ref = em(xc, tc)
+        ref.backward(dout)
+        torch.cuda.synchronize()
+
+        assert out.dtype == torch.bfloat16 and ref.dtype == torch.bfloat16
+        assert nerr(out, ref) < 1e-2, nerr(out, ref)
+        assert nerr(xg.grad, xc.grad) < 2e-2, nerr(xg.grad, xc.grad)
+        assert nerr(tg.grad, tc.grad) < 2e-2, nerr(tg.grad, tc.grad)
+        for (name, p), (_, q) in zip(blk.named_parameters(), em.named_parameters()):
+            assert p.grad is not None, name
+            assert nerr(p.grad, q.grad) < 3e-2, (name, nerr(p.grad, q.grad))
+
+
+def _state(batch, seed=0, **kw):
+    st = T.TrainState(_cfg(**kw), batch=batch, seed=seed, fixed_noise=True)
+    g = torch.Generator().manual_seed(4)
+    images = torch.rand((batch, 3, 32, 32), generator=g) * 2 - 1
+    t = torch.randint(0, 1000, (batch,), generator=g)
+    eps = torch.randn((batch, 3, 32, 32), generator=g)
+    st.set_batch(images.cuda(), t.cuda(), eps.cuda())
+    return st
+
+
+def test_graph_captured_step_matches_eager_steps():
+    """prepare_cuda_graph (train.py:104-149) on the full U-Net with delayed scaling: each
+    replay gives the loss and parameters of an eager step from the same state, with eager
+    work and synchronisation between replays."""
+    a = _state(4, fp8_scaling_type="delayed")
+    b = _state(4, fp8_scaling_type="delayed")
+    a.capture(warmup=3)                           # 3 eager warm-up steps, then capture
+    for _ in range(3):
+        b.eager_step()
+    torch.cuda.synchronize()
+    b.loss_acc.zero_()
+    a.loss_acc.zero_()
+    for i in range(3):
+        a.replay()
+        torch.cuda.synchronize()
+        b.eager_step()
+        torch.cuda.synchronize()
+        la, lb = float(a.loss_acc), float(b.loss_acc)
+        assert math.isfinite(la) and la == pytest.approx(lb, rel=1e-5), (i, la, lb)
+        for (name, p), q in zip(a.model.named_parameters(), b.model.parameters()):
+            torch.testing.assert_close(p, q, rtol=1e-4, atol=1e-6, msg=f"replay {i}: {name}")
+    for (name, p), q in zip(a.ema_ddpm.model.model.named_parameters(), b.ema_ddpm.model.model.parameters()):
+        torch.testing.assert_close(p, q, rtol=1e-4, atol=1e-6, msg=f"ema {name}")
+    for (name, buf), q in zip(a.model.named_buffers(), b.model.buffers()):
+        torch.testing.assert_close(buf, q, rtol=1e-5, atol=0, msg=name)
+
+
+def _conv_by_matmul(x: torch.Tensor, w: torch.Tensor, pad: int) -> torch.Tensor:
+    """bf16 conv (stride 1) as unfold + one 2-D GEMM, channels-last result."""
+    b, c, h, wd = x.shape
+    o, _, k, _ = w.shape
+    cols = F.unfold(x, k, padding=pad).transpose(1, 2).reshape(b * h * wd, c * k * k)
+    y = F.linear(cols, w.reshape(o, c * k * k))
+    return y.reshape(b, h, wd, o).permute(0, 3, 1, 2)
+
+
+def _bf16_reference(model: torch.nn.Module) -> torch.nn.Module:
+    """The same U-Net with every FP8 site in plain bf16 autocast arithmetic: 3x3 and 1x1
+    convs as unfold + GEMM, the linears as nn.Linear."""
+    for m in model.modules():
+        if isinstance(m, U.Conv2dFP8):
+            m.forward = types.MethodType(lambda self, x: _conv_by_matmul(x, self.conv.weight, 1), m)
+        elif isinstance(m, U.Conv1x1FP8):
+            m.forward = types.MethodType(lambda self, x: _conv_by_matmul(x, self.weight, 0), m)
+        elif isinstance(m, U.LinearFP8):
+            m.fp8 = False
+    return model
+
+
+def _smooth_images(n: int, seed: int) -> torch.Tensor:
+    """Synthetic images in [-1, 1] with spatial structure: bilinear upsampling of random 4x4
+    colour fields (something a denoiser can learn, unlike i.i.d. pixels)."""
+    g = torch.Generator().manual_seed(seed)
+    low = torch.rand((n, 3, 4, 4), generator=g) * 2 - 1
+    return F.interpolate(low, size=(32, 32), mode="bilinear", align_corners=False).clamp(-1, 1)
+
+
+def test_unet_loss_tracks_bf16_over_training():
+    """The FP8 U-Net (graph-captured) against the same model in bf16: same initialisation,
+    same images, timesteps and noise at every step, 1000 steps at batch 16, losses averaged
+    over windows of 100 steps.
+
+    * current scaling tracks bf16: every window within 15 %, windows 2-10 within 5 % on
+      average;
+    * delayed scaling with a 16-slot window stays closer to bf16 than with 1024 slots in every
+      window after the first (measured: ~13 % above bf16);
+    * delayed scaling with the reference's 1024-slot window (diffusion/unet.py:25) learns
+      but trails: the loss falls ~10x in the first 100 steps, and the maximum over the
+      window keeps the large early dy scales for 1024 steps, so small gradients lose their
+      mantissa bits in e4m3. The same state machine behaves the same way in the reference.
+    """
+    steps, batch, window = 1000, 16, 100
+    images = _smooth_images(64, seed=4).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    t_all = torch.randint(0, 1000, (steps, batch), device="cuda", generator=gen)
+    eps_all = torch.randn((steps, batch, 3, 32, 32), device="cuda", generator=gen)
+    curves = {}
+    for name in ("fp8-current", "fp8-delayed-h16", "fp8-delayed", "bf16"):
+        scaling = "current" if name == "fp8-current" else "delayed"
+        hist = 16 if name.endswith("h16") else 1024
+        st = T.TrainState(_cfg(fp8_scaling_type=scaling, fp8_amax_history=hist), batch=batch,
+                          seed=0, fixed_noise=True)
+        if name == "bf16":
+            _bf16_reference(st.model)
+        st.set_batch(images[:batch], t_all[0], eps_all[0])
+        st.capture(warmup=3)
+        losses = torch.zeros(steps, device="cuda")
+        for i in range(steps):
+            j = (i * batch) % images.shape[0]
+            st.set_batch(images[j:j + batch], t_all[i], eps_all[i])
+            st.loss_acc.zero_()
+            st.replay()
+            losses[i].copy_(st.loss_acc)
+        curves[name] = losses.cpu().numpy().reshape(-1, window).mean(axis=1)
+        print(f"loss curve {name}: window means " + " ".join(f"{m:.4f}" for m in curves[name]),
+              flush=True)
+        assert np.isfinite(curves[name]).all(), name
+        del st
+    bf = curves["bf16"]
+    assert bf[-1] < 0.2 * bf[0]
+    rel = {k: np.abs(v - bf) / bf for k, v in curves.items()}
+    assert rel["fp8-current"].max() <= 0.15, rel["fp8-current"]
+    assert rel["fp8-current"][1:].mean() <= 0.05, rel["fp8-current"]
+    # the window length is what separates delayed from current scaling
+    assert (rel["fp8-delayed-h16"][1:] < rel["fp8-delayed"][1:]).all(), rel
+    assert rel["fp8-delayed-h16"][1:].mean() <= 0.2, rel["fp8-delayed-h16"]
+    assert curves["fp8-delayed"][-1] < 0.5 * curves["fp8-delayed"][0]
