@@ -171,6 +171,44 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t 
 }
 
 // ---------------------------------------------------------------------------------------
+// Global -> LDS DMA and the explicit waits that pipeline it.
+// ---------------------------------------------------------------------------------------
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// 16-B-per-lane global -> LDS DMA (lane i lands at lds + 16 i). Issued through inline asm so
+// the compiler does not guard later LDS reads with conservative vmcnt(0) waits: all waits for
+// these DMAs are explicit in-order vmcnt counts in the kernels that issue them (in-order counting
+// keeps every compiler-inserted wait conservative, hence correct).
+__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(lds));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "m0");
+}
+
+// Same DMA with the LDS destination given as a 32-bit LDS address (wave-uniform).
+__device__ __forceinline__ void dma16_lds(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
+}
+
+// 32-bit LDS address of a __shared__ object (no generic-pointer null check).
+#define LDS_ADDR(obj) ((uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t*)(obj)))
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt | lgkmcnt | vmcnt[5:4]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Workgroup barrier that the compiler may not move memory operations across (the DMA
+// writes above are invisible to it).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------------------
 // Integer division by a launch-time constant without the ~40-instruction runtime divide.
 // ---------------------------------------------------------------------------------------
 // x / d for 0 <= x < 2^31 via a precomputed (magic, shift) pair (Granlund-Montgomery).

@@ -27,7 +27,9 @@ struct GnArgs {
   uint16_t* out;
   float* mean;
   float* rstd;
-  float* part;  // bwd: [4][N][C] per-image channel sums
+  float* part;  // bwd: [2][N][C] per-image channel sums of dgamma / dbeta
+  float* dfs;   // bwd: FiLM gradients [N][C] or null
+  float* dfb;
   int N, HW, C, G, cpg;
   float eps;
 };
@@ -252,8 +254,10 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
       const int64_t o = (int64_t)n * p.C + ch + e;
       p.part[0 * nc + o] = acc[1][e];  // dgamma partial
       p.part[1 * nc + o] = acc[0][e];  // dbeta partial
-      p.part[2 * nc + o] = acc[2][e];  // dfilm scale
-      p.part[3 * nc + o] = acc[3][e];  // dfilm shift
+      if (p.dfs) {                      // FiLM gradients are per image: final here
+        p.dfs[o] = acc[2][e];
+        p.dfb[o] = acc[3][e];
+      }
     }
     // group sums of gxh = gz*gamma and gxh*xhat, per 4-channel half
     float h1[2] = {0.f, 0.f}, h2[2] = {0.f, 0.f};
@@ -303,28 +307,33 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
   }
 }
 
-// dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c]; FiLM partials are the
-// per-image results already and are copied out.
+// dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c], summed in image order
+// within each of 4 interleaved slices, then over the slices (deterministic). One workgroup
+// per 64 channels: 64 channel lanes x 4 image slices.
 __global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __restrict__ part,
                                                               float* __restrict__ dgamma,
-                                                              float* __restrict__ dbeta,
-                                                              float* __restrict__ dfs,
-                                                              float* __restrict__ dfb, int N,
+                                                              float* __restrict__ dbeta, int N,
                                                               int C) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
+  __shared__ float red[2][4][64];
+  const int lane = threadIdx.x & 63;
+  const int slice = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
   const int64_t nc = (int64_t)N * C;
   float sg = 0.f, sb = 0.f;
-  for (int n = 0; n < N; ++n) {
-    sg += part[(int64_t)n * C + c];
-    sb += part[nc + (int64_t)n * C + c];
-    if (dfs) {
-      dfs[(int64_t)n * C + c] = part[2 * nc + (int64_t)n * C + c];
-      dfb[(int64_t)n * C + c] = part[3 * nc + (int64_t)n * C + c];
+  if (c < C) {
+#pragma unroll 8
+    for (int n = slice; n < N; n += 4) {
+      sg += part[(int64_t)n * C + c];
+      sb += part[nc + (int64_t)n * C + c];
     }
   }
-  dgamma[c] = sg;
-  dbeta[c] = sb;
+  red[0][slice][lane] = sg;
+  red[1][slice][lane] = sb;
+  __syncthreads();
+  if (slice == 0 && c < C) {
+    dgamma[c] = (red[0][0][lane] + red[0][1][lane]) + (red[0][2][lane] + red[0][3][lane]);
+    dbeta[c] = (red[1][0][lane] + red[1][1][lane]) + (red[1][2][lane] + red[1][3][lane]);
+  }
 }
 
 static bool gn_shape_ok(int N, int HW, int C, int G) {
@@ -364,7 +373,7 @@ extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const flo
 extern "C" int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G) {
   (void)HW;
   (void)G;
-  return (int64_t)4 * N * C * 4;
+  return (int64_t)2 * N * C * 4;
 }
 
 extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
@@ -394,14 +403,15 @@ extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float
   a.mean = const_cast<float*>(mean);
   a.rstd = const_cast<float*>(rstd);
   a.part = (float*)workspace;
+  a.dfs = film_scale ? dfilm_scale : nullptr;
+  a.dfb = film_scale ? dfilm_shift : nullptr;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
   gn_silu_bwd_kernel<<<grid, kGnThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
-  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 256), 256, 0, s>>>(
-      (const float*)workspace, dgamma, dbeta, film_scale ? dfilm_scale : nullptr,
-      film_scale ? dfilm_shift : nullptr, N, C);
+  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 256, 0, s>>>((const float*)workspace,
+                                                                    dgamma, dbeta, N, C);
   return launch_status();
 }

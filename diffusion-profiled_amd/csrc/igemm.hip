@@ -78,25 +78,6 @@ __shared__ __attribute__((aligned(1024))) uint8_t ig_slot[kWaves][kSlotBytes];
 // reads of ds_read_b128 conflict-free, where (r & 7) or ((r >> 1) & 7) cost 2 passes.
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-
-// 16-B-per-lane global -> LDS DMA (lane i lands at lds + 16 i). Issued through inline asm so
-// the compiler does not guard later LDS reads with conservative vmcnt(0) waits: all waits for
-// these DMAs are the explicit in-order vmcnt counts of the pipeline below (in-order counting
-// keeps every compiler-inserted wait conservative, hence correct).
-__device__ __forceinline__ void dma16(const void* src, const void* lds) {
-  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(lds));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "m0");
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt | lgkmcnt | vmcnt[5:4]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
-
 #ifdef DPA_IG_PROBE
 __device__ unsigned long long g_ig_probe[4096 * 16];
 #define IG_STAMP(slot)                                                                   \

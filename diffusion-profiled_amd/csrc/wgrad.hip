@@ -13,8 +13,10 @@
 // formed with ds_read_b64_tr_b8: a 16-lane group pointing at an 8-pixel x 16-channel block
 // receives, in lane j, the 8 pixels of channel j. No transposed copy touches HBM or VALU.
 //
-// Workgroup tile: 128 input channels x 128 output channels of one tap; 4 waves (2 x 2) of
-// 64 x 64. Pixels are split over workgroups (split-K), ordered so the workgroups that read
+// Workgroup tile: 128 input channels x 128 output channels of one tap. Four consumer waves
+// (2 x 2 of 64 x 64) run the MFMAs; four producer waves compute the DMA addresses and issue
+// the DMAs into a 4-deep LDS ring, so address arithmetic overlaps the matrix pipe on every
+// SIMD. Pixels are split over workgroups (split-K), ordered so the workgroups that read
 // one pixel range (all taps and channel tiles) share an XCD and its L2. Every split writes
 // an fp32 partial tile (through LDS, as contiguous 512-B rows); the reduce kernel sums the
 // splits in index order, scales by RN32(sx * sdy) and rounds to bf16.
@@ -22,23 +24,25 @@
 
 namespace dpa {
 
-constexpr int kWgThreads = 256;
+constexpr int kWgConsumers = 256;                  // 4 MFMA waves (2 x 2 of 64 x 64)
+constexpr int kWgProducers = 256;                  // 4 DMA waves
+constexpr int kWgThreads = kWgConsumers + kWgProducers;
 constexpr int kWgTile = 128;                       // channels per tile side, pixels per K-step
 constexpr int kWgOperandBytes = kWgTile * kWgTile;  // 16 KB
 constexpr int kWgStageBytes = 2 * kWgOperandBytes;  // x block then dy block
-constexpr int kWgLoads = kWgOperandBytes / 16 / kWgThreads;  // 4 DMA per operand per thread
+constexpr int kWgLoads = kWgOperandBytes / 16 / kWgProducers;  // 4 DMA per operand per producer
 constexpr int kWgPPitch = kWgTile * 4 + 16;  // fp32 partial-tile row pitch in LDS (bytes)
 
-__shared__ __attribute__((aligned(1024))) uint8_t wg_smem[3 * kWgStageBytes];
-static_assert(kWgTile * kWgPPitch <= 3 * kWgStageBytes, "partial tile must fit in LDS");
+constexpr int kWgStages = 4;                         // LDS ring depth (DMA latency budget)
+
+__shared__ __attribute__((aligned(1024))) uint8_t wg_smem[kWgStages * kWgStageBytes];
+static_assert(kWgTile * kWgPPitch <= kWgStages * kWgStageBytes, "partial tile must fit in LDS");
 
 __device__ __attribute__((aligned(64))) uint8_t wg_zero16[64];
 
 // Row r (a pixel, 128 B) keeps its 16-B granule g at g ^ wswz(r): conflict-free for the
 // transpose reads (8 rows per 16-lane group, 4 groups at row offsets of 32).
 __device__ __forceinline__ int wswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
-
-#define WG_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
 struct WgradArgs {
   const uint8_t* x;   // [N][H][W][Cin]
@@ -48,48 +52,28 @@ struct WgradArgs {
   int npix, nchunks, splits;
   int ci_tiles, co_tiles, taps;
   int total, per_xcd;
+  int dq, dpp;              // one chunk (kWgTile pixels) as a (p, q) increment (+ images)
+  int x_step, x_cq, x_cp;   // x byte-offset change per chunk, and on a q / p wrap
   FastDiv divQ, divP;
 };
 
-template <int ST>
-__device__ __forceinline__ void wg_issue(const WgradArgs& p, int chunk, int ci0, int co0, int kr,
-                                         int ks, int wave, int lane) {
-  uint8_t* st = wg_smem + ST * kWgStageBytes;
-#pragma unroll
-  for (int j = 0; j < kWgLoads; ++j) {
-    const int row = wave * 32 + 8 * j + (lane >> 3);
-    const int g = (lane & 7) ^ wswz(row);
-    const int pix = chunk * kWgTile + row;
-    const uint8_t* xs = wg_zero16;
-    const uint8_t* ds = wg_zero16;
-    if (pix < p.npix) {
-      ds = p.dy + (uint32_t)(pix * p.Cout + co0 + g * 16);
-      const uint32_t t = fdiv((uint32_t)pix, p.divQ);
-      const int q = pix - (int)t * p.Q;
-      const uint32_t n = fdiv(t, p.divP);
-      const int pp = (int)t - (int)n * p.P;
-      const int ih = pp * p.stride + kr - p.pad;
-      const int iw = q * p.stride + ks - p.pad;
-      if ((unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W)
-        xs = p.x + (uint32_t)((((int)n * p.H + ih) * p.W + iw) * p.Cin + ci0 + g * 16);
-    }
-    __builtin_amdgcn_global_load_lds(xs, WG_LDS(st + (wave * 32 + 8 * j) * kWgTile), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(ds, WG_LDS(st + kWgOperandBytes + (wave * 32 + 8 * j) * kWgTile),
-                                     16, 0, 0);
-  }
-}
+constexpr int kWgLoadsPerStage = 2 * kWgLoads;  // x and dy DMAs per producer thread per stage
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-// 32 pixels (K) x 1 channel per lane: lane l -> channel row (l & 15) of the 16-channel
-// group starting at granule G, pixels [32*(l>>4), +32), via four 8-pixel transpose reads.
-__device__ __forceinline__ v8i ld_frag_tr(const uint8_t* base, int G, int lane) {
-  const int k = lane & 15, q = lane >> 4;
+// Transpose-read address tables. With k = lane & 15, q = lane >> 4, m = k >> 1, h = k & 1,
+// fragment read s of granule G touches LDS row r = 32q + 8s + m at granule position
+// G ^ wswz(r), and wswz(r) = L ^ C(s) with L = (m >> 1) ^ 2q (lane) and
+// C(s) = ((s & 1) << 2) ^ (s >> 1). So the byte offset is T[G ^ C(s)] + 1024 s with
+// T[v] = (32q + m) * 128 + 8h + 16 (v ^ L): eight per-lane values, and every read of the
+// loop is one of them plus an immediate.
+__device__ __forceinline__ constexpr int wg_c(int s) { return ((s & 1) << 2) ^ (s >> 1); }
+
+__device__ __forceinline__ v8i ld_frag_tbl(const uint8_t* stage_op, const uint32_t (&T)[8], int i) {
   v8i f;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const int row = 32 * q + 8 * s + (k >> 1);
-    const uint8_t* a = base + row * kWgTile + ((G ^ wswz(row)) * 16) + 8 * (k & 1);
+    const uint8_t* a = stage_op + T[i ^ wg_c(s)] + 1024 * s;
     const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
         (v2i __attribute__((address_space(3)))*)(a));
     f[2 * s] = v.x;
@@ -98,29 +82,82 @@ __device__ __forceinline__ v8i ld_frag_tr(const uint8_t* base, int G, int lane) 
   return f;
 }
 
+// Per-thread DMA state: 4 LDS rows (pixels) of the current chunk, advanced one chunk per issue.
+struct WgRows {
+  int pix[kWgLoads], rp[kWgLoads], rq[kWgLoads], xo[kWgLoads];
+  uint32_t dyo[kWgLoads];
+};
+
 template <int ST>
-__device__ __forceinline__ void wg_step(const WgradArgs& p, int c, int c_end, int ci0, int co0,
-                                        int kr, int ks, int wave, int lane, int wc, int wo,
-                                        v4f (&acc)[4][4]) {
-  __syncthreads();  // this stage's DMA landed (the fence waits for it) and is visible to all
-  const uint8_t* sx = wg_smem + ST * kWgStageBytes;
-  const uint8_t* sd = sx + kWgOperandBytes;
-  v8i xf[4], df[4];
+__device__ __forceinline__ void wg_issue(const WgradArgs& p, WgRows& r, bool live_step, int kr,
+                                         int ks, uint32_t lds_wave, uint32_t dy_step) {
+  const uint32_t st = LDS_ADDR(wg_smem) + ST * kWgStageBytes + lds_wave;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xf[i] = ld_frag_tr(sx, wc * 4 + i, lane);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) df[i] = ld_frag_tr(sd, wo * 4 + i, lane);
-  if (c + 2 < c_end) wg_issue<(ST + 2) % 3>(p, c + 2, ci0, co0, kr, ks, wave, lane);
-  // D rows = input channels, D cols = output channels
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xf[i], df[j], acc[i][j]);
+  for (int j = 0; j < kWgLoads; ++j) {
+    // bitwise & (not &&): no short-circuit branches, only selects
+    const bool live = live_step & (r.pix[j] < p.npix);
+    const int ih = r.rp[j] * p.stride + kr - p.pad;
+    const int iw = r.rq[j] * p.stride + ks - p.pad;
+    const bool ok = live & ((unsigned)ih < (unsigned)p.H) & ((unsigned)iw < (unsigned)p.W);
+    const uint8_t* xs = ok ? p.x + r.xo[j] : wg_zero16;
+    const uint8_t* ds = live ? p.dy + r.dyo[j] : wg_zero16;
+    dma16_lds(xs, st + 8 * j * kWgTile);
+    dma16_lds(ds, st + kWgOperandBytes + 8 * j * kWgTile);
+    // next chunk: (p, q) += (dpp, dq) with carries; x offset follows
+    int q = r.rq[j] + p.dq;
+    const bool cq = q >= p.Q;
+    q = cq ? q - p.Q : q;
+    int pp = r.rp[j] + p.dpp + (cq ? 1 : 0);
+    const bool cp = pp >= p.P;
+    pp = cp ? pp - p.P : pp;
+    r.rq[j] = q;
+    r.rp[j] = pp;
+    r.xo[j] += p.x_step + (cq ? p.x_cq : 0) + (cp ? p.x_cp : 0);
+    r.dyo[j] += dy_step;
+    r.pix[j] += kWgTile;
+  }
 }
 
+// Consumer step s (stage ST = s % kWgStages): barrier (the producers have waited for stage
+// s+1's DMAs, and every consumer wave holds stage s's fragments in registers), then 16 MFMAs
+// per wave on stage s while reading stage s+1's fragments.
+template <int ST>
+__device__ __forceinline__ void wg_consume(const uint32_t (&Tx)[8], const uint32_t (&Td)[8],
+                                           v8i (&xf)[4], v8i (&df)[4], v4f (&acc)[4][4]) {
+  constexpr int NX = (ST + 1) % kWgStages;
+  wait_lgkmcnt0();
+  lds_barrier();
+  const uint8_t* nx = wg_smem + NX * kWgStageBytes;
+  // D rows = input channels, D cols = output channels
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xf[i], df[j], acc[i][j]);
+    xf[i] = ld_frag_tbl(nx, Tx, i);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // then 4 DS reads
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) df[j] = ld_frag_tbl(nx + kWgOperandBytes, Td, j);
+}
+
+// Producer step s: wait until stage s+1 has landed (stages s+2 .. s+kWgStages-1 may still be
+// in flight), barrier, then queue stage s+kWgStages into buffer ST, which every consumer
+// finished reading before this barrier.
+template <int ST>
+__device__ __forceinline__ void wg_produce(const WgradArgs& p, WgRows& r, int s, int nsteps,
+                                           int kr, int ks, uint32_t lds_wave, uint32_t dy_step) {
+  wait_vmcnt<(kWgStages - 2) * kWgLoadsPerStage>();
+  lds_barrier();
+  wg_issue<ST>(p, r, s + kWgStages < nsteps, kr, ks, lds_wave, dy_step);
+}
+
+// One workgroup: one (split, tap, ci tile, co tile); K-steps walk the split's chunks of
+// kWgTile pixels through a kWgStages-deep LDS ring. Waves 0-3 run the MFMAs, waves 4-7 the
+// address arithmetic and DMAs, so the two overlap on every SIMD.
 __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const WgradArgs p) {
   // XCD-aware order: logical workgroup index = split-major, so the workgroups reading one
-  // pixel range are consecutive and land on the same XCD (hardware deals round-robin).
+  // pixel range (all taps and channel tiles) are consecutive and land on the same XCD.
   const int logical = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
   if (logical >= p.total) return;
   const int per_split = p.ci_tiles * p.co_tiles * p.taps;
@@ -133,44 +170,105 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
   const int kr = tap / p.S, ks = tap - (tap / p.S) * p.S;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wc = wave & 1;   // input-channel half (D rows)
-  const int wo = wave >> 1;  // output-channel half (D cols)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   const int c_begin = (int)(((int64_t)p.nchunks * split) / p.splits);
   const int c_end = (int)(((int64_t)p.nchunks * (split + 1)) / p.splits);
+  const int nsteps = c_end - c_begin;
+  static_assert(kWgStages == 4, "prologue and loops below are written for 4 stages");
 
   v4f acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int wc = wave & 1;         // consumers: input-channel half (D rows)
+  const int wo = (wave >> 1) & 1;  // consumers: output-channel half (D cols)
 
-  if (c_begin < c_end) wg_issue<0>(p, c_begin, ci0, co0, kr, ks, wave, lane);
-  if (c_begin + 1 < c_end) wg_issue<1>(p, c_begin + 1, ci0, co0, kr, ks, wave, lane);
-  for (int c = c_begin; c < c_end; c += 3) {
-    wg_step<0>(p, c, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
-    if (c + 1 < c_end) wg_step<1>(p, c + 1, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
-    if (c + 2 < c_end) wg_step<2>(p, c + 2, c_end, ci0, co0, kr, ks, wave, lane, wc, wo, acc);
+  if (wave >= 4) {
+    // ---------------- producers ----------------
+    const int pw = wave - 4;
+    WgRows r;
+#pragma unroll
+    for (int j = 0; j < kWgLoads; ++j) {
+      const int row = pw * 32 + 8 * j + (lane >> 3);
+      const int g = (lane & 7) ^ wswz(row);  // pre-swizzled granule for this LDS row
+      const uint32_t pix = (uint32_t)(c_begin * kWgTile + row);
+      const uint32_t t = fdiv(pix, p.divQ);
+      const int q = (int)(pix - t * (uint32_t)p.Q);
+      const uint32_t n = fdiv(t, p.divP);
+      const int pp = (int)(t - n * (uint32_t)p.P);
+      r.pix[j] = (int)pix;
+      r.rq[j] = q;
+      r.rp[j] = pp;
+      r.xo[j] = ((((int)n * p.H + pp * p.stride + kr - p.pad) * p.W + q * p.stride + ks - p.pad) *
+                 p.Cin) + ci0 + g * 16;
+      r.dyo[j] = pix * (uint32_t)p.Cout + (uint32_t)(co0 + g * 16);
+    }
+    const uint32_t dy_step = (uint32_t)kWgTile * (uint32_t)p.Cout;
+    const uint32_t lds_wave = (uint32_t)(pw * 32 * kWgTile);
+    wg_issue<0>(p, r, 0 < nsteps, kr, ks, lds_wave, dy_step);
+    wg_issue<1>(p, r, 1 < nsteps, kr, ks, lds_wave, dy_step);
+    wg_issue<2>(p, r, 2 < nsteps, kr, ks, lds_wave, dy_step);
+    wg_issue<3>(p, r, 3 < nsteps, kr, ks, lds_wave, dy_step);
+    wait_vmcnt<(kWgStages - 1) * kWgLoadsPerStage>();  // stage 0 landed
+    lds_barrier();
+    for (int s = 0; s < nsteps; s += 4) {
+      wg_produce<0>(p, r, s, nsteps, kr, ks, lds_wave, dy_step);
+      if (s + 1 < nsteps) wg_produce<1>(p, r, s + 1, nsteps, kr, ks, lds_wave, dy_step);
+      if (s + 2 < nsteps) wg_produce<2>(p, r, s + 2, nsteps, kr, ks, lds_wave, dy_step);
+      if (s + 3 < nsteps) wg_produce<3>(p, r, s + 3, nsteps, kr, ks, lds_wave, dy_step);
+    }
+    wait_vmcnt<0>();  // trailing DMAs land before LDS is reused
+    lds_barrier();
+  } else {
+    // ---------------- consumers ----------------
+    uint32_t Tx[8], Td[8];
+    {
+      const int k = lane & 15, q = lane >> 4, m = k >> 1;
+      const int L = (m >> 1) ^ (2 * q);
+      const uint32_t lb = (uint32_t)((32 * q + m) * kWgTile + 8 * (k & 1));
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        Tx[u] = lb + 16u * (uint32_t)((u ^ (4 * wc)) ^ L);
+        Td[u] = lb + 16u * (uint32_t)((u ^ (4 * wo)) ^ L);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    lds_barrier();  // stage 0 landed
+    v8i xf[4], df[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xf[i] = ld_frag_tbl(wg_smem, Tx, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) df[j] = ld_frag_tbl(wg_smem + kWgOperandBytes, Td, j);
+    for (int s = 0; s < nsteps; s += 4) {
+      wg_consume<0>(Tx, Td, xf, df, acc);
+      if (s + 1 < nsteps) wg_consume<1>(Tx, Td, xf, df, acc);
+      if (s + 2 < nsteps) wg_consume<2>(Tx, Td, xf, df, acc);
+      if (s + 3 < nsteps) wg_consume<3>(Tx, Td, xf, df, acc);
+    }
+    wait_lgkmcnt0();
+    lds_barrier();  // pairs with the producers' final barrier
   }
 
-  // partial[split][co][tap*Cin + ci]: stage [co][ci] fp32 in LDS, then 512-B row stores
-  __syncthreads();
-  const int frow = lane & 15, fq = lane >> 4;
+  // partial[split][co][tap*Cin + ci]: consumers stage [co][ci] fp32 in LDS, then all eight
+  // waves store contiguous 512-B rows
+  if (wave < 4) {
+    const int frow = lane & 15, fq = lane >> 4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int co = wo * 64 + j * 16 + frow;
+    for (int j = 0; j < 4; ++j) {
+      const int co = wo * 64 + j * 16 + frow;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ci = wc * 64 + i * 16 + 4 * fq;
-      *reinterpret_cast<v4f*>(wg_smem + co * kWgPPitch + ci * 4) = acc[i][j];
+      for (int i = 0; i < 4; ++i) {
+        const int ci = wc * 64 + i * 16 + 4 * fq;
+        *reinterpret_cast<v4f*>(wg_smem + co * kWgPPitch + ci * 4) = acc[i][j];
+      }
     }
   }
   __syncthreads();
   const int64_t kk = (int64_t)p.taps * p.Cin;
   float* base = p.partial + (int64_t)split * p.Cout * kk + (int64_t)tap * p.Cin + ci0;
   constexpr int kChunks = kWgTile * 4 / 16;            // 32 x 16 B per co row
-  constexpr int kRowsPerPass = kWgThreads / kChunks;  // 8
+  constexpr int kRowsPerPass = kWgThreads / kChunks;  // 16
   const int ch = threadIdx.x % kChunks;
 #pragma unroll 4
   for (int r0 = 0; r0 < kWgTile; r0 += kRowsPerPass) {
@@ -278,6 +376,15 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   a.per_xcd = (int)ceil_div(a.total, 8);
   a.divQ = make_fastdiv((uint32_t)pl.Q);
   a.divP = make_fastdiv((uint32_t)pl.P);
+  {
+    // one chunk of kWgTile pixels = dn images + dpp rows + dq columns
+    const int dq = kWgTile % pl.Q, dpp = (kWgTile / pl.Q) % pl.P, dn = kWgTile / (pl.Q * pl.P);
+    a.dq = dq;
+    a.dpp = dpp;
+    a.x_step = ((dn * H + dpp * stride) * W + dq * stride) * Cin;
+    a.x_cq = (stride * W - pl.Q * stride) * Cin;       // q wraps: next output row
+    a.x_cp = (H - pl.P * stride) * W * Cin;            // p wraps: next image
+  }
   wgrad_partial_kernel<<<(unsigned)(a.per_xcd * 8), kWgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
