@@ -279,19 +279,31 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
 }
 
 // dw[e] = bf16( RN32(sum_{s in order} partial[s][e]) * RN32(sx * sdy) ), 4 elements/thread.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ partial,
-                                                           uint16_t* __restrict__ dw,
-                                                           const float* __restrict__ sx,
-                                                           const float* __restrict__ sdy,
-                                                           int64_t total, int splits) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+// Small workgroups spread the few hundred KB of output over every CU; the split loop issues
+// its loads in groups of 4 and still adds them in split order.
+constexpr int kRedThreads = 64;
+__global__ __launch_bounds__(kRedThreads) void wgrad_reduce_kernel(const float* __restrict__ partial,
+                                                                  uint16_t* __restrict__ dw,
+                                                                  const float* __restrict__ sx,
+                                                                  const float* __restrict__ sdy,
+                                                                  int64_t total, int splits) {
+  const int64_t i = ((int64_t)blockIdx.x * kRedThreads + threadIdx.x) * 4;
   if (i >= total) return;
   const float scale = sx[0] * sdy[0];
+  const float* src = partial + i;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const v4f v = *reinterpret_cast<const v4f*>(partial + (int64_t)s * total + i);
-    acc = acc + v;
+  int s = 0;
+  for (; s + 4 <= splits; s += 4) {
+    const v4f a = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 0) * total);
+    const v4f b = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 1) * total);
+    const v4f c = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 2) * total);
+    const v4f d = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 3) * total);
+    acc = acc + a;
+    acc = acc + b;
+    acc = acc + c;
+    acc = acc + d;
   }
+  for (; s < splits; ++s) acc = acc + *reinterpret_cast<const v4f*>(src + (int64_t)s * total);
   uint2 o;
   o.x = f32_to_bf16_bits(acc[0] * scale) | (f32_to_bf16_bits(acc[1] * scale) << 16);
   o.y = f32_to_bf16_bits(acc[2] * scale) | (f32_to_bf16_bits(acc[3] * scale) << 16);
@@ -389,7 +401,7 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   int st = launch_status();
   if (st != DPA_OK) return st;
   const int64_t total = (int64_t)Cout * R * S * Cin;
-  wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 1024), 256, 0, s>>>(
+  wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedThreads), kRedThreads, 0, s>>>(
       (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, pl.splits);
   return launch_status();
 }
