@@ -92,6 +92,41 @@ __device__ __forceinline__ float quant_div(float x, float scale) {
   return clamp_fp8(x / scale);
 }
 
+// The same quotient without a division per element: with r = RN32(1 / scale) a normal float,
+// q0 = RN(x r), e = x - scale q0 (exact through the FMA) and q1 = RN(q0 + e r) is the
+// correctly rounded x / scale (Markstein's correction; the test of every bf16 input against
+// every reachable scale checks it bit for bit). Where q0 is +-inf (x / scale overflows) q1 is
+// NaN, and where q1 is 0 its sign may differ from x / scale: q0 is kept in both cases.
+__device__ __forceinline__ float quant_rcp(float x, float scale, float r) {
+  const float q0 = x * r;
+  const float e = __builtin_fmaf(-q0, scale, x);
+  const float q1 = __builtin_fmaf(e, r, q0);
+  return clamp_fp8((q1 != q1 || q1 == 0.0f) ? q0 : q1);
+}
+
+// r = RN32(1 / scale) when the fast quotient is valid for this scale, else 0. The residual
+// x - scale q0 is ~2^-23 x; for every quotient that can round to a nonzero e4m3 value
+// (x / scale >= 2^-10) it stays a normal float when scale >= 2^-64. Smaller scales (tensors
+// whose amax is below ~2^-55) take the division.
+__device__ __forceinline__ float quant_recip(float scale) {
+  return (scale >= 0x1p-64f && scale <= 0x1p+120f) ? 1.0f / scale : 0.0f;
+}
+
+// 8 bf16 (one uint4) -> 8 e4m3 bytes (one uint2), fast quotient (r from quant_recip != 0).
+__device__ __forceinline__ uint2 quant8_rcp(uint4 v, float scale, float r) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = quant_rcp(__uint_as_float(w[i] << 16), scale, r);
+    f[2 * i + 1] = quant_rcp(__uint_as_float(w[i] & 0xffff0000u), scale, r);
+  }
+  uint2 o;
+  o.x = pack4_e4m3(f[0], f[1], f[2], f[3]);
+  o.y = pack4_e4m3(f[4], f[5], f[6], f[7]);
+  return o;
+}
+
 // 8 bf16 (one uint4) -> 8 e4m3 bytes (one uint2).
 __device__ __forceinline__ uint2 quant8(uint4 v, float scale) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};

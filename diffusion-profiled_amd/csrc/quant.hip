@@ -9,15 +9,19 @@
 //
 // Design: the amax is reduced as bf16 magnitude bit patterns with packed u16 max (exact and
 // order-free). Partials are one u32 per block; every block of the cast kernel re-reduces
-// the (<= kMaxPartials) partials from L2 and derives the scale itself, so current scaling
+// the (<= kAmaxBlocks) partials from L2 and derives the scale itself, so current scaling
 // needs two launches, no atomics and no zero-initialised state (safe under graph capture).
+// Tensors of at most kSmallMaxN elements take one single-workgroup launch instead. Both
+// passes keep kUnroll 16-B loads in flight per thread over a grid of a few blocks per CU.
 #include "dpa_common.hpp"
 
 namespace dpa {
 
 constexpr int kQThreads = 256;
 constexpr int kMaxPartials = 1024;
-constexpr int kElemsPerIter = 16;  // per thread and iteration: two uint4 of bf16
+constexpr int kUnroll = 8;          // uint4 loads in flight per thread
+constexpr int kAmaxBlocks = 512;    // amax pass grid cap (and partial count cap)
+constexpr int kCastBlocks = 1024;   // cast pass grid cap
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
   v = wave_max_u32(v);
@@ -41,6 +45,23 @@ __device__ __forceinline__ uint32_t reduce_partials(const uint32_t* partials, in
   return block_max_u32(m, red);
 }
 
+// Vector loop shared by the passes: every 8-element group v < n / 8 is visited once, kUnroll
+// groups (grid-strided) per thread and iteration with all their loads issued first; body(v,
+// data) gets the group index and its 16 bytes of bf16.
+template <typename Body>
+__device__ __forceinline__ void for_groups(const uint16_t* __restrict__ x, int64_t nv, Body body) {
+  const int64_t gs = (int64_t)gridDim.x * kQThreads;
+  int64_t v = (int64_t)blockIdx.x * kQThreads + threadIdx.x;
+  for (; v + (kUnroll - 1) * gs < nv; v += kUnroll * gs) {
+    uint4 d[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) d[u] = *reinterpret_cast<const uint4*>(x + 8 * (v + u * gs));
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) body(v + u * gs, d[u]);
+  }
+  for (; v < nv; v += gs) body(v, *reinterpret_cast<const uint4*>(x + 8 * v));
+}
+
 // Pass 1 (current scaling): per-block amax of |x| as bf16 bits.
 template <bool kVec>
 __global__ __launch_bounds__(kQThreads) void amax_partials_kernel(const uint16_t* __restrict__ x,
@@ -49,34 +70,30 @@ __global__ __launch_bounds__(kQThreads) void amax_partials_kernel(const uint16_t
   __shared__ uint32_t red[kQThreads / 64];
   us2 acc = {0, 0};
   uint32_t accs = 0;
-  const int64_t stride = (int64_t)gridDim.x * kQThreads * kElemsPerIter;
-  int64_t i = ((int64_t)blockIdx.x * kQThreads + threadIdx.x) * kElemsPerIter;
+  int64_t tail = 0;
   if (kVec) {
-    for (; i + kElemsPerIter <= n; i += stride) {
-      uint4 v0 = ld_nt16(x + i);
-      uint4 v1 = ld_nt16(x + i + 8);
-      acc = absmax8(acc, v0);
-      acc = absmax8(acc, v1);
-    }
-    // ragged tail: at most one partial group, handled by whichever thread reached it
-    if (i < n) {
-      for (int64_t j = i; j < n; ++j) {
-        uint32_t a = x[j] & 0x7fffu;
-        accs = accs > a ? accs : a;
-      }
-    }
-  } else {
-    for (; i < n; i += stride) {
-      for (int64_t j = i; j < i + kElemsPerIter && j < n; ++j) {
-        uint32_t a = x[j] & 0x7fffu;
-        accs = accs > a ? accs : a;
-      }
+    const int64_t nv = n >> 3;
+    for_groups(x, nv, [&](int64_t, uint4 d) { acc = absmax8(acc, d); });
+    tail = nv << 3;
+  }
+  if (blockIdx.x == 0) {  // ragged tail (or everything when x is not 16-B aligned)
+    for (int64_t j = tail + threadIdx.x; j < n; j += kQThreads) {
+      const uint32_t a = x[j] & 0x7fffu;
+      accs = accs > a ? accs : a;
     }
   }
   uint32_t m = acc.x > acc.y ? acc.x : acc.y;
   m = m > accs ? m : accs;
   m = block_max_u32(m, red);
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__device__ __forceinline__ void cast_tail(const uint16_t* __restrict__ x, int64_t from, int64_t n,
+                                          float scale, uint8_t* __restrict__ q) {
+  for (int64_t j = from + threadIdx.x; j < n; j += kQThreads) {
+    const float f = quant_div(bf16_bits_to_f32(x[j]), scale);
+    q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
+  }
 }
 
 // Pass 2 (current scaling): scale from the partials, then q = e4m3(clamp(x / scale)).
@@ -88,32 +105,21 @@ __global__ __launch_bounds__(kQThreads) void cast_current_kernel(
   const uint32_t amax_bits = reduce_partials(partials, np, red);
   const float scale = scale_from_amax_bits(amax_bits);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
-
-  const int64_t stride = (int64_t)gridDim.x * kQThreads * kElemsPerIter;
-  int64_t i = ((int64_t)blockIdx.x * kQThreads + threadIdx.x) * kElemsPerIter;
+  int64_t tail = 0;
   if (kVec) {
-    for (; i + kElemsPerIter <= n; i += stride) {
-      uint4 v0 = ld_nt16(x + i);
-      uint4 v1 = ld_nt16(x + i + 8);
-      uint2 a = quant8(v0, scale);
-      uint2 b = quant8(v1, scale);
-      uint4 o = {a.x, a.y, b.x, b.y};
-      st_nt16(q + i, o);
-    }
-    if (i < n) {
-      for (int64_t j = i; j < n; ++j) {
-        float f = quant_div(bf16_bits_to_f32(x[j]), scale);
-        q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
-      }
-    }
-  } else {
-    for (; i < n; i += stride) {
-      for (int64_t j = i; j < i + kElemsPerIter && j < n; ++j) {
-        float f = quant_div(bf16_bits_to_f32(x[j]), scale);
-        q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
-      }
-    }
+    const int64_t nv = n >> 3;
+    const float r = quant_recip(scale);
+    if (r != 0.0f)
+      for_groups(x, nv, [&](int64_t v, uint4 d) {
+        *reinterpret_cast<uint2*>(q + 8 * v) = quant8_rcp(d, scale, r);
+      });
+    else
+      for_groups(x, nv, [&](int64_t v, uint4 d) {
+        *reinterpret_cast<uint2*>(q + 8 * v) = quant8(d, scale);
+      });
+    tail = nv << 3;
   }
+  if (blockIdx.x == 0) cast_tail(x, tail, n, scale, q);
 }
 
 // Delayed scaling, one pass: q = cast(x, *prev_scale) and per-block amax of x.
@@ -125,36 +131,28 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
   const float scale = *prev_scale;
   us2 acc = {0, 0};
   uint32_t accs = 0;
-  const int64_t stride = (int64_t)gridDim.x * kQThreads * kElemsPerIter;
-  int64_t i = ((int64_t)blockIdx.x * kQThreads + threadIdx.x) * kElemsPerIter;
+  int64_t tail = 0;
   if (kVec) {
-    for (; i + kElemsPerIter <= n; i += stride) {
-      uint4 v0 = ld_nt16(x + i);
-      uint4 v1 = ld_nt16(x + i + 8);
-      acc = absmax8(acc, v0);
-      acc = absmax8(acc, v1);
-      uint2 a = quant8(v0, scale);
-      uint2 b = quant8(v1, scale);
-      uint4 o = {a.x, a.y, b.x, b.y};
-      st_nt16(q + i, o);
+    const int64_t nv = n >> 3;
+    const float r = quant_recip(scale);
+    if (r != 0.0f)
+      for_groups(x, nv, [&](int64_t v, uint4 d) {
+        acc = absmax8(acc, d);
+        *reinterpret_cast<uint2*>(q + 8 * v) = quant8_rcp(d, scale, r);
+      });
+    else
+      for_groups(x, nv, [&](int64_t v, uint4 d) {
+        acc = absmax8(acc, d);
+        *reinterpret_cast<uint2*>(q + 8 * v) = quant8(d, scale);
+      });
+    tail = nv << 3;
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t j = tail + threadIdx.x; j < n; j += kQThreads) {
+      const uint32_t a = x[j] & 0x7fffu;
+      accs = accs > a ? accs : a;
     }
-    if (i < n) {
-      for (int64_t j = i; j < n; ++j) {
-        uint32_t a = x[j] & 0x7fffu;
-        accs = accs > a ? accs : a;
-        float f = quant_div(bf16_bits_to_f32(x[j]), scale);
-        q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
-      }
-    }
-  } else {
-    for (; i < n; i += stride) {
-      for (int64_t j = i; j < i + kElemsPerIter && j < n; ++j) {
-        uint32_t a = x[j] & 0x7fffu;
-        accs = accs > a ? accs : a;
-        float f = quant_div(bf16_bits_to_f32(x[j]), scale);
-        q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
-      }
-    }
+    cast_tail(x, tail, n, scale, q);
   }
   uint32_t m = acc.x > acc.y ? acc.x : acc.y;
   m = m > accs ? m : accs;
@@ -170,8 +168,55 @@ __global__ __launch_bounds__(kQThreads) void finalize_scale_kernel(
   if (threadIdx.x == 0) *scale_out = scale_from_amax_bits(amax_bits);
 }
 
+// Small tensors (weights): one workgroup does amax and cast in a single launch; the second
+// pass re-reads x from L2. kDelayed: cast with *prev_scale, scale_out = scale of this amax.
+constexpr int kSmallThreads = 1024;
+constexpr int64_t kSmallMaxN = 1 << 14;
+
+template <bool kDelayed>
+__global__ __launch_bounds__(kSmallThreads) void quant_small_kernel(
+    const uint16_t* __restrict__ x, int64_t n, const float* __restrict__ prev_scale,
+    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+  __shared__ uint32_t red[kSmallThreads / 64];
+  const float prev = kDelayed ? *prev_scale : 0.0f;  // read before scale_out is written
+  const int64_t n16 = n & ~(int64_t)15;
+  us2 acc = {0, 0};
+  uint32_t accs = 0;
+  for (int64_t i = (int64_t)threadIdx.x * 16; i < n16; i += kSmallThreads * 16) {
+    acc = absmax8(acc, *reinterpret_cast<const uint4*>(x + i));
+    acc = absmax8(acc, *reinterpret_cast<const uint4*>(x + i + 8));
+  }
+  for (int64_t j = n16 + threadIdx.x; j < n; j += kSmallThreads) {
+    const uint32_t a = x[j] & 0x7fffu;
+    accs = accs > a ? accs : a;
+  }
+  uint32_t m = acc.x > acc.y ? acc.x : acc.y;
+  m = wave_max_u32(m > accs ? m : accs);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  uint32_t amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kSmallThreads / 64; ++w) amax = amax > red[w] ? amax : red[w];
+  const float cur = scale_from_amax_bits(amax);
+  const float scale = kDelayed ? prev : cur;
+  if (threadIdx.x == 0) *scale_out = cur;
+  const float r = quant_recip(scale);
+  for (int64_t i = (int64_t)threadIdx.x * 16; i < n16; i += kSmallThreads * 16) {
+    const uint4 v0 = *reinterpret_cast<const uint4*>(x + i);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(x + i + 8);
+    const uint2 a = r != 0.0f ? quant8_rcp(v0, scale, r) : quant8(v0, scale);
+    const uint2 b = r != 0.0f ? quant8_rcp(v1, scale, r) : quant8(v1, scale);
+    *reinterpret_cast<uint2*>(q + i) = a;  // q is only required to be 8-B aligned
+    *reinterpret_cast<uint2*>(q + i + 8) = b;
+  }
+  for (int64_t j = n16 + threadIdx.x; j < n; j += kSmallThreads) {
+    const float f = quant_div(bf16_bits_to_f32(x[j]), scale);
+    q[j] = (uint8_t)(pack4_e4m3(f, 0.f, 0.f, 0.f) & 0xffu);
+  }
+}
+
 static int grid_for(int64_t n, int cap) {
-  int64_t g = ceil_div(n, (int64_t)kQThreads * kElemsPerIter);
+  int64_t g = ceil_div(n, (int64_t)kQThreads * 8 * kUnroll);
   if (g < 1) g = 1;
   if (g > cap) g = cap;
   return (int)g;
@@ -193,12 +238,14 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
   if (!workspace || workspace_bytes < dpa_quant_workspace_bytes(n)) return DPA_ERR_WORKSPACE;
   if (!aligned(workspace, 4) || !aligned(scale_out, 4) || !aligned(x, 2)) return DPA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const bool vec = aligned(x, 16) && aligned(q, 16);
-  const int np = grid_for(n, kMaxPartials);
-  const int gc = grid_for(n, 4096);
+  const bool vec = aligned(x, 16) && aligned(q, 8);
+  const int np = vec ? grid_for(n, kAmaxBlocks) : 1;
+  const int gc = vec ? grid_for(n, kCastBlocks) : 1;
   auto* xp = (const uint16_t*)x;
   auto* part = (uint32_t*)workspace;
-  if (vec) {
+  if (vec && n <= kSmallMaxN) {
+    quant_small_kernel<false><<<1, kSmallThreads, 0, s>>>(xp, n, nullptr, (uint8_t*)q, scale_out);
+  } else if (vec) {
     amax_partials_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, part);
     cast_current_kernel<true><<<gc, kQThreads, 0, s>>>(xp, n, part, np, (uint8_t*)q, scale_out);
   } else {
@@ -219,10 +266,15 @@ extern "C" int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const flo
       !aligned(x, 2))
     return DPA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const bool vec = aligned(x, 16) && aligned(q, 16);
-  const int np = grid_for(n, kMaxPartials);
+  const bool vec = aligned(x, 16) && aligned(q, 8);
+  const int np = vec ? grid_for(n, kAmaxBlocks) : 1;
   auto* xp = (const uint16_t*)x;
   auto* part = (uint32_t*)workspace;
+  if (vec && n <= kSmallMaxN) {
+    quant_small_kernel<true><<<1, kSmallThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q,
+                                                          cur_scale_out);
+    return launch_status();
+  }
   if (vec)
     cast_delayed_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part);
   else

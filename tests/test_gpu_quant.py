@@ -172,3 +172,31 @@ def test_exhaustive_cast_domain_vs_golden(L):
         diff = np.nonzero(qg != qo)[0][:8]
         pytest.fail(f"{bad.size} scales differ; first scale {scales[i]!r}: x bits "
                     f"{[hex(v) for v in diff]} gpu {[hex(qg[v]) for v in diff]} oracle {[hex(qo[v]) for v in diff]}")
+
+
+def test_exhaustive_cast_domain_multiblock_path(L):
+    """The same domain through the multi-workgroup cast kernel: the 65536 bf16 inputs tiled
+    5 times (past the single-workgroup size limit), every 16th reachable scale; the first and
+    last copies must both give the golden digest."""
+    d = np.load(GOLDEN, allow_pickle=False)
+    scales, golden = d["scales"][::16], d["digests"].view(np.int64)[::16]
+    base = torch.from_numpy(np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.int16))
+    x = base.repeat(5).view(torch.bfloat16).cuda()
+    assert x.numel() > (1 << 18)
+    mix = _mix64(65536).cuda()
+    s_dev = torch.from_numpy(scales).cuda()
+    q = torch.empty(x.numel(), dtype=torch.uint8, device="cuda")
+    cur = torch.empty((), dtype=torch.float32, device="cuda")
+    ws = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = L.load().dpa_quantize_fp8_delayed_bf16
+    first = torch.empty(scales.size, dtype=torch.int64, device="cuda")
+    last = torch.empty(scales.size, dtype=torch.int64, device="cuda")
+    for i in range(scales.size):
+        st = fn(x.data_ptr(), x.numel(), s_dev[i:i + 1].data_ptr(), q.data_ptr(), cur.data_ptr(),
+                ws.data_ptr(), 4096, stream)
+        assert st == 0
+        first[i] = ((q[:65536].to(torch.int64) + 1) * mix).sum()
+        last[i] = ((q[-65536:].to(torch.int64) + 1) * mix).sum()
+    np.testing.assert_array_equal(first.cpu().numpy(), golden)
+    np.testing.assert_array_equal(last.cpu().numpy(), golden)
