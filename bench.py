@@ -48,6 +48,13 @@ def parse():
     ap.add_argument("--workload", default="cfg2",
                     choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1", "cfg4", "cfg5"])
     ap.add_argument("--no-unet", action="store_true", help="skip the U-Net step in the cfg2 line")
+    ap.add_argument("--part", default=None,
+                    help="profiling mode: run only this part (quantize|fwd|dgrad|wgrad) of the "
+                         "workload --reps times, print nothing else")
+    ap.add_argument("--reps", type=int, default=5)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="profiling mode: --reps device copies of this many MiB (counter "
+                         "calibration: a plain copy reads and writes exactly that many bytes)")
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -99,9 +106,13 @@ class ConvWorkload:
     def fwd(self):
         return self.K.conv2d_fp8_fwd_general(self.xq, self.wq, self.xs, self.ws, self.stride, self.pad)
 
+    def wtrans(self):
+        self.wq_t = self.K.weight_transpose_fp8(self.wq)
+
     def dgrad(self):
+        """The data-gradient GEMM kernel alone (the weight transpose is its own part)."""
         return self.K.conv2d_fp8_dgrad_general(self.dyq, self.wq, self.dys, self.ws, (self.h, self.w),
-                                               self.stride, self.pad)
+                                               self.stride, self.pad, weight_t=self.wq_t)
 
     def wgrad(self):
         return self.K.conv2d_fp8_wgrad_general(self.xq, self.dyq, self.xs, self.dys, self.k,
@@ -110,11 +121,13 @@ class ConvWorkload:
     def step(self):
         self.quantize()
         self.fwd()
+        self.wtrans()
         self.dgrad()
         self.wgrad()
 
     def parts(self):
-        return {"quantize": self.quantize, "fwd": self.fwd, "dgrad": self.dgrad, "wgrad": self.wgrad}
+        return {"quantize": self.quantize, "fwd": self.fwd, "wtrans": self.wtrans,
+                "dgrad": self.dgrad, "wgrad": self.wgrad}
 
     def step_flop(self):
         return 3 * self.flop
@@ -421,12 +434,36 @@ def main():
         sys.exit(2)
     K = importlib.import_module("diffusion-profiled_amd.fp8_kernels")
     importlib.import_module("diffusion-profiled_amd._lib").load()
+    if args.copy_mib:
+        # random bytes: constant fills may be stored compressed and under-report reads
+        g = torch.Generator(device="cuda").manual_seed(0)
+        src = torch.randint(0, 256, (args.copy_mib << 20,), dtype=torch.uint8, device="cuda",
+                            generator=g)
+        dst = torch.empty_like(src)
+        for _ in range(args.reps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copied {args.copy_mib} MiB x {args.reps}", flush=True)
+        return
+    if args.part:
+        wl = make_workload(K, args.workload)
+        wl.quantize()
+        if hasattr(wl, "wtrans"):
+            wl.wtrans()
+        fn = wl.parts()[args.part]
+        for _ in range(args.reps):
+            fn()
+        torch.cuda.synchronize()
+        print(f"{args.workload} {args.part} x {args.reps}", flush=True)
+        return
     if args.workload in ("cfg4", "cfg5"):
         return model_main(args)
     wl = make_workload(K, args.workload)
 
     # per-part device times (HIP events on the launch stream)
     wl.quantize()
+    if hasattr(wl, "wtrans"):
+        wl.wtrans()
     parts = {}
     for name, fn in wl.parts().items():
         parts[name] = time_part(fn, args.kernel_reps)
@@ -443,20 +480,26 @@ def main():
     dt = (time.perf_counter() - t0) / args.steps
 
     tflops = wl.step_flop() / dt / 1e12
-    gemm_parts = {k: v for k, v in parts.items() if k != "quantize"}
-    dominant = max(gemm_parts, key=gemm_parts.get)
-    dom_us = gemm_parts[dominant]
+    # dominant kernel = the MFMA kernel with the most device time per step: igemm_fp8_kernel
+    # (one fwd and one dgrad launch) or the weight-gradient pair (partial + split reduce)
+    igemm_launches = [parts[k] for k in ("fwd", "dgrad") if k in parts]
+    if "wgrad" in parts and parts["wgrad"] > sum(igemm_launches):
+        dominant, dom_us, dom_bytes = "wgrad_partial_kernel+wgrad_reduce_kernel", parts["wgrad"], wl.bytes["wgrad"]
+    else:
+        dominant = "igemm_fp8_kernel"
+        dom_us = sum(igemm_launches) / len(igemm_launches)
+        dom_bytes = sum(wl.bytes[k] for k in ("fwd", "dgrad") if k in parts) / len(igemm_launches)
     achieved = wl.flop / (dom_us * 1e-6) / 1e12
     traffic = None
     if os.path.exists(PROFILE_TRAFFIC):
-        try:
-            traffic = json.load(open(PROFILE_TRAFFIC)).get(args.workload, {}).get(dominant)
-        except Exception:
-            traffic = None
+        with open(PROFILE_TRAFFIC) as f:
+            traffic = json.load(f).get(args.workload, {}).get(dominant, {}).get("bytes_per_launch")
     kernels = {}
     for k, us in parts.items():
         if k == "quantize":
             kernels[k] = {"us": round(us, 2), "GB/s": round(wl.quant_bytes / (us * 1e-6) / 1e9, 1)}
+        elif k == "wtrans":
+            kernels[k] = {"us": round(us, 2)}
         else:
             kernels[k] = {"us": round(us, 2), "TFLOP/s": round(wl.flop / (us * 1e-6) / 1e12, 1),
                           "frac_fp8_peak": round(wl.flop / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4)}
@@ -482,7 +525,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": traffic,
-            "algorithmic_bytes": wl.bytes.get(dominant),
+            "algorithmic_bytes": dom_bytes,
+            "launch_us": round(dom_us, 2),
         },
         "kernels": kernels,
     }
