@@ -383,9 +383,21 @@ static void fill_common(IgemmArgs& a, const void* act, const void* wgt, void* ou
   a.bias = bias;
 }
 
+// halo-patch kernel for 3x3 / stride 1 / pad 1 on 16- and 32-pixel-wide images (hconv.hip)
+bool hconv_supported(int N, int H, int W, int C, int Cout);
+int hconv_run(const void* act, const void* wgt, const float* sa, const float* sb,
+              const float* bias, void* out, int N, int H, int W, int C, int Cout, int flip,
+              int num_cus, hipStream_t s);
+
+static bool use_hconv(int N, int H, int W, int C, int Cout, int R, int S, int stride, int pad) {
+  return R == 3 && S == 3 && stride == 1 && pad == 1 && hconv_supported(N, H, W, C, Cout);
+}
+
 static int conv_fwd(const void* xq, const void* wq, const float* xs, const float* ws,
                     const float* bias, void* y, int N, int H, int W, int Cin, int Cout, int R,
                     int S, int stride, int pad, hipStream_t s) {
+  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad))
+    return hconv_run(xq, wq, xs, ws, bias, y, N, H, W, Cin, Cout, 0, num_cus(), s);
   IgemmArgs a{};
   fill_common(a, xq, wq, y, xs, ws, bias);
   const int P = (H + 2 * pad - R) / stride + 1;
@@ -409,6 +421,9 @@ static int conv_fwd(const void* xq, const void* wq, const float* xs, const float
 static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const float* ws,
                       void* dx, int N, int H, int W, int Cin, int Cout, int R, int S,
                       int stride, int pad, hipStream_t s) {
+  // the 3x3 / s1 / p1 data gradient is a conv of dy with the mirrored, transposed weight
+  if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad))
+    return hconv_run(dyq, wt, dys, ws, nullptr, dx, N, H, W, Cout, Cin, 1, num_cus(), s);
   const int P = (H + 2 * pad - R) / stride + 1;
   const int Q = (W + 2 * pad - S) / stride + 1;
   for (int ay = 0; ay < stride; ++ay)
