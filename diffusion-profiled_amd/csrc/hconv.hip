@@ -261,22 +261,36 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
       const int st = t - (t >= 6 ? 6 : (t >= 3 ? 3 : 0));  // t % 3
       const int st1 = st == 2 ? 0 : st + 1;
       const uint8_t* pb = hc_b[st1];
+      // pixel fragments 0..2: 4 MFMAs each, then the next step's A fragment in its place;
+      // the DMAs of this step go out after the first group
 #pragma unroll
-      for (int pj = 0; pj < 4; ++pj) {
+      for (int pj = 0; pj < 3; ++pj) {
 #pragma unroll
         for (int ci = 0; ci < 4; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
         const uint32_t a0 = abase[pj] + aoff;
         fa[pj] = hc_frag2(pa, a0, a0 + 16);
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
+        if (pj == 0) {
+          issue_patch_slot(cn, t < kHcPatchLoads ? t : 0, patch_buf(gc + 1));
+          if (t < 6)
+            issue_b(cc, t + 3, st);
+          else
+            issue_b(cn, t - 6, st);
+        }
       }
-      issue_patch_slot(cn, t < kHcPatchLoads ? t : 0, patch_buf(gc + 1));
-      if (t < 6)
-        issue_b(cc, t + 3, st);
-      else
-        issue_b(cn, t - 6, st);
+      // pixel fragment 3: each weight fragment's last use, then its next-step reload
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fb[i] = hc_frag2(pb, b_addr[i], b_addr[i] ^ 16u);
+      for (int ci = 0; ci < 4; ++ci) {
+        acc[ci][3] = mfma16x16x128_e4m3(fb[ci], fa[3], acc[ci][3]);
+        fb[ci] = hc_frag2(pb, b_addr[ci], b_addr[ci] ^ 16u);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
+      }
+      {
+        const uint32_t a0 = abase[3] + aoff;
+        fa[3] = hc_frag2(pa, a0, a0 + 16);
+      }
     }
     const int j = (int)fdiv((uint32_t)gc, p.divKC);
     if (gc - j * p.KC == p.KC - 1) epilogue(cc.m0, cc.n0);
