@@ -120,10 +120,13 @@ __device__ __forceinline__ void wg_issue(const WgradArgs& p, WgRows& r, bool liv
 
 // Consumer step s (stage ST = s % kWgStages): barrier (the producers have waited for stage
 // s+1's DMAs, and every consumer wave holds stage s's fragments in registers), then 16 MFMAs
-// per wave on stage s while reading stage s+1's fragments.
+// per wave on stage s (fragments xc, dc) with the 32 transpose reads of stage s+1 (into xn,
+// dn) spread between them, two per MFMA, so the LDS reads overlap the matrix pipe and have
+// all landed by the next barrier.
 template <int ST>
 __device__ __forceinline__ void wg_consume(const uint32_t (&Tx)[8], const uint32_t (&Td)[8],
-                                           v8i (&xf)[4], v8i (&df)[4], v4f (&acc)[4][4]) {
+                                           const v8i (&xc)[4], const v8i (&dc)[4], v8i (&xn)[4],
+                                           v8i (&dn)[4], v4f (&acc)[4][4]) {
   constexpr int NX = (ST + 1) % kWgStages;
   wait_lgkmcnt0();
   lds_barrier();
@@ -132,13 +135,15 @@ __device__ __forceinline__ void wg_consume(const uint32_t (&Tx)[8], const uint32
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xf[i], df[j], acc[i][j]);
-    xf[i] = ld_frag_tbl(nx, Tx, i);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // then 4 DS reads
-  }
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x128_e4m3(xc[i], dc[j], acc[i][j]);
+    xn[i] = ld_frag_tbl(nx, Tx, i);
+    dn[i] = ld_frag_tbl(nx + kWgOperandBytes, Td, i);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) df[j] = ld_frag_tbl(nx + kWgOperandBytes, Td, j);
+    for (int k = 0; k < 4; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
+    }
+  }
 }
 
 // Producer step s: wait until stage s+1 has landed (stages s+2 .. s+kWgStages-1 may still be
@@ -235,16 +240,17 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
     lds_barrier();  // stage 0 landed
-    v8i xf[4], df[4];
+    // two fragment sets (a, b) alternate between "current" and "next" from step to step
+    v8i xa[4], da[4], xb[4], db[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xf[i] = ld_frag_tbl(wg_smem, Tx, i);
+    for (int i = 0; i < 4; ++i) xa[i] = ld_frag_tbl(wg_smem, Tx, i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) df[j] = ld_frag_tbl(wg_smem + kWgOperandBytes, Td, j);
+    for (int j = 0; j < 4; ++j) da[j] = ld_frag_tbl(wg_smem + kWgOperandBytes, Td, j);
     for (int s = 0; s < nsteps; s += 4) {
-      wg_consume<0>(Tx, Td, xf, df, acc);
-      if (s + 1 < nsteps) wg_consume<1>(Tx, Td, xf, df, acc);
-      if (s + 2 < nsteps) wg_consume<2>(Tx, Td, xf, df, acc);
-      if (s + 3 < nsteps) wg_consume<3>(Tx, Td, xf, df, acc);
+      wg_consume<0>(Tx, Td, xa, da, xb, db, acc);
+      if (s + 1 < nsteps) wg_consume<1>(Tx, Td, xb, db, xa, da, acc);
+      if (s + 2 < nsteps) wg_consume<2>(Tx, Td, xa, da, xb, db, acc);
+      if (s + 3 < nsteps) wg_consume<3>(Tx, Td, xb, db, xa, da, acc);
     }
     wait_lgkmcnt0();
     lds_barrier();  // pairs with the producers' final barrier
@@ -345,6 +351,25 @@ static WgradPlan plan_wgrad(int N, int H, int W, int Cin, int Cout, int R, int S
   return pl;
 }
 
+// Three-tap kernel for 3x3 / stride-1 / pad-1 convolutions of 16- and 32-pixel-wide images
+// (hwgrad.hip); its partial tiles have the layout wgrad_reduce_kernel sums.
+bool hwgrad_supported(int N, int H, int W, int Cin, int Cout);
+int hwgrad_splits(int N, int H, int W, int Cin, int Cout, int split_k);
+int hwgrad_partial_run(const void* xq, const void* dyq, float* partial, int N, int H, int W,
+                       int Cin, int Cout, int splits, hipStream_t s);
+
+static bool use_hwgrad(int N, int H, int W, int Cin, int Cout, int R, int S, int stride,
+                       int pad) {
+  return R == 3 && S == 3 && stride == 1 && pad == 1 && hwgrad_supported(N, H, W, Cin, Cout);
+}
+
+static int wgrad_splits(int N, int H, int W, int Cin, int Cout, int R, int S, int stride,
+                        int pad, int split_k) {
+  if (use_hwgrad(N, H, W, Cin, Cout, R, S, stride, pad))
+    return hwgrad_splits(N, H, W, Cin, Cout, split_k);
+  return plan_wgrad(N, H, W, Cin, Cout, R, S, stride, pad, split_k).splits;
+}
+
 }  // namespace dpa
 
 using namespace dpa;
@@ -352,9 +377,9 @@ using namespace dpa;
 extern "C" int64_t dpa_conv2d_wgrad_workspace_bytes(int N, int H, int W, int Cin, int Cout,
                                                     int R, int S, int stride, int pad,
                                                     int split_k) {
-  if (!wgrad_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad)) return 0;
-  WgradPlan pl = plan_wgrad(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
-  return (int64_t)pl.splits * Cout * R * S * Cin * 4;
+  if (!wgrad_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad) || split_k < 0) return 0;
+  const int splits = wgrad_splits(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
+  return (int64_t)splits * Cout * R * S * Cin * 4;
 }
 
 extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float* x_scale,
@@ -365,15 +390,24 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   if (!xq || !dyq || !x_scale || !dy_scale || !dw) return DPA_ERR_NULL;
   if (!wgrad_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad)) return DPA_ERR_SHAPE;
   if (split_k < 0) return DPA_ERR_SIZE;
-  WgradPlan pl = plan_wgrad(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
-  const int64_t need = (int64_t)pl.splits * Cout * R * S * Cin * 4;
+  const int splits = wgrad_splits(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
+  const int64_t need = (int64_t)splits * Cout * R * S * Cin * 4;
   if (!workspace || workspace_bytes < need) return DPA_ERR_WORKSPACE;
   if (!aligned(xq, 16) || !aligned(dyq, 16) || !aligned(workspace, 16) || !aligned(dw, 8))
     return DPA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t total = (int64_t)Cout * R * S * Cin;
+  if (use_hwgrad(N, H, W, Cin, Cout, R, S, stride, pad)) {
+    int st = hwgrad_partial_run(xq, dyq, (float*)workspace, N, H, W, Cin, Cout, splits, s);
+    if (st != DPA_OK) return st;
+    wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedThreads), kRedThreads, 0, s>>>(
+        (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, splits);
+    return launch_status();
+  }
+  WgradPlan pl = plan_wgrad(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
   // 32-bit byte offsets inside the kernel
   if ((int64_t)N * H * W * Cin > 0x7fffffff || (int64_t)pl.npix * Cout > 0x7fffffff)
     return DPA_ERR_SIZE;
-  hipStream_t s = (hipStream_t)stream;
   WgradArgs a{};
   a.x = (const uint8_t*)xq;
   a.dy = (const uint8_t*)dyq;
@@ -400,7 +434,6 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   wgrad_partial_kernel<<<(unsigned)(a.per_xcd * 8), kWgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
-  const int64_t total = (int64_t)Cout * R * S * Cin;
   wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedThreads), kRedThreads, 0, s>>>(
       (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, pl.splits);
   return launch_status();

@@ -171,6 +171,20 @@ def test_wgrad_split_invariance(K):
     assert_bf16_close(nhwc_bits(c.cpu()), ref, "default vs 1")
 
 
+@pytest.mark.parametrize("n,h,w,split_k", [(3, 16, 16, 2), (3, 16, 16, 5), (3, 32, 32, 5),
+                                           (2, 32, 32, 1)])
+def test_wgrad_three_tap_splits_across_images(K, n, h, w, split_k):
+    """3x3 stride-1 wgrad of 16/32-wide images (three taps per workgroup): pixel splits that
+    start and end inside an image and cross image boundaries, against the exact oracle."""
+    xq, xs, wq, ws, dyq, dys = quantized_inputs(K, n, 128, 256, h, w, seed=n + h + split_k)
+    dw = K.conv2d_fp8_wgrad_general(xq, dyq, xs, dys, 3, 1, 1, split_k)
+    torch.cuda.synchronize()
+    xb, db = (nhwc_bits(t.cpu().view(torch.uint8)) for t in (xq, dyq))
+    dw_ref = O.conv2d_wgrad(xb, db, f32(xs), f32(dys), 3, 1, 1)
+    frac = assert_bf16_close(nhwc_bits(dw.cpu()), dw_ref, f"wgrad split {split_k}")
+    assert frac > 0.9, frac
+
+
 def test_zero_weight_gives_zero_output(K):
     """conv_2 is zero-initialised in the reference (diffusion/unet.py:146): scale 1, y == 0."""
     x = randn_bf16((2, 256, 16, 16), seed=1)
