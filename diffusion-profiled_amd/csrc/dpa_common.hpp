@@ -14,6 +14,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kFp8Max = 448.0f;  // torch.finfo(torch.float8_e4m3fn).max
 
@@ -191,6 +192,10 @@ __device__ __forceinline__ void st_nt16(void* p, uint4 v) {
   u32x4 w = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
 }
+__device__ __forceinline__ void st_nt8(void* p, uint2 v) {
+  u32x2 w = {v.x, v.y};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
+}
 
 // Two fp32 -> packed bf16 pair (round to nearest even) with gfx950's v_cvt_pk_bf16_f32.
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -234,13 +239,24 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+// LDS (and scalar-memory) operations complete in order, so lgkmcnt(N) waits for all but the
+// N most recently issued LDS operations.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt");
+  __builtin_amdgcn_s_waitcnt(0xc07f | (N << 8));
+}
 
 // Workgroup barrier that the compiler may not move memory operations across (the DMA
-// writes above are invisible to it).
+// writes above are invisible to it), nor any other instruction: the scheduler would
+// otherwise hoist the next step's MFMAs (register-only) above it, next to the fragment reads
+// they consume, and undo the read-ahead of the pipelined loops.
 __device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // ---------------------------------------------------------------------------------------

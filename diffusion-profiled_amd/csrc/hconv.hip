@@ -251,8 +251,11 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
   // gc+1 (a duplicate of slot 0 for t >= 6) and the weight slice three steps ahead.
   for (int gc = 0; gc < nchunks; ++gc) {
     for (int t = 0; t < 9; ++t) {
+      // the weight-fragment reads of the previous step (from the stage the DMAs below
+      // refill) must be done; the two reads of the last A fragment, issued after them and
+      // from a patch buffer no DMA of this step touches, may still be in flight
       wait_vmcnt<kHcBLoads + 1>();
-      wait_lgkmcnt0();
+      wait_lgkmcnt<2>();
       lds_barrier();
       const int t1 = t == 8 ? 0 : t + 1;
       const int ty1 = t1 >= 6 ? 2 : (t1 >= 3 ? 1 : 0);

