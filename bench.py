@@ -132,6 +132,18 @@ class ConvWorkload:
     def step_flop(self):
         return 3 * self.flop
 
+    def kernel_names(self):
+        """Kernels the library launches for this layer's GEMMs, following its dispatch
+        (csrc/igemm.hip use_hconv, csrc/wgrad.hip use_hwgrad): 3x3 / stride-1 convs of 16- or
+        32-wide images go to the halo-patch and three-tap kernels."""
+        s1 = self.k == 3 and self.stride == 1 and self.pad == 1 and self.w in (16, 32)
+        conv = "hconv_fp8_kernel" if (s1 and self.h % (256 // self.w) == 0) else "igemm_fp8_kernel"
+        if s1 and self.h % (128 // self.w) == 0 and self.cin % 64 == 0:
+            wg = f"hwgrad_partial_kernel<{self.w}>+wgrad_reduce_kernel"
+        else:
+            wg = "wgrad_partial_kernel+wgrad_reduce_kernel"
+        return {"fwd": conv, "dgrad": conv, "wgrad": wg}
+
     def config(self):
         return {
             "workload": self.name,
@@ -480,15 +492,16 @@ def main():
     dt = (time.perf_counter() - t0) / args.steps
 
     tflops = wl.step_flop() / dt / 1e12
-    # dominant kernel = the MFMA kernel with the most device time per step: igemm_fp8_kernel
+    # dominant kernel = the MFMA kernel with the most device time per step: the conv kernel
     # (one fwd and one dgrad launch) or the weight-gradient pair (partial + split reduce)
-    igemm_launches = [parts[k] for k in ("fwd", "dgrad") if k in parts]
-    if "wgrad" in parts and parts["wgrad"] > sum(igemm_launches):
-        dominant, dom_us, dom_bytes = "wgrad_partial_kernel+wgrad_reduce_kernel", parts["wgrad"], wl.bytes["wgrad"]
+    names = wl.kernel_names() if hasattr(wl, "kernel_names") else {"fwd": "igemm_fp8_kernel"}
+    conv_launches = [parts[k] for k in ("fwd", "dgrad") if k in parts]
+    if "wgrad" in parts and parts["wgrad"] > sum(conv_launches):
+        dominant, dom_us, dom_bytes = names["wgrad"], parts["wgrad"], wl.bytes["wgrad"]
     else:
-        dominant = "igemm_fp8_kernel"
-        dom_us = sum(igemm_launches) / len(igemm_launches)
-        dom_bytes = sum(wl.bytes[k] for k in ("fwd", "dgrad") if k in parts) / len(igemm_launches)
+        dominant = names["fwd"]
+        dom_us = sum(conv_launches) / len(conv_launches)
+        dom_bytes = sum(wl.bytes[k] for k in ("fwd", "dgrad") if k in parts) / len(conv_launches)
     achieved = wl.flop / (dom_us * 1e-6) / 1e12
     traffic = None
     if os.path.exists(PROFILE_TRAFFIC):
@@ -502,7 +515,8 @@ def main():
             kernels[k] = {"us": round(us, 2)}
         else:
             kernels[k] = {"us": round(us, 2), "TFLOP/s": round(wl.flop / (us * 1e-6) / 1e12, 1),
-                          "frac_fp8_peak": round(wl.flop / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+                          "frac_fp8_peak": round(wl.flop / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                          "kernel": names.get(k, names["fwd"])}
     out = {
         "metric": METRIC,
         "value": round(tflops, 2),

@@ -5,17 +5,19 @@
 // (:132-133, eps 1e-5, affine). Under autocast GroupNorm runs in fp32; the FP8 conv then
 // rounds its input to bf16 (diffusion/fp8_kernels.py:835), which is what `out` stores.
 //
-// Layout: one workgroup per (image n, 64-channel slab): 256 threads = 32 pixel lanes x 8
-// granules of 8 channels (16 B of bf16). Every group of the slab lies inside the slab
-// (64 % (C/G) == 0), so the statistics reduce inside the workgroup: 4-channel half-granule
-// partials -> wave shuffles over the 8 pixel lanes of a wave -> LDS over the 4 waves.
-// The kernels make two passes over their inputs (the second mostly from L2).
+// Layout: one workgroup per (image n, 64-channel slab): PLN pixel lanes (32, 64 or 128 by
+// image size) x 8 granules of 8 channels (16 B of bf16). Every group of the slab lies inside
+// the slab (64 % (C/G) == 0), so the statistics reduce inside the workgroup: 4-channel
+// half-granule partials -> wave shuffles over the 8 pixel lanes of a wave -> LDS over the
+// waves. Each lane keeps four 16-B loads in flight. The kernels make several passes over
+// their inputs (after the first mostly from L2).
 #include "dpa_common.hpp"
 
 namespace dpa {
 
-constexpr int kGnThreads = 256;
 constexpr int kSlab = 64;  // channels per workgroup
+constexpr int kGnUnrollFwd = 4;  // pixels per lane per loop iteration (loads in flight)
+constexpr int kGnUnrollBwd = 2;  // (two sources per pixel)
 
 struct GnArgs {
   const uint16_t* x;
@@ -43,10 +45,12 @@ __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
   }
 }
 
-// Sum v over the 32 pixel lanes that share this thread's granule; result valid in all lanes
-// of LDS slot [granule]. red must hold 4 waves x 8 granules x nvals floats.
-template <int NV>
+// Sum v over the PLN pixel lanes that share this thread's granule (8 per wave by shuffles,
+// then the waves in order through LDS); result valid in every lane. red holds
+// (PLN / 8) waves x 8 granules x NV floats.
+template <int NV, int PLN>
 __device__ __forceinline__ void slab_reduce(float (&v)[NV], float* red) {
+  constexpr int kWaves = PLN / 8;
   const int gq = threadIdx.x & 7;
   const int wave = threadIdx.x >> 6;
 #pragma unroll
@@ -63,9 +67,12 @@ __device__ __forceinline__ void slab_reduce(float (&v)[NV], float* red) {
   }
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
-    v[k] = red[(0 * 8 + gq) * NV + k] + red[(1 * 8 + gq) * NV + k] +
-           red[(2 * 8 + gq) * NV + k] + red[(3 * 8 + gq) * NV + k];
+  for (int k = 0; k < NV; ++k) v[k] = red[gq * NV + k];
+#pragma unroll 1
+  for (int w = 1; w < kWaves; ++w) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] += red[(w * 8 + gq) * NV + k];
+  }
   __syncthreads();
 }
 
@@ -79,47 +86,82 @@ __device__ __forceinline__ float group_sum(const float* hs, int half_idx, int cp
   return s;
 }
 
-__global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p) {
-  __shared__ float red[4 * 8 * 2];
+// Pixel loop of a pass: lane pl visits pixels pl, pl + PLN, ... in groups of U whose 16-B
+// loads (from each of the NL sources) are all issued before any is used; pixels past HW load
+// pixel HW - 1 (a valid address) and reach body(px, ok, v0, v1) with ok false.
+template <int PLN, int NL, int U, typename F>
+__device__ __forceinline__ void gn_pixels(const uint16_t* const (&src)[NL], int C, int pl, int HW,
+                                          F body) {
+  for (int px0 = pl; px0 < HW; px0 += U * PLN) {
+    int pxs[U];
+    bool oks[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int px = px0 + u * PLN;
+      oks[u] = px < HW;
+      pxs[u] = oks[u] ? px : HW - 1;
+    }
+    uint4 v[NL][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int l = 0; l < NL; ++l)
+        v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * C);
+#pragma unroll
+    for (int u = 0; u < U; ++u) body(pxs[u], oks[u], v[0][u], v[NL - 1][u]);
+  }
+}
+
+// Layout: one workgroup per (image n, 64-channel slab): 8 x PLN threads = PLN pixel lanes x
+// 8 granules of 8 channels (16 B of bf16).
+template <int PLN>
+__global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
+  __shared__ float red[(PLN / 8) * 8 * 2];
   __shared__ float hs[16];
   const int n = blockIdx.y;
   const int c0 = blockIdx.x * kSlab;
   const int gq = threadIdx.x & 7;
-  const int pl = threadIdx.x >> 3;  // 0..31
+  const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
-  const uint16_t* xb = p.x + (int64_t)n * p.HW * p.C + ch;
+  const int HW = p.HW;
+  const uint16_t* xb = p.x + (int64_t)n * HW * p.C + ch;
 
   // pass 1: mean
   float s[2] = {0.f, 0.f};
-  for (int px = pl; px < p.HW; px += 32) {
+  const uint16_t* const xsrc[1] = {xb};
+  gn_pixels<PLN, 1, kGnUnrollFwd>(xsrc, p.C, pl, HW, [&](int, bool ok, uint4 xv, uint4) {
     float f[8];
-    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
-    s[0] += (f[0] + f[1]) + (f[2] + f[3]);
-    s[1] += (f[4] + f[5]) + (f[6] + f[7]);
-  }
-  slab_reduce<2>(s, red);
+    unpack8(xv, f);
+    if (ok) {
+      s[0] += (f[0] + f[1]) + (f[2] + f[3]);
+      s[1] += (f[4] + f[5]) + (f[6] + f[7]);
+    }
+  });
+  slab_reduce<2, PLN>(s, red);
   if ((threadIdx.x >> 3) == 0) {
     hs[2 * gq] = s[0];
     hs[2 * gq + 1] = s[1];
   }
   __syncthreads();
-  const float inv_cnt = 1.0f / (float)((int64_t)p.HW * p.cpg);
+  const float inv_cnt = 1.0f / (float)((int64_t)HW * p.cpg);
   const float mu[2] = {group_sum(hs, 2 * gq, p.cpg) * inv_cnt,
                        group_sum(hs, 2 * gq + 1, p.cpg) * inv_cnt};
   __syncthreads();
 
   // pass 2: biased variance around the mean
   float q[2] = {0.f, 0.f};
-  for (int px = pl; px < p.HW; px += 32) {
+  gn_pixels<PLN, 1, kGnUnrollFwd>(xsrc, p.C, pl, HW, [&](int, bool ok, uint4 xv, uint4) {
     float f[8];
-    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
+    unpack8(xv, f);
+    if (ok) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float d = f[e] - mu[e >> 2];
-      q[e >> 2] += d * d;
+      for (int e = 0; e < 8; ++e) {
+        const float d = f[e] - mu[e >> 2];
+        q[e >> 2] += d * d;
+      }
     }
-  }
-  slab_reduce<2>(q, red);
+  });
+  slab_reduce<2, PLN>(q, red);
   if ((threadIdx.x >> 3) == 0) {
     hs[2 * gq] = q[0];
     hs[2 * gq + 1] = q[1];
@@ -148,8 +190,7 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p)
   float a[8], b[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float gm = p.gamma[ch + e];
-    a[e] = gm;
+    a[e] = p.gamma[ch + e];
     b[e] = p.beta[ch + e];
   }
   float fsc[8], fsh[8];
@@ -160,10 +201,10 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p)
       fsh[e] = p.fb[(int64_t)n * p.C + ch + e];
     }
   }
-  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
-  for (int px = pl; px < p.HW; px += 32) {
+  uint16_t* ob = p.out + (int64_t)n * HW * p.C + ch;
+  gn_pixels<PLN, 1, kGnUnrollFwd>(xsrc, p.C, pl, HW, [&](int px, bool ok, uint4 xv, uint4) {
     float f[8];
-    unpack8(*reinterpret_cast<const uint4*>(xb + (int64_t)px * p.C), f);
+    unpack8(xv, f);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -177,8 +218,8 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p)
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
-    *reinterpret_cast<uint4*>(ob + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
-  }
+    if (ok) *reinterpret_cast<uint4*>(ob + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+  });
 }
 
 // Backward. With zp = film? fs*z + fb : z (z = GN output), u = silu(zp):
@@ -186,15 +227,17 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_fwd_kernel(const GnArgs p)
 //   dfs = sum_hw g * z,  dfb = sum_hw g;   gz = film? g * fs : g
 //   dgamma += sum gz * xhat, dbeta += sum gz;   gxh = gz * gamma
 //   dx = rstd * (gxh - mean_grp(gxh) - xhat * mean_grp(gxh * xhat))
-__global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p) {
-  __shared__ float red[4 * 8 * 32];
+template <int PLN>
+__global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
+  __shared__ float red[(PLN / 8) * 8 * 32];
   __shared__ float hs[2][16];
   const int n = blockIdx.y;
   const int c0 = blockIdx.x * kSlab;
   const int gq = threadIdx.x & 7;
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
-  const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const int HW = p.HW;
+  const int64_t base = (int64_t)n * HW * p.C + ch;
 
   float mu[2], rs[2];
 #pragma unroll
@@ -218,31 +261,34 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
-  for (int px = pl; px < p.HW; px += 32) {
+  const uint16_t* const srcs[2] = {p.x + base, p.dout + base};
+  gn_pixels<PLN, 2, kGnUnrollBwd>(srcs, p.C, pl, HW, [&](int, bool ok, uint4 xv, uint4 dv) {
     float f[8], d[8];
-    unpack8(*reinterpret_cast<const uint4*>(p.x + base + (int64_t)px * p.C), f);
-    unpack8(*reinterpret_cast<const uint4*>(p.dout + base + (int64_t)px * p.C), d);
+    unpack8(xv, f);
+    unpack8(dv, d);
+    if (ok) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xh = (f[e] - mu[e >> 2]) * rs[e >> 2];
-      const float z = xh * gm[e] + bt[e];
-      const float zp = fsc[e] * z + fsh[e];
-      const float sg = 1.0f / (1.0f + expf(-zp));
-      const float g = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
-      const float gz = g * fsc[e];
-      acc[0][e] += gz;
-      acc[1][e] += gz * xh;
-      acc[2][e] += g * z;
-      acc[3][e] += g;
+      for (int e = 0; e < 8; ++e) {
+        const float xh = (f[e] - mu[e >> 2]) * rs[e >> 2];
+        const float z = xh * gm[e] + bt[e];
+        const float zp = fsc[e] * z + fsh[e];
+        const float sg = 1.0f / (1.0f + expf(-zp));
+        const float g = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
+        const float gz = g * fsc[e];
+        acc[0][e] += gz;
+        acc[1][e] += gz * xh;
+        acc[2][e] += g * z;
+        acc[3][e] += g;
+      }
     }
-  }
+  });
   // reduce the 32 per-channel sums over pixel lanes
   {
     float* v = &acc[0][0];
     float tmp[32];
 #pragma unroll
     for (int k = 0; k < 32; ++k) tmp[k] = v[k];
-    slab_reduce<32>(tmp, red);
+    slab_reduce<32, PLN>(tmp, red);
 #pragma unroll
     for (int k = 0; k < 32; ++k) v[k] = tmp[k];
   }
@@ -272,7 +318,7 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
     hs[1][2 * gq + 1] = h2[1];
   }
   __syncthreads();
-  const float inv_cnt = 1.0f / (float)((int64_t)p.HW * p.cpg);
+  const float inv_cnt = 1.0f / (float)((int64_t)HW * p.cpg);
   float m1[2], m2[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -281,10 +327,10 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
   }
 
   // pass 2: dx
-  for (int px = pl; px < p.HW; px += 32) {
+  gn_pixels<PLN, 2, kGnUnrollBwd>(srcs, p.C, pl, HW, [&](int px, bool ok, uint4 xv, uint4 dv) {
     float f[8], d[8];
-    unpack8(*reinterpret_cast<const uint4*>(p.x + base + (int64_t)px * p.C), f);
-    unpack8(*reinterpret_cast<const uint4*>(p.dout + base + (int64_t)px * p.C), d);
+    unpack8(xv, f);
+    unpack8(dv, d);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -303,8 +349,8 @@ __global__ __launch_bounds__(kGnThreads) void gn_silu_bwd_kernel(const GnArgs p)
       }
       o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
     }
-    *reinterpret_cast<uint4*>(p.out + base + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
-  }
+    if (ok) *reinterpret_cast<uint4*>(p.out + base + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+  });
 }
 
 // dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c], summed in image order
@@ -336,6 +382,9 @@ __global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __res
   }
 }
 
+// Pixel lanes per workgroup: enough that every lane has a few pixels to stream.
+static int gn_pixel_lanes(int HW) { return HW >= 1024 ? 128 : (HW >= 256 ? 64 : 32); }
+
 static bool gn_shape_ok(int N, int HW, int C, int G) {
   if (N <= 0 || HW <= 0 || C <= 0 || G <= 0) return false;
   if (C % G != 0 || C % kSlab != 0) return false;
@@ -366,7 +415,13 @@ extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const flo
   a.rstd = rstd;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = eps;
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  gn_silu_fwd_kernel<<<grid, kGnThreads, 0, (hipStream_t)stream>>>(a);
+  const int pln = gn_pixel_lanes(HW);
+  if (pln == 128)
+    gn_silu_fwd_kernel<128><<<grid, 8 * 128, 0, (hipStream_t)stream>>>(a);
+  else if (pln == 64)
+    gn_silu_fwd_kernel<64><<<grid, 8 * 64, 0, (hipStream_t)stream>>>(a);
+  else
+    gn_silu_fwd_kernel<32><<<grid, 8 * 32, 0, (hipStream_t)stream>>>(a);
   return launch_status();
 }
 
@@ -408,7 +463,13 @@ extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  gn_silu_bwd_kernel<<<grid, kGnThreads, 0, s>>>(a);
+  const int pln = gn_pixel_lanes(HW);
+  if (pln == 128)
+    gn_silu_bwd_kernel<128><<<grid, 8 * 128, 0, s>>>(a);
+  else if (pln == 64)
+    gn_silu_bwd_kernel<64><<<grid, 8 * 64, 0, s>>>(a);
+  else
+    gn_silu_bwd_kernel<32><<<grid, 8 * 32, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
   gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 256, 0, s>>>((const float*)workspace,

@@ -205,31 +205,37 @@ class ResidualBlock(nn.Module):
 class _Attention(torch.autograd.Function):
     """softmax(q k^T / sqrt(d)) v over [B*heads, L, d] with dense batched products only.
 
-    Every right operand handed to bmm is a contiguous tensor (the transposes are
-    materialised), and the softmax and its gradient run in float32."""
+    No operand of a batched product is a transposed view (transposes are materialised on the
+    small [B, d, L] side, and the two products whose natural form has a transposed L x L
+    operand are computed transposed). The softmax and its gradient take bf16 scores and
+    work in float32 inside torch's kernels, so no float32 L x L tensor is written. The scale
+    is folded into q (and k in the backward); for d a power of four it is a power of two and
+    the fold is exact."""
 
     @staticmethod
     def forward(ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         scale = 1.0 / math.sqrt(q.shape[-1])
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        s = torch.bmm(q, k.transpose(1, 2).contiguous()).float() * scale
-        p = torch.softmax(s, dim=-1)
-        pl = p.to(q.dtype)
-        o = torch.bmm(pl, v)
-        ctx.save_for_backward(q, k, v, pl)
+        # autocast would run the softmax on a float32 copy of the scores
+        with torch.autocast(device_type="cuda", enabled=False):
+            qs = (q * scale).contiguous()
+            k, v = k.contiguous(), v.contiguous()
+            s = torch.bmm(qs, k.transpose(1, 2).contiguous())
+            p = torch.softmax(s, dim=-1)
+            o = torch.bmm(p, v)
+        ctx.save_for_backward(qs, k, v, p)
         ctx.scale = scale
         return o
 
     @staticmethod
     def backward(ctx: Any, do: torch.Tensor):
-        q, k, v, pl = ctx.saved_tensors
-        do = do.to(q.dtype).contiguous()
-        dv = torch.bmm(pl.transpose(1, 2).contiguous(), do)
-        dp = torch.bmm(do, v.transpose(1, 2).contiguous()).float()
-        p = pl.float()
-        ds = (p * (dp - (dp * p).sum(-1, keepdim=True)) * ctx.scale).to(q.dtype)
-        dq = torch.bmm(ds, k)
-        dk = torch.bmm(ds.transpose(1, 2).contiguous(), q)
+        qs, k, v, p = ctx.saved_tensors
+        with torch.autocast(device_type="cuda", enabled=False):
+            do = do.to(qs.dtype).contiguous()
+            dv = torch.bmm(do.transpose(1, 2).contiguous(), p).transpose(1, 2)   # (p^T do)
+            dp = torch.bmm(do, v.transpose(1, 2).contiguous())
+            ds = torch._softmax_backward_data(dp, p, -1, p.dtype)
+            dq = torch.bmm(ds, (k * ctx.scale).contiguous())
+            dk = torch.bmm(qs.transpose(1, 2).contiguous(), ds).transpose(1, 2)  # (ds^T qs)
         return dq, dk, dv
 
 
