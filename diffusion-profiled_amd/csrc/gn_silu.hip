@@ -218,7 +218,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
-    if (ok) *reinterpret_cast<uint4*>(ob + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+    if (ok) st_nt16(ob + (int64_t)px * p.C, uint4{o[0], o[1], o[2], o[3]});
   });
 }
 
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
       }
       o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
     }
-    if (ok) *reinterpret_cast<uint4*>(p.out + base + (int64_t)px * p.C) = uint4{o[0], o[1], o[2], o[3]};
+    if (ok) st_nt16(p.out + base + (int64_t)px * p.C, uint4{o[0], o[1], o[2], o[3]});
   });
 }
 

@@ -23,7 +23,9 @@
 // ((row ^ (row >> 3)) & 7), conflict-free for the 16-row fragment reads.
 // Epilogue per finished tile, per wave, while the next tile's DMA is in flight:
 //   out = bf16(RN32(acc * RN32(sa * sb)) [+ bias]), staged through the wave's private 2 KB
-// LDS slot so every pixel's 64 channels leave as one 128-B run.
+// LDS slot so every pixel's 64 channels leave as one 128-B run, with nontemporal stores (the
+// output is not read again by this kernel; plain stores left the next launch's first loads
+// queued behind write-backs).
 #include "dpa_common.hpp"
 
 namespace dpa {
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
         const int r = c >> 3, g = c & 7;
         const uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((g ^ (r & 7)) * 16));
         const int m = m0 + wm * kWTM + pj * 16 + r;
-        if (m < p.M) *reinterpret_cast<uint4*>(p.out + out_offset(p, m) + c0 + g * 8) = v;
+        if (m < p.M) st_nt16(p.out + out_offset(p, m) + c0 + g * 8, v);
       }
     }
 #pragma unroll
