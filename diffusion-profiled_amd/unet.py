@@ -12,8 +12,9 @@ underneath differs:
   run as one fused HIP kernel each way (``gn_silu``).
 * With ``UNetConfig.fp8_linears`` the bias-free linears (time MLP, FiLM projection, qkv, out)
   and the 1x1 skip convs use the FP8 GEMM with current scaling.
-* Attention (diffusion/unet.py:181-203) is written out with batched products on dense
-  operands (no transposed views) and a float32 softmax.
+* Attention (diffusion/unet.py:181-203) is the reference's ``scaled_dot_product_attention``
+  on the GPU, limited to its fused kernels; ``_Attention`` (dense batched products, no
+  transposed-view operands) serves the CPU.
 
 The torch ops around them (LayerNorm, interpolate, concat, the 3->128 and 128->3 convs whose
 channel counts the FP8 kernels do not take) stay in PyTorch-ROCm, as in the reference.
@@ -239,6 +240,19 @@ class _Attention(torch.autograd.Function):
         return dq, dk, dv
 
 
+_GPU_SDPA = True  # False: the dense formulation below on the GPU too
+
+
+def _fused_sdpa():
+    """SDPA restricted to the memory-efficient and flash kernels (preferred in that order)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    backends = [SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]
+    try:
+        return sdpa_kernel(backends, set_priority=True)
+    except TypeError:  # older torch: no priority argument
+        return sdpa_kernel(backends)
+
+
 class CHWAttention(nn.Module):
     """diffusion/unet.py:164-203."""
 
@@ -267,8 +281,18 @@ class CHWAttention(nn.Module):
             return t.reshape(b, h * w, self.nh, hd).transpose(1, 2).reshape(b * self.nh, h * w, hd)
 
         dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else q.dtype
-        o = _Attention.apply(heads(q).to(dt), heads(k).to(dt), heads(v).to(dt))
-        o = o.reshape(b, self.nh, h * w, hd).transpose(1, 2).reshape(b, h * w, c)
+        if _on_gpu(x) and _GPU_SDPA:
+            # the reference's F.scaled_dot_product_attention (diffusion/unet.py:196), limited to
+            # the fused (memory-efficient / flash) kernels: the math fallback would run bf16
+            # batched products on transposed views
+            def bnld(t):                                           # b l (nh hd) -> b nh l hd
+                return t.reshape(b, h * w, self.nh, hd).transpose(1, 2).to(dt)
+            with _fused_sdpa():
+                o = F.scaled_dot_product_attention(bnld(q), bnld(k), bnld(v))
+            o = o.transpose(1, 2).reshape(b, h * w, c)
+        else:
+            o = _Attention.apply(heads(q).to(dt), heads(k).to(dt), heads(v).to(dt))
+            o = o.reshape(b, self.nh, h * w, hd).transpose(1, 2).reshape(b, h * w, c)
         o = self.out(o)
         out = o.reshape(b, h, w, c).permute(0, 3, 1, 2) + resid
         return out / math.sqrt(2.0)
