@@ -24,6 +24,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
     ),
+    "dpa_quantize_fp8_delayed_window_bf16": (
+        c_int,
+        [c_void_p, c_int64] + [c_void_p] * 5 + [c_int64, c_int, c_void_p, c_int64, c_void_p],
+    ),
+    "dpa_window_max3_f32": (c_int, [c_void_p] * 3 + [c_int64, c_void_p, c_void_p]),
     "dpa_conv2d_fwd_fp8": (
         c_int,
         [c_void_p] * 6 + [c_int] * 9 + [c_void_p],

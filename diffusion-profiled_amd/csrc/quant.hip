@@ -161,12 +161,68 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
-// Delayed scaling, finalize: cur_scale = scale(max(partials))  (finalize_amax_kernel).
+// Amax-window state of a delayed-scaling module (diffusion/unet.py:82-91 and
+// diffusion/fp8_kernels.py:888-889): window[pos] = scale and, for the last tensor of the
+// forward, pos = (pos + 1) % len. A pos outside [0, len) (never produced by this update)
+// leaves both untouched. Called by one thread.
+__device__ __forceinline__ void window_record(float scale, float* window, int64_t* pos,
+                                              int64_t len, int advance) {
+  if (!window) return;
+  const int64_t p = *pos;
+  if (p < 0 || p >= len) return;
+  window[p] = scale;
+  if (advance) *pos = p + 1 == len ? 0 : p + 1;
+}
+
+// Delayed scaling, finalize: cur_scale = scale(max(partials))  (finalize_amax_kernel), and
+// the optional window update.
 __global__ __launch_bounds__(kQThreads) void finalize_scale_kernel(
-    const uint32_t* __restrict__ partials, int np, float* __restrict__ scale_out) {
+    const uint32_t* __restrict__ partials, int np, float* __restrict__ scale_out,
+    float* __restrict__ window, int64_t* __restrict__ pos, int64_t len, int advance) {
   __shared__ uint32_t red[kQThreads / 64];
   const uint32_t amax_bits = reduce_partials(partials, np, red);
-  if (threadIdx.x == 0) *scale_out = scale_from_amax_bits(amax_bits);
+  if (threadIdx.x == 0) {
+    const float cur = scale_from_amax_bits(amax_bits);
+    *scale_out = cur;
+    window_record(cur, window, pos, len, advance);
+  }
+}
+
+// torch.max of each of three fp32 windows (diffusion/unet.py:72-73, fp8_kernels.py:849):
+// one workgroup per window; NaN if the window holds a NaN, as torch.max.
+__global__ __launch_bounds__(kQThreads) void window_max3_kernel(const float* __restrict__ w0,
+                                                                const float* __restrict__ w1,
+                                                                const float* __restrict__ w2,
+                                                                int64_t n, float* __restrict__ out) {
+  __shared__ float redm[kQThreads / 64];
+  __shared__ int redn[kQThreads / 64];
+  const float* w = blockIdx.x == 0 ? w0 : (blockIdx.x == 1 ? w1 : w2);
+  float m = -INFINITY;
+  int nan = 0;
+  for (int64_t i = threadIdx.x; i < n; i += kQThreads) {
+    const float v = w[i];
+    nan |= v != v;
+    m = fmaxf(m, v);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, o, 64));
+    nan |= __shfl_xor(nan, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    redm[threadIdx.x >> 6] = m;
+    redn[threadIdx.x >> 6] = nan;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kQThreads / 64; ++k) {
+      m = fmaxf(m, redm[k]);
+      nan |= redn[k];
+    }
+    m = fmaxf(m, redm[0]);
+    nan |= redn[0];
+    out[blockIdx.x] = nan ? __builtin_nanf("") : m;
+  }
 }
 
 // Small tensors (weights): one workgroup does amax and cast in a single launch; the second
@@ -177,7 +233,8 @@ constexpr int64_t kSmallMaxN = 1 << 14;
 template <bool kDelayed>
 __global__ __launch_bounds__(kSmallThreads) void quant_small_kernel(
     const uint16_t* __restrict__ x, int64_t n, const float* __restrict__ prev_scale,
-    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+    uint8_t* __restrict__ q, float* __restrict__ scale_out, float* __restrict__ window,
+    int64_t* __restrict__ pos, int64_t len, int advance) {
   __shared__ uint32_t red[kSmallThreads / 64];
   const float prev = kDelayed ? *prev_scale : 0.0f;  // read before scale_out is written
   const int64_t n16 = n & ~(int64_t)15;
@@ -200,7 +257,10 @@ __global__ __launch_bounds__(kSmallThreads) void quant_small_kernel(
   for (int w = 1; w < kSmallThreads / 64; ++w) amax = amax > red[w] ? amax : red[w];
   const float cur = scale_from_amax_bits(amax);
   const float scale = kDelayed ? prev : cur;
-  if (threadIdx.x == 0) *scale_out = cur;
+  if (threadIdx.x == 0) {
+    *scale_out = cur;
+    window_record(cur, window, pos, len, advance);
+  }
   const float r = quant_recip(scale);
   for (int64_t i = (int64_t)threadIdx.x * 16; i < n16; i += kSmallThreads * 16) {
     const uint4 v0 = *reinterpret_cast<const uint4*>(x + i);
@@ -248,7 +308,8 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
   auto* xp = (const uint16_t*)x;
   auto* part = (uint32_t*)workspace;
   if (vec && n <= kSmallMaxN) {
-    quant_small_kernel<false><<<1, kSmallThreads, 0, s>>>(xp, n, nullptr, (uint8_t*)q, scale_out);
+    quant_small_kernel<false><<<1, kSmallThreads, 0, s>>>(xp, n, nullptr, (uint8_t*)q, scale_out,
+                                                           nullptr, nullptr, 0, 0);
   } else if (vec) {
     amax_partials_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, part);
     cast_current_kernel<true><<<gc, kQThreads, 0, s>>>(xp, n, part, np, (uint8_t*)q, scale_out);
@@ -260,9 +321,10 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
   return launch_status();
 }
 
-extern "C" int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const float* prev_scale,
-                                             void* q, float* cur_scale_out, void* workspace,
-                                             int64_t workspace_bytes, void* stream) {
+static int quantize_delayed(const void* x, int64_t n, const float* prev_scale, void* q,
+                            float* cur_scale_out, float* window, int64_t* window_pos,
+                            int64_t window_len, int advance, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
   if (!x || !q || !prev_scale || !cur_scale_out) return DPA_ERR_NULL;
   if (n <= 0) return DPA_ERR_SIZE;
   if (!workspace || workspace_bytes < dpa_quant_workspace_bytes(n)) return DPA_ERR_WORKSPACE;
@@ -276,13 +338,45 @@ extern "C" int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const flo
   auto* part = (uint32_t*)workspace;
   if (vec && n <= kSmallMaxN) {
     quant_small_kernel<true><<<1, kSmallThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q,
-                                                          cur_scale_out);
+                                                          cur_scale_out, window, window_pos,
+                                                          window_len, advance);
     return launch_status();
   }
   if (vec)
     cast_delayed_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part);
   else
     cast_delayed_kernel<false><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part);
-  finalize_scale_kernel<<<1, kQThreads, 0, s>>>(part, np, cur_scale_out);
+  finalize_scale_kernel<<<1, kQThreads, 0, s>>>(part, np, cur_scale_out, window, window_pos,
+                                                 window_len, advance);
+  return launch_status();
+}
+
+extern "C" int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const float* prev_scale,
+                                             void* q, float* cur_scale_out, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+  return quantize_delayed(x, n, prev_scale, q, cur_scale_out, nullptr, nullptr, 0, 0, workspace,
+                          workspace_bytes, stream);
+}
+
+extern "C" int dpa_quantize_fp8_delayed_window_bf16(const void* x, int64_t n,
+                                                    const float* prev_scale, void* q,
+                                                    float* cur_scale_out, float* window,
+                                                    int64_t* window_pos, int64_t window_len,
+                                                    int advance_pos, void* workspace,
+                                                    int64_t workspace_bytes, void* stream) {
+  if (!window || !window_pos) return DPA_ERR_NULL;
+  if (window_len <= 0) return DPA_ERR_SIZE;
+  if (!aligned(window, 4) || !aligned(window_pos, 8)) return DPA_ERR_ALIGN;
+  return quantize_delayed(x, n, prev_scale, q, cur_scale_out, window, window_pos, window_len,
+                          advance_pos ? 1 : 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dpa_window_max3_f32(const float* w0, const float* w1, const float* w2, int64_t n,
+                                   float* out3, void* stream) {
+  if (!w0 || !w1 || !w2 || !out3) return DPA_ERR_NULL;
+  if (n <= 0) return DPA_ERR_SIZE;
+  if (!aligned(w0, 4) || !aligned(w1, 4) || !aligned(w2, 4) || !aligned(out3, 4))
+    return DPA_ERR_ALIGN;
+  window_max3_kernel<<<3, kQThreads, 0, (hipStream_t)stream>>>(w0, w1, w2, n, out3);
   return launch_status();
 }

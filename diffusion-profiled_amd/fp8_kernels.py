@@ -136,6 +136,43 @@ def _quantize_impl(tensor: torch.Tensor, prev_scale: torch.Tensor | None) -> tup
     return quantized, scale
 
 
+def quantize_fp8_delayed_window(tensor: torch.Tensor, prev_scale: torch.Tensor,
+                                window: torch.Tensor, window_pos: torch.Tensor,
+                                advance: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """``quantize_fp8_delayed`` plus the module's amax-window update in the same launches:
+    ``window[window_pos] = cur_scale`` and, if ``advance``, ``window_pos = (window_pos + 1) %
+    len(window)`` (diffusion/unet.py:82-91, fp8_kernels.py:888-889)."""
+    assert tensor.dtype == torch.bfloat16 and tensor.is_cuda, f"{tensor.dtype} {tensor.is_cuda}"
+    torch_checks_scale(prev_scale, tensor.device)
+    assert window.dtype == torch.float32 and window.is_cuda and window.is_contiguous()
+    assert window_pos.dtype == torch.long and window_pos.is_cuda and window_pos.numel() == 1
+    if not _dense(tensor):
+        tensor = tensor.contiguous()
+    n = tensor.numel()
+    quantized = torch.empty_like(tensor, dtype=FP8_DTYPE, memory_format=torch.preserve_format)
+    scale = torch.empty((), device=tensor.device, dtype=torch.float32)
+    ws_bytes = _lib.query("dpa_quant_workspace_bytes", n)
+    workspace = torch.empty(ws_bytes, device=tensor.device, dtype=torch.uint8)
+    _lib.call(
+        "dpa_quantize_fp8_delayed_window_bf16",
+        tensor.data_ptr(), n, prev_scale.data_ptr(), quantized.data_ptr(), scale.data_ptr(),
+        window.data_ptr(), window_pos.data_ptr(), window.numel(), 1 if advance else 0,
+        workspace.data_ptr(), ws_bytes, _stream(tensor),
+    )
+    return quantized, scale
+
+
+def window_max3(w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """``torch.stack([w0.max(), w1.max(), w2.max()])`` for three equal-length fp32 windows in
+    one launch (diffusion/unet.py:72-73, fp8_kernels.py:849)."""
+    for w in (w0, w1, w2):
+        assert w.dtype == torch.float32 and w.is_cuda and w.is_contiguous() and w.numel() == w0.numel()
+    out = torch.empty(3, device=w0.device, dtype=torch.float32)
+    _lib.call("dpa_window_max3_f32", w0.data_ptr(), w1.data_ptr(), w2.data_ptr(), w0.numel(),
+              out.data_ptr(), _stream(w0))
+    return out
+
+
 def quantize_fp8_delayed(tensor: torch.Tensor, prev_scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Tensorwise quantization from bfloat16 to fp8 with delay: cast with ``prev_scale`` and
     return the scale of the current amax (diffusion/fp8_kernels.py:518-556)."""
@@ -435,6 +472,45 @@ class Conv2dFP8Specialized(torch.autograd.Function):
         dx = conv2d_bwd_input_fp8_prequantized(dy_fp8, weight_fp8, dy_scale, weight_scale)
         dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale)
         return dx, dw, None, None, None
+
+
+class Conv2dFP8DelayedWindowed(torch.autograd.Function):
+    """Delayed-scaling FP8 3x3 conv with the module's amax-window bookkeeping inside: the same
+    arithmetic, saved tensors and window/position updates as ``Conv2dFP8.forward`` on top of
+    ``Conv2dFP8Specialized`` (diffusion/unet.py:69-91, fp8_kernels.py:845-889), with the three
+    window maxima in one launch and each window write riding on its quantization's finalize
+    launch instead of separate torch reductions, scatters and position arithmetic."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, win_acts: torch.Tensor,
+                win_weights: torch.Tensor, win_dy: torch.Tensor,
+                window_pos: torch.Tensor) -> torch.Tensor:
+        x = x.to(torch.bfloat16)
+        weight = weight.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        assert x.is_contiguous(memory_format=torch.channels_last)
+        hist = window_max3(win_acts, win_weights, win_dy)   # before this step's writes
+        x_scale, weight_scale, dy_scale = hist[0], hist[1], hist[2]
+        x_fp8, _ = quantize_fp8_delayed_window(x, x_scale, win_acts, window_pos, advance=False)
+        weight_fp8, _ = quantize_fp8_delayed_window(weight, weight_scale, win_weights, window_pos,
+                                                    advance=True)
+        ctx.dy_window = win_dy
+        ctx.window_pos = window_pos
+        ctx.save_for_backward(x_fp8, weight_fp8, x_scale, weight_scale, dy_scale)
+        return conv2d_fwd_fp8_prequantized(x_fp8, weight_fp8, x_scale, weight_scale)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor) -> Any:
+        dy = dy.contiguous(memory_format=torch.channels_last)
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+        x_fp8, weight_fp8, x_scale, weight_scale, dy_scale = ctx.saved_tensors
+        dy_fp8, _ = quantize_fp8_delayed_window(dy, dy_scale, ctx.dy_window, ctx.window_pos,
+                                                advance=False)
+        dx = conv2d_bwd_input_fp8_prequantized(dy_fp8, weight_fp8, dy_scale, weight_scale)
+        dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale)
+        return dx, dw, None, None, None, None
 
 
 def triton_conv2d_fp8(

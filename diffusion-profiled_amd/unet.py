@@ -63,7 +63,13 @@ def _on_gpu(x: torch.Tensor) -> bool:
 
 
 class Conv2dFP8(nn.Module):
-    """3x3 / stride 1 / pad 1 conv, FP8 when the shape allows (diffusion/unet.py:32-94)."""
+    """3x3 / stride 1 / pad 1 conv, FP8 when the shape allows (diffusion/unet.py:32-94).
+
+    In delayed mode the window maxima and window/position updates run inside
+    ``K.Conv2dFP8DelayedWindowed`` (same state machine, fewer launches);
+    ``fused_window_update = False`` selects the reference's op-by-op form."""
+
+    fused_window_update = True
 
     def __init__(
         self,
@@ -102,6 +108,10 @@ class Conv2dFP8(nn.Module):
             x = x.contiguous(memory_format=torch.channels_last)
             if self.scaling_type == "current":
                 return K.triton_conv2d_fp8(x, self.conv.weight)
+            if self.fused_window_update:
+                return K.Conv2dFP8DelayedWindowed.apply(
+                    x, self.conv.weight, self.amax_window_acts, self.amax_window_weights,
+                    self.amax_window_dy, self.window_pos)
             with torch.no_grad():
                 x_scale_hist = torch.max(self.amax_window_acts)
                 w_scale_hist = torch.max(self.amax_window_weights)

@@ -18,6 +18,9 @@
  * Reference interfaces replaced (fattorib/diffusion-profiled, diffusion/fp8_kernels.py):
  *   dpa_quantize_fp8_bf16          <- quantize_fp8                        :559-601 (K1+K2+K3)
  *   dpa_quantize_fp8_delayed_bf16  <- quantize_fp8_delayed                :518-556 (K4+K2)
+ *   dpa_quantize_fp8_delayed_window_bf16, dpa_window_max3_f32
+ *                                  <- the amax-window updates of diffusion/unet.py:72-91
+ *                                     and fp8_kernels.py:849, :888-889 (torch ops there)
  *   dpa_conv2d_fwd_fp8             <- conv2d_fwd_fp8_prequantized         :604-639 (K5)
  *   dpa_conv2d_dgrad_fp8           <- conv2d_bwd_input_fp8_prequantized   :671-709 (K6)
  *   dpa_conv2d_wgrad_fp8           <- conv2d_bwd_weight_fp8_prequantized  :723-808 (K7+K8+K9)
@@ -69,6 +72,23 @@ int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* scale_out,
 int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const float* prev_scale, void* q,
                                   float* cur_scale_out, void* workspace,
                                   int64_t workspace_bytes, void* stream);
+
+/* dpa_quantize_fp8_delayed_bf16 plus the amax-window update of the delayed-scaling module:
+ * window[*window_pos] <- cur_scale, then, if advance_pos, *window_pos <- (*window_pos + 1) %
+ * window_len (window_pos is the module's int64 position tensor). Replaces the
+ * scatter_ / add_ / remainder_ of diffusion/unet.py:82-91 (weights, acts) and
+ * diffusion/fp8_kernels.py:888-889 (dy); the window update rides on the finalize launch. */
+int dpa_quantize_fp8_delayed_window_bf16(const void* x, int64_t n, const float* prev_scale,
+                                         void* q, float* cur_scale_out, float* window,
+                                         int64_t* window_pos, int64_t window_len,
+                                         int advance_pos, void* workspace,
+                                         int64_t workspace_bytes, void* stream);
+
+/* out3[i] <- torch.max(w_i) over n floats, for three windows in one launch (NaN if a window
+ * holds one). Replaces the torch.max(amax_window_*) of diffusion/unet.py:72-73 and
+ * diffusion/fp8_kernels.py:849. */
+int dpa_window_max3_f32(const float* w0, const float* w1, const float* w2, int64_t n,
+                        float* out3, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * FP8 implicit-GEMM convolution, NHWC activations, OHWI weights, fp32 accumulation,

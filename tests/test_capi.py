@@ -64,6 +64,12 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_conv2d_fwd_fp8(fake, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 1, 1, 2, 0, nul) == -4
     assert lib.dpa_gemm_fp8(fake, fake, fake, fake, nul, fake, 16, 100, 128, nul) == -4
     assert lib.dpa_gn_silu_fwd_bf16(fake, fake, fake, nul, nul, fake, fake, fake, 1, 16, 96, 32, 1e-5, nul) == -4
+    assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, nul, fake, 4, 0,
+                                                    fake, 4096, nul) == -1
+    assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, fake, fake, 0, 0,
+                                                    fake, 4096, nul) == -2
+    assert lib.dpa_window_max3_f32(nul, fake, fake, 4, fake, nul) == -1
+    assert lib.dpa_window_max3_f32(fake, fake, fake, 0, fake, nul) == -2
     # workspace too small
     assert lib.dpa_quantize_fp8_bf16(fake, 16, fake, fake, fake, 8, nul) == -5
     assert lib.dpa_conv2d_dgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -5

@@ -6,6 +6,8 @@ the whole (bf16 x, scale) domain (65536 x 32639 pairs) against tests/golden/cast
 """
 from __future__ import annotations
 
+import math
+
 import os
 
 import numpy as np
@@ -101,6 +103,35 @@ def test_delayed(K):
         q, s = K.quantize_fp8_delayed(x.cuda(), torch.tensor(prev, device="cuda"))
         assert np.float32(s.item()) == s_ref
         np.testing.assert_array_equal(bits(q), q_ref)
+
+
+@pytest.mark.parametrize("n", [3000, 128 * 32 * 32 * 16])   # single-launch and two-pass paths
+def test_delayed_window_update(K, n):
+    """quantize_fp8_delayed_window: the same bytes and scale as quantize_fp8_delayed, plus
+    window[pos] = scale and pos advancing modulo the window length (diffusion/unet.py:86-91)."""
+    x = randn_bf16((n,), seed=n)
+    prev = torch.tensor(np.float32(0.02), device="cuda")
+    q0, s0 = K.quantize_fp8_tensor(x.cuda(), prev)
+    win = torch.full((4,), -1.0, device="cuda")
+    pos = torch.tensor(2, dtype=torch.long, device="cuda")
+    q1, s1 = K.quantize_fp8_delayed_window(x.cuda(), prev, win, pos, advance=False)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(q1), bits(q0))
+    assert s1.item() == s0.item()
+    assert win.cpu().tolist() == [-1.0, -1.0, s0.item(), -1.0] and int(pos) == 2
+    for expect_pos in (3, 0, 1, 2):                              # advance, wrapping at 4
+        K.quantize_fp8_delayed_window(x.cuda(), prev, win, pos, advance=True)
+        torch.cuda.synchronize()
+        assert int(pos) == expect_pos
+    assert win.cpu().tolist() == [s0.item()] * 4
+    # window maxima of three windows in one launch, as torch.max
+    w3 = [torch.rand(1024, device="cuda") for _ in range(3)]
+    w3[1][17] = 0.0
+    m = K.window_max3(*w3)
+    torch.cuda.synchronize()
+    assert m.cpu().tolist() == [float(w.max()) for w in w3]
+    w3[2][5] = float("nan")
+    assert math.isnan(K.window_max3(*w3)[2].item())
 
 
 def test_every_reachable_scale_current(L):

@@ -84,6 +84,32 @@ def test_conv_module_delayed_scaling_vs_oracle():
         assert_bf16_close(bits(dw), O.conv2d_wgrad(xq, dyq, xs_h, dys_h), f"dw {step}")
 
 
+def test_conv_module_fused_window_update_matches_op_by_op():
+    """The delayed-scaling module with its window bookkeeping fused into the quantization
+    launches equals the reference's op-by-op form (torch.max, scatter_, add_, remainder_)
+    bit for bit: windows, position, y, dx and dw over steps that wrap the window."""
+    torch.manual_seed(1)
+    a = U.Conv2dFP8(128, 128, True, "delayed", amax_history=3).cuda()
+    b = U.Conv2dFP8(128, 128, True, "delayed", amax_history=3).cuda()
+    b.load_state_dict(a.state_dict())
+    b.fused_window_update = False
+    for step in range(5):
+        x = randn_bf16((2, 128, 32, 32), seed=30 + step, std=0.5 + step)
+        dy = randn_bf16((2, 128, 32, 32), seed=40 + step, std=1e-2 * (step + 1))
+        outs = []
+        for mod in (a, b):
+            xd = x.cuda().contiguous(memory_format=torch.channels_last).requires_grad_()
+            mod.conv.weight.grad = None
+            y = mod(xd)
+            y.backward(dy.cuda().contiguous(memory_format=torch.channels_last))
+            outs.append((y.detach(), xd.grad, mod.conv.weight.grad.clone()))
+        torch.cuda.synchronize()
+        for name in ("amax_window_acts", "amax_window_weights", "amax_window_dy", "window_pos"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), (step, name)
+        for ta, tb in zip(*outs):
+            assert torch.equal(ta, tb), step
+
+
 def _cfg(**kw):
     base = dict(fp8_scaling_type="current", p_drop=0.0)
     base.update(kw)
