@@ -58,6 +58,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p] * 14 + [c_int64] + [c_int] * 4 + [c_void_p],
     ),
+    "dpa_gn_silu_film_fwd_bf16": (
+        c_int,
+        [c_void_p] * 7 + [c_int] * 4 + [c_float, c_void_p],
+    ),
+    "dpa_gn_silu_film_bwd_bf16": (
+        c_int,
+        [c_void_p] * 12 + [c_int64] + [c_int] * 4 + [c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

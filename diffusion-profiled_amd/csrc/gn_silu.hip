@@ -32,6 +32,8 @@ struct GnArgs {
   float* part;  // bwd: [2][N][C] per-image channel sums of dgamma / dbeta
   float* dfs;   // bwd: FiLM gradients [N][C] or null
   float* dfb;
+  const uint16_t* wb;  // or FiLM from the bf16 time projection [N][2C]: scale bf16(w + 1), shift b
+  uint16_t* dwb;       // bwd: its gradient [N][2C] bf16, or null
   int N, HW, C, G, cpg;
   float eps;
 };
@@ -84,6 +86,36 @@ __device__ __forceinline__ float group_sum(const float* hs, int half_idx, int cp
   float s = 0.f;
   for (int i = 0; i < hpg; ++i) s += hs[g0 + i];
   return s;
+}
+
+// FiLM scale/shift of channels ch..ch+7 of image n: fp32 [N][C] pairs, or the bf16 time
+// projection [N][2C] with scale bf16(w + 1) (the reference adds 1 in bf16) and shift b; no FiLM
+// gives 1 and 0.
+__device__ __forceinline__ bool load_film(const GnArgs& p, int n, int ch, float (&fsc)[8],
+                                          float (&fsh)[8]) {
+  if (p.fs) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      fsc[e] = p.fs[(int64_t)n * p.C + ch + e];
+      fsh[e] = p.fb[(int64_t)n * p.C + ch + e];
+    }
+    return true;
+  }
+  if (p.wb) {
+    const uint16_t* w = p.wb + (int64_t)n * 2 * p.C + ch;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      fsc[e] = bf16_bits_to_f32((uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(w[e]) + 1.0f));
+      fsh[e] = bf16_bits_to_f32(w[p.C + e]);
+    }
+    return true;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    fsc[e] = 1.0f;
+    fsh[e] = 0.0f;
+  }
+  return false;
 }
 
 // Pixel loop of a pass: lane pl visits pixels pl, pl + PLN, ... in groups of U whose 16-B
@@ -194,13 +226,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
     b[e] = p.beta[ch + e];
   }
   float fsc[8], fsh[8];
-  if (p.fs) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      fsc[e] = p.fs[(int64_t)n * p.C + ch + e];
-      fsh[e] = p.fb[(int64_t)n * p.C + ch + e];
-    }
-  }
+  const bool film = load_film(p, n, ch, fsc, fsh);
   uint16_t* ob = p.out + (int64_t)n * HW * p.C + ch;
   gn_pixels<PLN, 1, kGnUnrollFwd>(xsrc, p.C, pl, HW, [&](int px, bool ok, uint4 xv, uint4) {
     float f[8];
@@ -213,7 +239,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
       for (int k = 0; k < 2; ++k) {
         const int ee = e + k;
         float v = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
-        if (p.fs) v = fsc[ee] * v + fsh[ee];
+        if (film) v = fsc[ee] * v + fsh[ee];
         z[k] = v / (1.0f + expf(-v));
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
@@ -251,9 +277,8 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
   for (int e = 0; e < 8; ++e) {
     gm[e] = p.gamma[ch + e];
     bt[e] = p.beta[ch + e];
-    fsc[e] = p.fs ? p.fs[(int64_t)n * p.C + ch + e] : 1.0f;
-    fsh[e] = p.fs ? p.fb[(int64_t)n * p.C + ch + e] : 0.0f;
   }
+  load_film(p, n, ch, fsc, fsh);
 
   // pass 1: per-channel sums of gz, gz*xhat, g*z, g
   float acc[4][8];
@@ -303,6 +328,10 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
       if (p.dfs) {                      // FiLM gradients are per image: final here
         p.dfs[o] = acc[2][e];
         p.dfb[o] = acc[3][e];
+      } else if (p.dwb) {
+        const int64_t ob = (int64_t)n * 2 * p.C + ch + e;
+        p.dwb[ob] = (uint16_t)f32_to_bf16_bits(acc[2][e]);
+        p.dwb[ob + p.C] = (uint16_t)f32_to_bf16_bits(acc[3][e]);
       }
     }
     // group sums of gxh = gz*gamma and gxh*xhat, per 4-channel half
@@ -396,20 +425,20 @@ static bool gn_shape_ok(int N, int HW, int C, int G) {
 
 using namespace dpa;
 
-extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
-                                    const float* film_scale, const float* film_shift, void* out,
-                                    float* mean, float* rstd, int N, int HW, int C, int G,
-                                    float eps, void* stream) {
+static int gn_fwd(const void* x, const float* gamma, const float* beta, const float* film_scale,
+                  const float* film_shift, const void* film_wb, void* out, float* mean,
+                  float* rstd, int N, int HW, int C, int G, float eps, void* stream) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
-  if (!aligned(x, 16) || !aligned(out, 16)) return DPA_ERR_ALIGN;
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(film_wb, 2)) return DPA_ERR_ALIGN;
   GnArgs a{};
   a.x = (const uint16_t*)x;
   a.gamma = gamma;
   a.beta = beta;
   a.fs = film_scale;
   a.fb = film_shift;
+  a.wb = (const uint16_t*)film_wb;
   a.out = (uint16_t*)out;
   a.mean = mean;
   a.rstd = rstd;
@@ -425,27 +454,43 @@ extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const flo
   return launch_status();
 }
 
+extern "C" int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                                    const float* film_scale, const float* film_shift, void* out,
+                                    float* mean, float* rstd, int N, int HW, int C, int G,
+                                    float eps, void* stream) {
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, nullptr, out, mean, rstd, N, HW, C, G,
+                eps, stream);
+}
+
+extern "C" int dpa_gn_silu_film_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                                         const void* film_wb, void* out, float* mean, float* rstd,
+                                         int N, int HW, int C, int G, float eps, void* stream) {
+  if (!film_wb) return DPA_ERR_NULL;
+  return gn_fwd(x, gamma, beta, nullptr, nullptr, film_wb, out, mean, rstd, N, HW, C, G, eps,
+                stream);
+}
+
 extern "C" int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G) {
   (void)HW;
   (void)G;
   return (int64_t)2 * N * C * 4;
 }
 
-extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
-                                    const float* beta, const float* film_scale,
-                                    const float* film_shift, const float* mean,
-                                    const float* rstd, void* dx, float* dgamma, float* dbeta,
-                                    float* dfilm_scale, float* dfilm_shift, void* workspace,
-                                    int64_t workspace_bytes, int N, int HW, int C, int G,
-                                    void* stream) {
+static int gn_bwd(const void* x, const void* dout, const float* gamma, const float* beta,
+                  const float* film_scale, const float* film_shift, const void* film_wb,
+                  const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
+                  float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
+                  int64_t workspace_bytes, int N, int HW, int C, int G, void* stream) {
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (film_scale && (!dfilm_scale || !dfilm_shift)) return DPA_ERR_NULL;
+  if (film_wb && !dfilm_wb) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
   if (!workspace || workspace_bytes < dpa_gn_silu_bwd_workspace_bytes(N, HW, C, G))
     return DPA_ERR_WORKSPACE;
-  if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4))
+  if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4) ||
+      !aligned(film_wb, 2) || !aligned(dfilm_wb, 2))
     return DPA_ERR_ALIGN;
   GnArgs a{};
   a.x = (const uint16_t*)x;
@@ -454,12 +499,14 @@ extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float
   a.beta = beta;
   a.fs = film_scale;
   a.fb = film_shift;
+  a.wb = (const uint16_t*)film_wb;
   a.out = (uint16_t*)dx;
   a.mean = const_cast<float*>(mean);
   a.rstd = const_cast<float*>(rstd);
   a.part = (float*)workspace;
   a.dfs = film_scale ? dfilm_scale : nullptr;
   a.dfb = film_scale ? dfilm_shift : nullptr;
+  a.dwb = film_wb ? (uint16_t*)dfilm_wb : nullptr;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
@@ -475,4 +522,27 @@ extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float
   gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 256, 0, s>>>((const float*)workspace,
                                                                     dgamma, dbeta, N, C);
   return launch_status();
+}
+
+extern "C" int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                                    const float* beta, const float* film_scale,
+                                    const float* film_shift, const float* mean,
+                                    const float* rstd, void* dx, float* dgamma, float* dbeta,
+                                    float* dfilm_scale, float* dfilm_shift, void* workspace,
+                                    int64_t workspace_bytes, int N, int HW, int C, int G,
+                                    void* stream) {
+  return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, nullptr, mean, rstd, dx, dgamma,
+                dbeta, dfilm_scale, dfilm_shift, nullptr, workspace, workspace_bytes, N, HW, C, G,
+                stream);
+}
+
+extern "C" int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                                         const float* beta, const void* film_wb,
+                                         const float* mean, const float* rstd, void* dx,
+                                         float* dgamma, float* dbeta, void* dfilm_wb,
+                                         void* workspace, int64_t workspace_bytes, int N, int HW,
+                                         int C, int G, void* stream) {
+  if (!film_wb || !dfilm_wb) return DPA_ERR_NULL;
+  return gn_bwd(x, dout, gamma, beta, nullptr, nullptr, film_wb, mean, rstd, dx, dgamma, dbeta,
+                nullptr, nullptr, dfilm_wb, workspace, workspace_bytes, N, HW, C, G, stream);
 }

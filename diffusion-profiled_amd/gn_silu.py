@@ -105,5 +105,56 @@ class GroupNormSiLU(torch.autograd.Function):
         return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, gfs, gfb
 
 
+class GroupNormSiLUFilm(torch.autograd.Function):
+    """silu(bf16(w + 1) * GroupNorm(x) + b) with (w, b) = chunk(film_wb, 2, dim=1), the time
+    projection of diffusion/unet.py:157-159, read by the kernel in bf16; the backward returns
+    the gradient of film_wb [N, 2C, 1, 1] (bf16) directly."""
+
+    @staticmethod
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb):
+        n, c, h, w = x.shape
+        xb = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        wb = film_wb.contiguous()
+        assert wb.dtype == torch.bfloat16 and wb.numel() == n * 2 * c
+        out = torch.empty_like(xb, memory_format=torch.channels_last)
+        mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
+        rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
+        g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
+        _lib.call(
+            "dpa_gn_silu_film_fwd_bf16",
+            xb.data_ptr(), g32.data_ptr(), b32.data_ptr(), wb.data_ptr(), out.data_ptr(),
+            mean.data_ptr(), rstd.data_ptr(), n, h * w, c, groups, float(eps), _stream(xb),
+        )
+        ctx.groups = groups
+        ctx.x_dtype = x.dtype
+        ctx.wb_shape = film_wb.shape
+        ctx.save_for_backward(xb, gamma, beta, mean, rstd, wb)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout):
+        xb, gamma, beta, mean, rstd, wb = ctx.saved_tensors
+        n, c, h, w = xb.shape
+        dout = dout.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        dx = torch.empty_like(xb, memory_format=torch.channels_last)
+        dgamma = torch.empty(c, device=xb.device, dtype=torch.float32)
+        dbeta = torch.empty(c, device=xb.device, dtype=torch.float32)
+        dwb = torch.empty(ctx.wb_shape, device=xb.device, dtype=torch.bfloat16)
+        ws_bytes = _lib.query("dpa_gn_silu_bwd_workspace_bytes", n, h * w, c, ctx.groups)
+        ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
+        _lib.call(
+            "dpa_gn_silu_film_bwd_bf16",
+            xb.data_ptr(), dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+            beta.float().contiguous().data_ptr(), wb.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+            dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), dwb.data_ptr(), ws.data_ptr(),
+            ws_bytes, n, h * w, c, ctx.groups, _stream(xb),
+        )
+        return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, dwb
+
+
+def group_norm_silu_film(x, gamma, beta, groups: int, eps: float, film_wb):
+    return GroupNormSiLUFilm.apply(x, gamma, beta, groups, eps, film_wb)
+
+
 def group_norm_silu(x, gamma, beta, groups: int, eps: float = 1e-5, film_scale=None, film_shift=None):
     return GroupNormSiLU.apply(x, gamma, beta, groups, eps, film_scale, film_shift)

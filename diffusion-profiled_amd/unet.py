@@ -32,7 +32,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import fp8_kernels as K
-from .gn_silu import group_norm_silu, supported as gn_supported
+from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
 
 @dataclass
@@ -207,8 +207,14 @@ class ResidualBlock(nn.Module):
         resid = x
         x = self.conv_1(norm_silu(self.norm1, x, self.fused))
         wb = self.t_embed_wb(t)
-        w, b = torch.chunk(wb, chunks=2, dim=1)
-        h = norm_silu(self.norm2, x, self.fused, w + 1, b)
+        if (self.fused and _on_gpu(x) and wb.dtype == torch.bfloat16
+                and gn_supported(x.shape[1], self.norm2.num_groups)):
+            # the kernel reads (w, b) from wb and forms bf16(w + 1) itself
+            h = group_norm_silu_film(x, self.norm2.weight, self.norm2.bias,
+                                     self.norm2.num_groups, self.norm2.eps, wb)
+        else:
+            w, b = torch.chunk(wb, chunks=2, dim=1)
+            h = norm_silu(self.norm2, x, self.fused, w + 1, b)
         x = self.conv_2(self.dropout(h))
         return (self.skip_connection(resid) + x) / math.sqrt(2.0)
 

@@ -179,6 +179,20 @@ int dpa_gn_silu_bwd_bf16(const void* x, const void* dout, const float* gamma,
                          float* dbeta, float* dfilm_scale, float* dfilm_shift, void* workspace,
                          int64_t workspace_bytes, int N, int HW, int C, int G, void* stream);
 
+/* dpa_gn_silu_fwd_bf16 / _bwd with the FiLM taken straight from the bf16 time projection
+ * film_wb [N, 2C] of diffusion/unet.py:157-158 (w = film_wb[:, :C], b = film_wb[:, C:]):
+ * scale bf16(w + 1) (the reference's bf16 add), shift b. The backward writes the gradient of
+ * film_wb [N, 2C] in bf16 (the reference's chunk/add/dtype-cast backward, in place of three
+ * more launches). */
+int dpa_gn_silu_film_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                              const void* film_wb, void* out, float* mean, float* rstd, int N,
+                              int HW, int C, int G, float eps, void* stream);
+int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                              const float* beta, const void* film_wb, const float* mean,
+                              const float* rstd, void* dx, float* dgamma, float* dbeta,
+                              void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N,
+                              int HW, int C, int G, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,3 +148,33 @@ def test_gn_silu_cfg4_full_size_vs_torch_fp32(G):
                       (fb.grad, fbr.grad)):
         assert got.shape == want.shape
         assert nerr(got, want) < 1e-3
+
+
+@pytest.mark.parametrize("n,c,h,w", [(3, 256, 16, 16), (2, 128, 32, 32), (2, 512, 8, 8)])
+def test_gn_silu_film_from_time_projection_matches_split_form(G, n, c, h, w):
+    """GroupNormSiLUFilm (the kernel reads wb = [w | b] in bf16 and forms bf16(w + 1)) equals
+    GroupNormSiLU on the reference's w + 1 and b (diffusion/unet.py:157-159) bit for bit:
+    output, dx, dgamma, dbeta, and d(wb) = [d(w + 1) | d(b)] in bf16."""
+    g = torch.Generator().manual_seed(n + c)
+    x = (torch.randn((n, c, h, w), generator=g) * 2 + 0.5).to(torch.bfloat16)
+    gamma, beta, _, _ = params(c, n, c + 1, False)
+    wb = (0.3 * torch.randn((n, 2 * c, 1, 1), generator=g)).to(torch.bfloat16).cuda()
+    dout = randn_bf16((n, c, h, w), seed=c + 7)
+
+    xa = cl(x).requires_grad_()
+    ga, ba = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    wba = wb.clone().requires_grad_()
+    ya = G.group_norm_silu_film(xa, ga, ba, GROUPS, 1e-5, wba)
+    ya.backward(cl(dout))
+
+    xb = cl(x).requires_grad_()
+    gb, bb = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    wbb = wb.clone().requires_grad_()
+    wpart, bpart = torch.chunk(wbb, 2, dim=1)
+    yb = G.group_norm_silu(xb, gb, bb, GROUPS, 1e-5, wpart + 1, bpart)
+    yb.backward(cl(dout))
+    torch.cuda.synchronize()
+    for got, ref, what in ((ya, yb, "out"), (xa.grad, xb.grad, "dx"), (ga.grad, gb.grad, "dgamma"),
+                           (ba.grad, bb.grad, "dbeta"), (wba.grad, wbb.grad, "dwb")):
+        assert got.dtype == ref.dtype and got.shape == ref.shape, what
+        assert torch.equal(got.detach(), ref.detach()), what
