@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   issue(ig_st[2], 2);
   IG_STAMP(2);
   wait_vmcnt<2 * kLoadsPerStage>();
-  __builtin_amdgcn_s_barrier();
+  lds_barrier();
 #pragma unroll
   for (int i = 0; i < 4; ++i) fb[i] = ld_frag(ig_st[0] + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
 #pragma unroll
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int nx = cur == 2 ? 0 : cur + 1;
     wait_vmcnt<kLoadsPerStage>();
     wait_lgkmcnt0();
-    __builtin_amdgcn_s_barrier();
+    lds_barrier();
     const uint8_t* nxt = ig_st[nx];
 #pragma unroll
     for (int pj = 0; pj < 4; ++pj) {
