@@ -49,6 +49,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 6 + [c_int64] + [c_int] * 10 + [c_void_p],
     ),
     "dpa_gemm_fp8": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_conv2d_fwd_split_workspace_bytes": (c_int64, [c_int] * 9),
+    "dpa_conv2d_fwd_fp8_split": (
+        c_int,
+        [c_void_p] * 7 + [c_int64] + [c_int] * 9 + [c_void_p],
+    ),
+    "dpa_conv2d_dgrad_split_workspace_bytes": (c_int64, [c_int] * 9),
+    "dpa_conv2d_dgrad_fp8_wt_split": (
+        c_int,
+        [c_void_p] * 6 + [c_int64] + [c_int] * 9 + [c_void_p],
+    ),
+    "dpa_gemm_split_workspace_bytes": (c_int64, [c_int] * 3),
+    "dpa_gemm_fp8_split": (c_int, [c_void_p] * 7 + [c_int64] + [c_int] * 3 + [c_void_p]),
     "dpa_gn_silu_fwd_bf16": (
         c_int,
         [c_void_p] * 8 + [c_int] * 4 + [c_float, c_void_p],

@@ -59,12 +59,14 @@ struct IgemmArgs {
   int oy_step, oy_off, ox_step, ox_off;  // out pixel = (i*oy_step + oy_off, j*ox_step + ox_off)
   int iy_step, ix_step;                  // in pixel  = (i*iy_step + dy, j*ix_step + dx)
   int M;                                 // N * Pg * Qg
-  int tiles_n, tiles, tiles_per_xcd, wg_per_xcd;
+  int tiles_n, tiles, tiles_per_xcd, wg_per_xcd;  // tiles: work items (tiles x splits)
   // tap grid: tap (ty, tx), ty < ny, tx < nx: input offset (dy0 + ty*dys, dx0 + tx*dxs),
   // weight tap w0 + ty*wys + tx*wxs
   int ny, nx, dy0, dys, dx0, dxs, w0, wys, wxs;
-  int kc_per_tap, nk;  // K-steps per tap (C / 128) and per tile
-  FastDiv divQ, divP, divKC, divNX, divNK, divTN;
+  int kc_per_tap, nk;  // K-steps per tap (C / 128) and per work item (a tile's K range)
+  int splits;          // K ranges per tile: work item = (tile, split), item / splits = tile
+  float* partial;      // splits > 1: fp32 partial sums per work item, in accumulator order
+  FastDiv divQ, divP, divKC, divNX, divNK, divTN, divSP;
 };
 
 // 16 zero bytes: the DMA source for padding taps and rows past M.
@@ -124,8 +126,8 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   const int wn = wave / kWavesM;  // channel half (64 cols)
   const int frow = lane & 15, fq = lane >> 4;
 
-  // this workgroup's tiles: XCD x owns tiles [x*tiles_per_xcd, +tiles_per_xcd); its
-  // wg_per_xcd workgroups take them round-robin
+  // this workgroup's work items (tile, K range): XCD x owns items [x*tiles_per_xcd,
+  // +tiles_per_xcd); its wg_per_xcd workgroups take them round-robin
   const int xcd = blockIdx.x & 7;
   const int wi = blockIdx.x >> 3;
   const int t_begin = xcd * p.tiles_per_xcd + wi;
@@ -140,8 +142,11 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   // ---- DMA side: row metadata of the tile being loaded ----
   int a_off[kALoads], a_mask[kALoads], b_off[kBLoads];
   int dma_tile = -1;
+  int dma_k0 = 0;  // first global K-step of the item being loaded
   auto set_dma_tile = [&](int j) __attribute__((always_inline)) {
-    const int tile = t_begin + j * p.wg_per_xcd;
+    const int item = t_begin + j * p.wg_per_xcd;
+    const int tile = (int)fdiv((uint32_t)item, p.divSP);
+    dma_k0 = (item - tile * p.splits) * nk;
     const int tm = (int)fdiv((uint32_t)tile, p.divTN);
     const int tn = tile - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
@@ -183,11 +188,11 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const bool live = s < total;
     const int ss = live ? s : 0;
     const int j = (int)fdiv((uint32_t)ss, p.divNK);
-    const int k = ss - j * nk;
     if (live && j != dma_tile) {
       set_dma_tile(j);
       dma_tile = j;
     }
+    const int k = ss - j * nk + dma_k0;
     const int t = (int)fdiv((uint32_t)k, p.divKC);
     const int c0 = (k - t * p.kc_per_tap) * kBK;
     const int ty = (int)fdiv((uint32_t)t, p.divNX);
@@ -217,14 +222,30 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   v8i fa[4], fb[4];
 
-  // finished tile j: scale, bias, bf16 -> wave slot -> 128-B runs per pixel
+  // finished item j: scale, bias, bf16 -> wave slot -> 128-B runs per pixel; or, with
+  // split K, the raw fp32 sums of its K range as the accumulators hold them: item i's
+  // kBM x kBN block at partial + i * kBM * kBN, wave-major, then (pj, ci, lane), 16 B per
+  // lane, so every store instruction writes 1 KB contiguously
   auto epilogue = [&](int j) __attribute__((always_inline)) {
-    const int tile = t_begin + j * p.wg_per_xcd;
+    const int item = t_begin + j * p.wg_per_xcd;
+    const int tile = (int)fdiv((uint32_t)item, p.divSP);
     const int tm = (int)fdiv((uint32_t)tile, p.divTN);
     const int tn = tile - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
-    uint8_t* slot = ig_slot[wave];
     const int c0 = n0 + wn * kWTN;
+    if (p.splits > 1) {
+      float* part = p.partial + (int64_t)item * (kBM * kBN) + wave * (16 * 256) + lane * 4;
+#pragma unroll
+      for (int pj = 0; pj < 4; ++pj) {
+#pragma unroll
+        for (int ci = 0; ci < 4; ++ci) {
+          __builtin_nontemporal_store(acc[ci][pj], reinterpret_cast<v4f*>(part + (pj * 4 + ci) * 256));
+          acc[ci][pj] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      return;
+    }
+    uint8_t* slot = ig_slot[wave];
 #pragma unroll
     for (int pj = 0; pj < 4; ++pj) {
 #pragma unroll
@@ -321,6 +342,38 @@ __global__ __launch_bounds__(256) void weight_transpose_kernel(const uint8_t* __
   }
 }
 
+// Split-K finish: out = bf16(RN32(RN32(sum over splits, in order) * RN32(sa * sb)) [+ bias]).
+// Thread (tile, wave, pj, ci, lane) of the partial layout above sums the splits of one
+// accumulator block (1 KB-contiguous loads per wave) and writes pixel
+// m0 + 64 wm + 16 pj + frow, channels c0 + 16 ci + 4 fq .. +3. Grid: tiles x 8192 threads.
+constexpr int kRedThreadsPerTile = kWaves * 16 * 64;
+__global__ __launch_bounds__(256) void igemm_split_reduce_kernel(const IgemmArgs p) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int tile = t / kRedThreadsPerTile;
+  const int r = t - tile * kRedThreadsPerTile;
+  const int wave = r >> 10, pj = (r >> 8) & 3, ci = (r >> 6) & 3, lane = r & 63;
+  const int tm = (int)fdiv((uint32_t)tile, p.divTN);
+  const int tn = tile - tm * p.tiles_n;
+  const int m = tm * kBM + (wave % kWavesM) * kWTM + pj * 16 + (lane & 15);
+  if (m >= p.M) return;
+  const int c = tn * kBN + (wave / kWavesM) * kWTN + ci * 16 + 4 * (lane >> 4);
+  const float* q = p.partial + (int64_t)tile * p.splits * (kBM * kBN) + r * 4;
+  v4f acc = *reinterpret_cast<const v4f*>(q);
+  for (int sp = 1; sp < p.splits; ++sp)
+    acc = acc + *reinterpret_cast<const v4f*>(q + (int64_t)sp * (kBM * kBN));
+  const float scale = p.sa[0] * p.sb[0];
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = acc[e] * scale;
+    if (p.bias) v[e] = v[e] + p.bias[c + e];
+  }
+  uint2 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  st_nt8(p.out + out_offset(p, m) + c, o);
+}
+
 static int g_num_cus = 0;
 
 static int num_cus() {
@@ -335,34 +388,80 @@ static int num_cus() {
   return g_num_cus;
 }
 
-// act geometry (N, Hi, Wi, C), output geometry, tap grid already in `a`
-static int launch_igemm(IgemmArgs& a, int N, hipStream_t s) {
+// Split-K plan for a launch of `tiles` output tiles and nk K-steps per tile. Each split adds
+// a fixed cost per work item (pipeline fill, a 128 KB fp32 partial block written and read
+// back), so a split pays only when the tiles leave most CUs idle and each part keeps enough
+// K-steps. Measured on MI355X (event time, both kernels, 4x4 and 8x8 U-Net shapes): about six
+// K-steps per part is best once there are 16+ tiles, and tiny launches (fewer tiles) gain
+// from parts of two steps when the tile has at least eight. Picks the largest divisor d of
+// nk with nk / d >= that minimum and tiles * d <= CUs; 1 means no split. *bytes gets the
+// partial buffer it needs (one kBM x kBN fp32 block per work item).
+static int plan_splits(int tiles, int nk, int cus, int64_t* bytes) {
+  int best = 1;
+  if (nk >= 8 && tiles * 2 <= cus) {
+    const int min_steps = (tiles >= 16 && nk >= 12) ? 6 : 2;
+    for (int d = 2; d <= nk / min_steps; ++d)
+      if (nk % d == 0 && tiles * d <= cus) best = d;
+  }
+  *bytes = best > 1 ? (int64_t)best * tiles * kBM * kBN * 4 : 0;
+  return best;
+}
+
+static void finish_geometry(IgemmArgs& a) {
+  a.kc_per_tap = a.C / kBK;
+  a.nk = a.ny * a.nx * a.kc_per_tap;
+  a.tiles_n = a.Cout / kBN;
+}
+
+static int64_t igemm_workspace(IgemmArgs& a) {
+  if (a.M <= 0) return 0;
+  finish_geometry(a);
+  const int tiles = (int)ceil_div(a.M, kBM) * a.tiles_n;
+  int64_t bytes = 0;
+  plan_splits(tiles, a.nk, num_cus(), &bytes);
+  return bytes;
+}
+
+// act geometry (N, Hi, Wi, C), output geometry, tap grid already in `a`; split K when a
+// workspace of the planned size is given
+static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
+                        int64_t workspace_bytes) {
   if (a.M <= 0) return DPA_OK;
   const int64_t act_bytes = (int64_t)N * a.Hi * a.Wi * a.C;
   const int64_t wgt_bytes = (int64_t)a.Cout * a.T * a.C;
   const int64_t out_elems = (int64_t)N * a.Ho * a.Wo * a.Cout;
   if (act_bytes > kMaxOperandBytes || wgt_bytes > kMaxOperandBytes || out_elems > kMaxOperandBytes)
     return DPA_ERR_SIZE;
+  finish_geometry(a);
   const int tiles_m = (int)ceil_div(a.M, kBM);
-  a.tiles_n = a.Cout / kBN;
-  a.tiles = tiles_m * a.tiles_n;
+  const int tiles = tiles_m * a.tiles_n;
+  int64_t need = 0;
+  int splits = plan_splits(tiles, a.nk, num_cus(), &need);
+  if (splits > 1 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+    splits = 1;
+  a.splits = splits;
+  a.partial = (float*)workspace;
+  a.nk /= splits;
+  a.tiles = tiles * splits;
   a.tiles_per_xcd = (int)ceil_div(a.tiles, 8);
-  // one workgroup per CU (160 KB of LDS each), never more than there are tiles
+  // one workgroup per CU (160 KB of LDS each), never more than there are work items
   int grid = num_cus();
   grid = (grid / 8) * 8;
   if (grid < 8) grid = 8;
   const int max_grid = a.tiles_per_xcd * 8;
   if (grid > max_grid) grid = max_grid;
   a.wg_per_xcd = grid / 8;
-  a.kc_per_tap = a.C / kBK;
-  a.nk = a.ny * a.nx * a.kc_per_tap;
   a.divQ = make_fastdiv((uint32_t)a.Qg);
   a.divP = make_fastdiv((uint32_t)a.Pg);
   a.divKC = make_fastdiv((uint32_t)a.kc_per_tap);
   a.divNX = make_fastdiv((uint32_t)a.nx);
   a.divNK = make_fastdiv((uint32_t)a.nk);
   a.divTN = make_fastdiv((uint32_t)a.tiles_n);
+  a.divSP = make_fastdiv((uint32_t)a.splits);
   igemm_fp8_kernel<<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  int st = launch_status();
+  if (st != DPA_OK || splits == 1) return st;
+  igemm_split_reduce_kernel<<<(unsigned)(tiles * (kRedThreadsPerTile / 256)), 256, 0, s>>>(a);
   return launch_status();
 }
 
@@ -395,13 +494,8 @@ static bool use_hconv(int N, int H, int W, int C, int Cout, int R, int S, int st
   return R == 3 && S == 3 && stride == 1 && pad == 1 && hconv_supported(N, H, W, C, Cout);
 }
 
-static int conv_fwd(const void* xq, const void* wq, const float* xs, const float* ws,
-                    const float* bias, void* y, int N, int H, int W, int Cin, int Cout, int R,
-                    int S, int stride, int pad, hipStream_t s) {
-  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad))
-    return hconv_run(xq, wq, xs, ws, bias, y, N, H, W, Cin, Cout, 0, num_cus(), s);
-  IgemmArgs a{};
-  fill_common(a, xq, wq, y, xs, ws, bias);
+static void fwd_geometry(IgemmArgs& a, int N, int H, int W, int Cin, int Cout, int R, int S,
+                         int stride, int pad) {
   const int P = (H + 2 * pad - R) / stride + 1;
   const int Q = (W + 2 * pad - S) / stride + 1;
   a.Hi = H; a.Wi = W; a.C = Cin; a.Cout = Cout; a.T = R * S;
@@ -413,44 +507,86 @@ static int conv_fwd(const void* xq, const void* wq, const float* xs, const float
   a.ny = R; a.nx = S;
   a.dy0 = -pad; a.dys = 1; a.dx0 = -pad; a.dxs = 1;
   a.w0 = 0; a.wys = S; a.wxs = 1;
-  return launch_igemm(a, N, s);
+}
+
+static int conv_fwd(const void* xq, const void* wq, const float* xs, const float* ws,
+                    const float* bias, void* y, int N, int H, int W, int Cin, int Cout, int R,
+                    int S, int stride, int pad, hipStream_t s, void* workspace = nullptr,
+                    int64_t workspace_bytes = 0) {
+  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad))
+    return hconv_run(xq, wq, xs, ws, bias, y, N, H, W, Cin, Cout, 0, num_cus(), s);
+  IgemmArgs a{};
+  fill_common(a, xq, wq, y, xs, ws, bias);
+  fwd_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad);
+  return launch_igemm(a, N, s, workspace, workspace_bytes);
+}
+
+static int64_t conv_fwd_workspace(int N, int H, int W, int Cin, int Cout, int R, int S,
+                                  int stride, int pad) {
+  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad)) return 0;
+  IgemmArgs a{};
+  fwd_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad);
+  return igemm_workspace(a);
 }
 
 // dx[n, h, w, ci] = sum_{r,s,co} dy[n, (h+pad-r)/st, (w+pad-s)/st, co] * w[co, r, s, ci]
 // over the (r, s) for which the division is exact and in range: one launch per output
 // parity class (ay, ax); within a class the usable r (and s) form an arithmetic progression
 // of step `stride`, so the class's taps are again a linear grid.
+// Parity class (ay, ax) of the data gradient: the class's output pixels and taps.
+static int dgrad_geometry(IgemmArgs& a, int N, int H, int W, int Cin, int Cout, int R, int S,
+                      int stride, int pad, int ay, int ax) {
+  const int P = (H + 2 * pad - R) / stride + 1;
+  const int Q = (W + 2 * pad - S) / stride + 1;
+  a.Hi = P; a.Wi = Q; a.C = Cout; a.Cout = Cin; a.T = R * S;
+  a.Pg = (H - ay + stride - 1) / stride;
+  a.Qg = (W - ax + stride - 1) / stride;
+  a.Ho = H; a.Wo = W;
+  a.oy_step = stride; a.oy_off = ay; a.ox_step = stride; a.ox_off = ax;
+  a.iy_step = 1; a.ix_step = 1;
+  a.M = N * a.Pg * a.Qg;
+  // first r with (ay + pad - r) divisible by stride, then every stride-th
+  const int r0 = (ay + pad) % stride, s0 = (ax + pad) % stride;
+  a.ny = (R - r0 + stride - 1) / stride;
+  a.nx = (S - s0 + stride - 1) / stride;
+  if (a.ny <= 0 || a.nx <= 0 || a.M == 0) return DPA_ERR_SHAPE;
+  a.dy0 = (ay + pad - r0) / stride; a.dys = -1;
+  a.dx0 = (ax + pad - s0) / stride; a.dxs = -1;
+  a.w0 = r0 * S + s0; a.wys = stride * S; a.wxs = stride;
+  return DPA_OK;
+}
+
 static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const float* ws,
                       void* dx, int N, int H, int W, int Cin, int Cout, int R, int S,
-                      int stride, int pad, hipStream_t s) {
+                      int stride, int pad, hipStream_t s, void* workspace = nullptr,
+                      int64_t workspace_bytes = 0) {
   // the 3x3 / s1 / p1 data gradient is a conv of dy with the mirrored, transposed weight
   if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad))
     return hconv_run(dyq, wt, dys, ws, nullptr, dx, N, H, W, Cout, Cin, 1, num_cus(), s);
-  const int P = (H + 2 * pad - R) / stride + 1;
-  const int Q = (W + 2 * pad - S) / stride + 1;
   for (int ay = 0; ay < stride; ++ay)
     for (int ax = 0; ax < stride; ++ax) {
       IgemmArgs a{};
       fill_common(a, dyq, wt, dx, dys, ws, nullptr);
-      a.Hi = P; a.Wi = Q; a.C = Cout; a.Cout = Cin; a.T = R * S;
-      a.Pg = (H - ay + stride - 1) / stride;
-      a.Qg = (W - ax + stride - 1) / stride;
-      a.Ho = H; a.Wo = W;
-      a.oy_step = stride; a.oy_off = ay; a.ox_step = stride; a.ox_off = ax;
-      a.iy_step = 1; a.ix_step = 1;
-      a.M = N * a.Pg * a.Qg;
-      // first r with (ay + pad - r) divisible by stride, then every stride-th
-      const int r0 = (ay + pad) % stride, s0 = (ax + pad) % stride;
-      a.ny = (R - r0 + stride - 1) / stride;
-      a.nx = (S - s0 + stride - 1) / stride;
-      if (a.ny <= 0 || a.nx <= 0 || a.M == 0) return DPA_ERR_SHAPE;
-      a.dy0 = (ay + pad - r0) / stride; a.dys = -1;
-      a.dx0 = (ax + pad - s0) / stride; a.dxs = -1;
-      a.w0 = r0 * S + s0; a.wys = stride * S; a.wxs = stride;
-      int st = launch_igemm(a, N, s);
+      int st = dgrad_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad, ay, ax);
+      if (st != DPA_OK) return st;
+      st = launch_igemm(a, N, s, workspace, workspace_bytes);  // classes run in stream order
       if (st != DPA_OK) return st;
     }
   return DPA_OK;
+}
+
+static int64_t conv_dgrad_workspace(int N, int H, int W, int Cin, int Cout, int R, int S,
+                                    int stride, int pad) {
+  if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad)) return 0;
+  int64_t most = 0;
+  for (int ay = 0; ay < stride; ++ay)
+    for (int ax = 0; ax < stride; ++ax) {
+      IgemmArgs a{};
+      if (dgrad_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad, ay, ax) != DPA_OK) continue;
+      const int64_t b = igemm_workspace(a);
+      if (b > most) most = b;
+    }
+  return most;
 }
 
 }  // namespace dpa
@@ -519,4 +655,72 @@ extern "C" int dpa_gemm_fp8(const void* a, const void* b, const float* a_scale,
   // a linear is a 1x1 convolution over M "pixels" of K channels
   return conv_fwd(a, b, a_scale, b_scale, bias, c, M, 1, 1, K, N, 1, 1, 1, 0,
                   (hipStream_t)stream);
+}
+
+// ---- split-K variants: same results up to fp32 summation order, for launches whose output
+// tiles leave most CUs idle (small images, small batches) ----
+
+extern "C" int64_t dpa_conv2d_fwd_split_workspace_bytes(int N, int H, int W, int Cin, int Cout,
+                                                         int R, int S, int stride, int pad) {
+  if (!conv_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad)) return 0;
+  return conv_fwd_workspace(N, H, W, Cin, Cout, R, S, stride, pad);
+}
+
+extern "C" int dpa_conv2d_fwd_fp8_split(const void* xq, const void* wq, const float* x_scale,
+                                        const float* w_scale, const float* bias, void* y,
+                                        void* workspace, int64_t workspace_bytes, int N, int H,
+                                        int W, int Cin, int Cout, int R, int S, int stride,
+                                        int pad, void* stream) {
+  if (!xq || !wq || !x_scale || !w_scale || !y) return DPA_ERR_NULL;
+  if (!conv_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad)) return DPA_ERR_SHAPE;
+  if (workspace_bytes < conv_fwd_workspace(N, H, W, Cin, Cout, R, S, stride, pad) ||
+      (workspace_bytes > 0 && !workspace))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(xq, 16) || !aligned(wq, 16) || !aligned(y, 8) || !aligned(workspace, 16))
+    return DPA_ERR_ALIGN;
+  return conv_fwd(xq, wq, x_scale, w_scale, bias, y, N, H, W, Cin, Cout, R, S, stride, pad,
+                  (hipStream_t)stream, workspace, workspace_bytes);
+}
+
+extern "C" int64_t dpa_conv2d_dgrad_split_workspace_bytes(int N, int H, int W, int Cin, int Cout,
+                                                           int R, int S, int stride, int pad) {
+  if (!conv_shape_ok(N, H, W, Cout, Cin, R, S, stride, pad)) return 0;
+  return conv_dgrad_workspace(N, H, W, Cin, Cout, R, S, stride, pad);
+}
+
+extern "C" int dpa_conv2d_dgrad_fp8_wt_split(const void* dyq, const void* wq_t,
+                                             const float* dy_scale, const float* w_scale,
+                                             void* dx, void* workspace, int64_t workspace_bytes,
+                                             int N, int H, int W, int Cin, int Cout, int R,
+                                             int S, int stride, int pad, void* stream) {
+  if (!dyq || !wq_t || !dy_scale || !w_scale || !dx) return DPA_ERR_NULL;
+  if (!conv_shape_ok(N, H, W, Cout, Cin, R, S, stride, pad)) return DPA_ERR_SHAPE;
+  if (workspace_bytes < conv_dgrad_workspace(N, H, W, Cin, Cout, R, S, stride, pad) ||
+      (workspace_bytes > 0 && !workspace))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(dyq, 16) || !aligned(wq_t, 16) || !aligned(dx, 8) || !aligned(workspace, 16))
+    return DPA_ERR_ALIGN;
+  return conv_dgrad(dyq, wq_t, dy_scale, w_scale, dx, N, H, W, Cin, Cout, R, S, stride, pad,
+                    (hipStream_t)stream, workspace, workspace_bytes);
+}
+
+extern "C" int64_t dpa_gemm_split_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % kBK != 0 || N % kBN != 0) return 0;
+  return conv_fwd_workspace(M, 1, 1, K, N, 1, 1, 1, 0);
+}
+
+extern "C" int dpa_gemm_fp8_split(const void* a, const void* b, const float* a_scale,
+                                  const float* b_scale, const float* bias, void* c,
+                                  void* workspace, int64_t workspace_bytes, int M, int N, int K,
+                                  void* stream) {
+  if (!a || !b || !a_scale || !b_scale || !c) return DPA_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0) return DPA_ERR_SIZE;
+  if (K % kBK != 0 || N % kBN != 0) return DPA_ERR_SHAPE;
+  if (workspace_bytes < conv_fwd_workspace(M, 1, 1, K, N, 1, 1, 1, 0) ||
+      (workspace_bytes > 0 && !workspace))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 8) || !aligned(workspace, 16))
+    return DPA_ERR_ALIGN;
+  return conv_fwd(a, b, a_scale, b_scale, bias, c, M, 1, 1, K, N, 1, 1, 1, 0,
+                  (hipStream_t)stream, workspace, workspace_bytes);
 }

@@ -108,6 +108,11 @@ def _nhwc(t: torch.Tensor) -> torch.Tensor:
 # --------------------------------------------------------------------------------------
 # quantization (diffusion/fp8_kernels.py:518-601)
 # --------------------------------------------------------------------------------------
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """Device scratch of ``nbytes`` (None for 0), 16-B aligned as the caching allocator's are."""
+    return torch.empty(nbytes, device=device, dtype=torch.uint8) if nbytes > 0 else None
+
+
 def _dense(t: torch.Tensor) -> bool:
     return t.is_contiguous() or (t.ndim == 4 and t.is_contiguous(memory_format=torch.channels_last))
 
@@ -211,9 +216,12 @@ def conv2d_fp8_fwd_general(
     stride: int = 1,
     padding: int = 1,
     bias: torch.Tensor | None = None,
+    split: bool = True,
 ) -> torch.Tensor:
     """FP8 conv forward for 3x3 (pad 1, stride 1|2) and 1x1 (pad 0, stride 1); NCHW-logical,
-    channels-last bf16 output. ``bias`` (fp32 [Cout]) is added after dequantization."""
+    channels-last bf16 output. ``bias`` (fp32 [Cout]) is added after dequantization.
+    ``split`` lets the library split the reduction of launches too small to fill the GPU
+    (fp32 partial sums in a workspace); False runs the single-pass kernel only."""
     assert x.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE
     torch_checks_scale(x_scale, x.device)
     torch_checks_scale(weight_scale, x.device)
@@ -227,11 +235,20 @@ def conv2d_fp8_fwd_general(
                     memory_format=torch.channels_last)
     if bias is not None:
         assert bias.dtype == torch.float32 and bias.numel() == cout and bias.is_contiguous()
+    geom = (batch, height, width, cin, cout, kh, kw, stride, padding)
+    if split:
+        ws_bytes = _lib.query("dpa_conv2d_fwd_split_workspace_bytes", *geom)
+        workspace = _workspace(ws_bytes, x.device)
+        _lib.call(
+            "dpa_conv2d_fwd_fp8_split",
+            x.data_ptr(), weight.data_ptr(), x_scale.data_ptr(), weight_scale.data_ptr(),
+            _ptr(bias), y.data_ptr(), _ptr(workspace), ws_bytes, *geom, _stream(x),
+        )
+        return y
     _lib.call(
         "dpa_conv2d_fwd_fp8",
         x.data_ptr(), weight.data_ptr(), x_scale.data_ptr(), weight_scale.data_ptr(),
-        _ptr(bias), y.data_ptr(), batch, height, width, cin, cout, kh, kw, stride, padding,
-        _stream(x),
+        _ptr(bias), y.data_ptr(), *geom, _stream(x),
     )
     return y
 
@@ -245,9 +262,11 @@ def conv2d_fp8_dgrad_general(
     stride: int = 1,
     padding: int = 1,
     weight_t: torch.Tensor | None = None,
+    split: bool = True,
 ) -> torch.Tensor:
     """FP8 data gradient; ``input_hw`` is the forward input's (H, W). ``weight_t`` may carry
-    the weight already transposed to [Cin][R][S][Cout] bytes."""
+    the weight already transposed to [Cin][R][S][Cout] bytes. ``split`` as in
+    conv2d_fp8_fwd_general (False: the single-pass kernel only)."""
     assert dy.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE
     torch_checks_scale(dy_scale, dy.device)
     torch_checks_scale(weight_scale, dy.device)
@@ -259,7 +278,19 @@ def conv2d_fp8_dgrad_general(
     height, width = input_hw
     dx = torch.empty((batch, cin, height, width), device=dy.device, dtype=torch.bfloat16,
                      memory_format=torch.channels_last)
-    if weight_t is None:
+    geom = (batch, height, width, cin, cout, kh, kw, stride, padding)
+    if split:
+        if weight_t is None:
+            weight_t = weight_transpose_fp8(weight)
+        assert weight_t.numel() == weight.numel() and weight_t.is_contiguous()
+        ws_bytes = _lib.query("dpa_conv2d_dgrad_split_workspace_bytes", *geom)
+        workspace = _workspace(ws_bytes, dy.device)
+        _lib.call(
+            "dpa_conv2d_dgrad_fp8_wt_split",
+            dy.data_ptr(), weight_t.data_ptr(), dy_scale.data_ptr(), weight_scale.data_ptr(),
+            dx.data_ptr(), _ptr(workspace), ws_bytes, *geom, _stream(dy),
+        )
+    elif weight_t is None:
         ws_bytes = _lib.query("dpa_conv2d_dgrad_workspace_bytes", cin, cout, kh, kw)
         workspace = torch.empty(ws_bytes, device=dy.device, dtype=torch.uint8)
         _lib.call(
@@ -570,8 +601,10 @@ def linear_fp8_prequantized(
     a_scale: torch.Tensor,
     b_scale: torch.Tensor,
     bias: torch.Tensor | None = None,
+    split: bool = True,
 ) -> torch.Tensor:
-    """c[M, N] = bf16(a[M, K] @ b[N, K]^T * a_scale * b_scale [+ bias]); e4m3 inputs."""
+    """c[M, N] = bf16(a[M, K] @ b[N, K]^T * a_scale * b_scale [+ bias]); e4m3 inputs.
+    ``split`` as in conv2d_fp8_fwd_general."""
     assert a.dtype == FP8_DTYPE and b.dtype == FP8_DTYPE and a.is_cuda and b.is_cuda
     assert a.ndim == 2 and b.ndim == 2 and a.shape[1] == b.shape[1]
     torch_checks_scale(a_scale, a.device)
@@ -583,6 +616,13 @@ def linear_fp8_prequantized(
     c = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
     if bias is not None:
         assert bias.dtype == torch.float32 and bias.numel() == n and bias.is_contiguous()
+    if split:
+        ws_bytes = _lib.query("dpa_gemm_split_workspace_bytes", m, n, k)
+        workspace = _workspace(ws_bytes, a.device)
+        _lib.call("dpa_gemm_fp8_split", a.data_ptr(), b.data_ptr(), a_scale.data_ptr(),
+                  b_scale.data_ptr(), _ptr(bias), c.data_ptr(), _ptr(workspace), ws_bytes, m, n,
+                  k, _stream(a))
+        return c
     _lib.call("dpa_gemm_fp8", a.data_ptr(), b.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(),
               _ptr(bias), c.data_ptr(), m, n, k, _stream(a))
     return c
@@ -603,10 +643,12 @@ def linear_fp8_dgrad_prequantized(
     weight: torch.Tensor,
     dy_scale: torch.Tensor,
     weight_scale: torch.Tensor,
+    split: bool = True,
 ) -> torch.Tensor:
     """dx[M, K] = bf16(dy[M, N] @ weight[N, K] * dy_scale * weight_scale); e4m3 inputs.
 
-    Runs the 1x1 data-gradient kernel on M one-pixel images."""
+    Runs the 1x1 data-gradient kernel on M one-pixel images; ``split`` as in
+    conv2d_fp8_fwd_general."""
     assert dy.dtype == FP8_DTYPE and weight.dtype == FP8_DTYPE and dy.ndim == weight.ndim == 2
     assert dy.shape[1] == weight.shape[0]
     torch_checks_scale(dy_scale, dy.device)
@@ -616,6 +658,19 @@ def linear_fp8_dgrad_prequantized(
     m, n = dy.shape
     k = weight.shape[1]
     dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    if split:
+        weight_t = torch.empty((k, n), device=dy.device, dtype=FP8_DTYPE)
+        _lib.call("dpa_weight_transpose_fp8", weight.data_ptr(), weight_t.data_ptr(), n, 1, 1, k,
+                  _stream(dy))
+        geom = (m, 1, 1, k, n, 1, 1, 1, 0)
+        ws_bytes = _lib.query("dpa_conv2d_dgrad_split_workspace_bytes", *geom)
+        workspace = _workspace(ws_bytes, dy.device)
+        _lib.call(
+            "dpa_conv2d_dgrad_fp8_wt_split",
+            dy.data_ptr(), weight_t.data_ptr(), dy_scale.data_ptr(), weight_scale.data_ptr(),
+            dx.data_ptr(), _ptr(workspace), ws_bytes, *geom, _stream(dy),
+        )
+        return dx
     ws_bytes = _lib.query("dpa_conv2d_dgrad_workspace_bytes", k, n, 1, 1)
     workspace = torch.empty(ws_bytes, device=dy.device, dtype=torch.uint8)
     _lib.call(

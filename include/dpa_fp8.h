@@ -151,6 +151,33 @@ int dpa_gemm_fp8(const void* a, const void* b, const float* a_scale, const float
                  const float* bias, void* c, int M, int N, int K, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Split-K variants of the forward conv, the data gradient (pre-transposed weight) and the
+ * GEMM. No counterpart in the reference (its kernels launch one program per output tile,
+ * diffusion/fp8_kernels.py:624-637 and :694-707); same arguments and results as the entries
+ * above up to fp32 summation order. When the output tiles would leave most CUs idle (small
+ * images or batches), each tile's K range (taps x channels) is split into equal parts whose
+ * fp32 partial sums go to the workspace; a second kernel adds them in split order and
+ * applies the same epilogue. The *_split_workspace_bytes queries return the bytes needed
+ * (0 when the shape is not split); a workspace of that size must be passed, 16-B aligned.
+ * ---------------------------------------------------------------------------------------- */
+int64_t dpa_conv2d_fwd_split_workspace_bytes(int N, int H, int W, int Cin, int Cout, int R,
+                                             int S, int stride, int pad);
+int dpa_conv2d_fwd_fp8_split(const void* xq, const void* wq, const float* x_scale,
+                             const float* w_scale, const float* bias, void* y, void* workspace,
+                             int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout,
+                             int R, int S, int stride, int pad, void* stream);
+int64_t dpa_conv2d_dgrad_split_workspace_bytes(int N, int H, int W, int Cin, int Cout, int R,
+                                               int S, int stride, int pad);
+int dpa_conv2d_dgrad_fp8_wt_split(const void* dyq, const void* wq_t, const float* dy_scale,
+                                  const float* w_scale, void* dx, void* workspace,
+                                  int64_t workspace_bytes, int N, int H, int W, int Cin,
+                                  int Cout, int R, int S, int stride, int pad, void* stream);
+int64_t dpa_gemm_split_workspace_bytes(int M, int N, int K);
+int dpa_gemm_fp8_split(const void* a, const void* b, const float* a_scale, const float* b_scale,
+                       const float* bias, void* c, void* workspace, int64_t workspace_bytes,
+                       int M, int N, int K, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Fused GroupNorm + optional FiLM + SiLU on NHWC bf16, fp32 statistics (biased variance).
  *   z   = gamma[c] * (x - mean[n,g]) * rstd[n,g] + beta[c]
  *   z'  = film_scale ? film_scale[n,c] * z + film_shift[n,c] : z

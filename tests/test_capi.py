@@ -74,6 +74,13 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_quantize_fp8_bf16(fake, 16, fake, fake, fake, 8, nul) == -5
     assert lib.dpa_conv2d_dgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -5
     assert lib.dpa_conv2d_wgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 2, 8, 8, 128, 128, 3, 3, 1, 1, 0, nul) == -5
+    assert lib.dpa_conv2d_fwd_fp8_split(fake, fake, fake, fake, nul, fake, fake, 10, 128, 4, 4, 256, 256, 3, 3, 1, 1, nul) == -5
+    assert lib.dpa_conv2d_fwd_fp8_split(fake, fake, fake, fake, nul, fake, nul, 1 << 30, 128, 4, 4, 256, 256, 3, 3, 1, 1, nul) == -5
+    assert lib.dpa_conv2d_dgrad_fp8_wt_split(fake, fake, fake, fake, fake, fake, 10, 128, 4, 4, 256, 256, 3, 3, 1, 1, nul) == -5
+    assert lib.dpa_gemm_fp8_split(fake, fake, fake, fake, nul, fake, fake, 10, 128, 512, 1024, nul) == -5
+    assert lib.dpa_conv2d_fwd_fp8_split(nul, fake, fake, fake, nul, fake, fake, 10, 128, 4, 4, 256, 256, 3, 3, 1, 1, nul) == -1
+    assert lib.dpa_gemm_fp8_split(fake, fake, fake, fake, nul, fake, fake, 1 << 30, 128, 500, 1024, nul) == -4
+    assert lib.dpa_conv2d_dgrad_fp8_wt_split(fake, fake, fake, fake, fake, fake, 1 << 30, 128, 4, 4, 256, 256, 5, 5, 1, 2, nul) == -4
     # misaligned e4m3 operand
     odd = ctypes.c_void_p(0x1001)
     assert lib.dpa_conv2d_fwd_fp8(odd, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -3
@@ -86,3 +93,24 @@ def test_workspace_queries(lib):
     assert ws > 0 and ws % (128 * 128 * 9 * 4) == 0
     assert lib.dpa_conv2d_wgrad_workspace_bytes(128, 32, 32, 128, 128, 3, 3, 1, 1, 4) == 4 * 128 * 128 * 9 * 4
     assert lib.dpa_conv2d_wgrad_workspace_bytes(128, 32, 32, 100, 128, 3, 3, 1, 1, 0) == 0
+
+
+def test_split_workspace_queries(lib):
+    """Split-K plans (256 CUs; one 256 x 128 fp32 block per work item): the 4x4 / 256-channel
+    U-Net conv has 16 output tiles and 18 K-steps, so it splits 3 ways (six K-steps per
+    part); launches that fill the GPU, and the halo-kernel shapes, need none."""
+    block = 256 * 128 * 4
+    assert lib.dpa_conv2d_fwd_split_workspace_bytes(128, 32, 32, 128, 128, 3, 3, 1, 1) == 0
+    assert lib.dpa_conv2d_fwd_split_workspace_bytes(128, 4, 4, 256, 256, 3, 3, 1, 1) == 3 * 16 * block
+    assert lib.dpa_conv2d_dgrad_split_workspace_bytes(128, 4, 4, 256, 256, 3, 3, 1, 1) == 3 * 16 * block
+    # 8x8, 512 -> 256: 64 tiles, 36 K-steps: 4 ways (256 work items = CUs)
+    assert lib.dpa_conv2d_fwd_split_workspace_bytes(128, 8, 8, 512, 256, 3, 3, 1, 1) == 4 * 64 * block
+    # cfg1 GEMM: 768 tiles, no split; a 128-row GEMM with K = 1024 and 512 outputs: 4 tiles,
+    # 8 K-steps: 4 ways of two steps
+    assert lib.dpa_gemm_split_workspace_bytes(32768, 768, 256) == 0
+    assert lib.dpa_gemm_split_workspace_bytes(128, 512, 1024) == 4 * 4 * block
+    # fewer than eight K-steps per tile never split; unsupported shapes report 0
+    assert lib.dpa_gemm_split_workspace_bytes(128, 512, 512) == 0
+    assert lib.dpa_gemm_split_workspace_bytes(128, 512, 128) == 0
+    assert lib.dpa_gemm_split_workspace_bytes(128, 500, 1024) == 0
+    assert lib.dpa_conv2d_fwd_split_workspace_bytes(128, 4, 4, 96, 256, 3, 3, 1, 1) == 0

@@ -192,3 +192,63 @@ def test_zero_weight_gives_zero_output(K):
     y = K.conv2d_fwd_fp8(cl(x), cl(wz))
     torch.cuda.synchronize()
     assert not bits(y.cpu()).any()
+
+
+SPLIT_SHAPES = [
+    (128, 256, 256, 4, 4, 3, 1, 1),   # U-Net 4x4 level: 16 output tiles, 3-way K split
+    (32, 512, 256, 8, 8, 3, 1, 1),    # 8x8, 512 -> 256
+    (16, 256, 256, 8, 8, 3, 2, 1),    # stride-2 downsample; dgrad parity classes split too
+    (24, 1024, 128, 4, 4, 1, 1, 0),   # 1x1 projection, ragged last tile (384 pixels)
+    (5, 128, 256, 3, 5, 3, 1, 1),     # ragged, 9 K-steps: 3-way split
+]
+
+
+@pytest.mark.parametrize("n,cin,cout,h,w,k,stride,pad", SPLIT_SHAPES)
+def test_split_k_conv_matches_single_pass_and_oracle(K, n, cin, cout, h, w, k, stride, pad):
+    """Launches too small to fill the GPU split their K range (fp32 partials reduced in split
+    order): fwd and dgrad against the exact oracle, and against the single-pass kernel."""
+    L = dpa_mod("_lib")
+    geom = (n, h, w, cin, cout, k, k, stride, pad)
+    assert L.query("dpa_conv2d_fwd_split_workspace_bytes", *geom) > 0
+    xq, xs, wq, ws, dyq, dys = quantized_inputs(K, n, cin, cout, h, w, k, stride, pad, seed=n + h)
+    y = K.conv2d_fp8_fwd_general(xq, wq, xs, ws, stride, pad)
+    y1 = K.conv2d_fp8_fwd_general(xq, wq, xs, ws, stride, pad, split=False)
+    dx = K.conv2d_fp8_dgrad_general(dyq, wq, dys, ws, (h, w), stride, pad)
+    dx1 = K.conv2d_fp8_dgrad_general(dyq, wq, dys, ws, (h, w), stride, pad, split=False)
+    torch.cuda.synchronize()
+    xb, wb, db = (nhwc_bits(t.cpu().view(torch.uint8)) for t in (xq, wq, dyq))
+    y_ref = O.conv2d_fwd(xb, wb, f32(xs), f32(ws), stride, pad)
+    dx_ref = O.conv2d_dgrad(db, wb, f32(dys), f32(ws), (h, w), stride, pad)
+    tag = f"{geom}"
+    for got, ref, name in ((y, y_ref, "fwd"), (y1, y_ref, "fwd single"), (dx, dx_ref, "dgrad"),
+                           (dx1, dx_ref, "dgrad single")):
+        frac = assert_bf16_close(nhwc_bits(got.cpu()), ref, f"{name} {tag}")
+        assert frac > 0.97, (name, frac)
+    assert_bf16_close(nhwc_bits(y.cpu()), nhwc_bits(y1.cpu()), "fwd split vs single " + tag)
+
+
+def test_split_k_gemm_and_linear_dgrad(K):
+    """A 128-row GEMM (the U-Net's time-embedding shape class) with bias, split 4 ways, and
+    the linear's data gradient, against the oracle and the single-pass kernel."""
+    L = dpa_mod("_lib")
+    m, k, n = 128, 1024, 512
+    assert L.query("dpa_gemm_split_workspace_bytes", m, n, k) > 0
+    x = randn_bf16((m, k), seed=11)
+    wt = kaiming_uniform_bf16((n, k), seed=12)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(13))
+    dy = randn_bf16((m, n), seed=14, std=1e-2)
+    xq, xs = K.quantize_fp8_tensor(x.cuda())
+    wq, ws = K.quantize_fp8_tensor(wt.cuda())
+    dyq, dys = K.quantize_fp8_tensor(dy.cuda())
+    y = K.linear_fp8_prequantized(xq, wq, xs, ws, bias.cuda())
+    y1 = K.linear_fp8_prequantized(xq, wq, xs, ws, bias.cuda(), split=False)
+    dx = K.linear_fp8_dgrad_prequantized(dyq, wq, dys, ws)
+    dx1 = K.linear_fp8_dgrad_prequantized(dyq, wq, dys, ws, split=False)
+    torch.cuda.synchronize()
+    y_ref = O.gemm(bits(xq.cpu()), bits(wq.cpu()), f32(xs), f32(ws), bias.numpy())
+    wT = np.ascontiguousarray(bits(wq.cpu()).T)
+    dx_ref = O.gemm(bits(dyq.cpu()), wT, f32(dys), f32(ws))
+    for got, ref, name in ((y, y_ref, "gemm"), (y1, y_ref, "gemm single"), (dx, dx_ref, "dgrad"),
+                           (dx1, dx_ref, "dgrad single")):
+        frac = assert_bf16_close(bits(got.cpu()), ref, name)
+        assert frac > 0.97, (name, frac)
