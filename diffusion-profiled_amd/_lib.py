@@ -65,6 +65,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p] * 8 + [c_int] * 4 + [c_float, c_void_p],
     ),
+    "dpa_gn_silu_fwd_workspace_bytes": (c_int64, [c_int] * 4),
+    "dpa_gn_silu_fwd_ws_bf16": (
+        c_int,
+        [c_void_p] * 10 + [c_int64] + [c_int] * 4 + [c_float, c_void_p],
+    ),
     "dpa_gn_silu_bwd_workspace_bytes": (c_int64, [c_int] * 4),
     "dpa_gn_silu_bwd_bf16": (
         c_int,

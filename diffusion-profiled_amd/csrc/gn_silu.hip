@@ -11,6 +11,17 @@
 // half-granule partials -> wave shuffles over the 8 pixel lanes of a wave -> LDS over the
 // waves. Each lane keeps four 16-B loads in flight. The kernels make several passes over
 // their inputs (after the first mostly from L2).
+//
+// Images of 256+ pixels use a chunked form instead, which spreads each (image, slab) over
+// workgroups of 128 pixels (2048 workgroups at 32x32 x 128 channels, batch 128, against 256
+// for one workgroup per slab, whose passes were latency-bound): every workgroup holds its
+// chunk in registers, and the per-group statistics cross workgroups through a workspace
+// between two launches.
+//   forward:  stats (chunk mean and sum of squared deviations per group) ->
+//             apply (merge the chunks in order, Chan et al.'s pairwise update; normalise)
+//   backward: sums (per-channel chunk sums of the four backward terms) ->
+//             apply (chunk sums in order -> group means -> dx; chunk 0 also writes the
+//             per-image dgamma/dbeta partials and the FiLM gradients)
 #include "dpa_common.hpp"
 
 namespace dpa {
@@ -37,6 +48,16 @@ struct GnArgs {
   int N, HW, C, G, cpg;
   float eps;
 };
+
+// sigmoid(v) = 1 / (1 + e^-v) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32,
+// about 1 ulp each), e^-v = 2^(-v log2 e). The SiLU and its derivative are rounded to bf16
+// (2^16 fp32 ulps), so this changes an output bit only at rounding ties; the IEEE-exact
+// exponential and division cost about a third of the forward kernels' time. Saturates as the
+// exact form does: e^-v overflows to inf below v = -88.7 and the result is 0.
+__device__ __forceinline__ float sigmoid_hw(float v) {
+  const float e = __builtin_amdgcn_exp2f(v * -1.44269504f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -240,7 +261,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
         const int ee = e + k;
         float v = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
         if (film) v = fsc[ee] * v + fsh[ee];
-        z[k] = v / (1.0f + expf(-v));
+        z[k] = v * sigmoid_hw(v);
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
@@ -297,7 +318,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
         const float xh = (f[e] - mu[e >> 2]) * rs[e >> 2];
         const float z = xh * gm[e] + bt[e];
         const float zp = fsc[e] * z + fsh[e];
-        const float sg = 1.0f / (1.0f + expf(-zp));
+        const float sg = sigmoid_hw(zp);
         const float g = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
         const float gz = g * fsc[e];
         acc[0][e] += gz;
@@ -371,7 +392,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
         const float xh = (f[ee] - mu[h]) * rs[h];
         const float z = xh * gm[ee] + bt[ee];
         const float zp = fsc[ee] * z + fsh[ee];
-        const float sg = 1.0f / (1.0f + expf(-zp));
+        const float sg = sigmoid_hw(zp);
         const float g = d[ee] * (sg * (1.0f + zp * (1.0f - sg)));
         const float gxh = g * fsc[ee] * gm[ee];
         r2[k] = rs[h] * (gxh - m1[h] - xh * m2[h]);
@@ -411,6 +432,386 @@ __global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __res
   }
 }
 
+// ---- chunked form (HW >= kChunkMinHW) ----
+constexpr int kChPLN = 32;                 // pixel lanes per workgroup (256 threads)
+constexpr int kChU = 4;                    // pixels per lane, all loads in flight
+constexpr int kChunkPx = kChPLN * kChU;    // 128 pixels per workgroup
+constexpr int kChunkMinHW = 256;
+constexpr int kMaxChunks = 64;             // larger images run the one-launch form
+static_assert(8 * kChPLN == 4 * kSlab, "backward apply: four chunk slices of 64 channels");
+
+// Lane pl's pixels of the chunk starting at px0: px0 + pl + 32 u; pixels past HW load pixel
+// HW - 1 (a valid address) with ok false.
+template <int NL>
+__device__ __forceinline__ void chunk_load(const uint16_t* const (&src)[NL], int C, int px0,
+                                           int pl, int HW, uint4 (&v)[NL][kChU],
+                                           bool (&ok)[kChU], int (&pxs)[kChU]) {
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    const int px = px0 + pl + u * kChPLN;
+    ok[u] = px < HW;
+    pxs[u] = ok[u] ? px : HW - 1;
+  }
+#pragma unroll
+  for (int u = 0; u < kChU; ++u)
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+      v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * C);
+}
+
+__device__ __forceinline__ int chunk_pixels(int HW, int chunk) {
+  const int r = HW - chunk * kChunkPx;
+  return r < kChunkPx ? r : kChunkPx;
+}
+
+// Forward, launch 1: grid (C / 64, N, chunks). cs[n][chunk][g] = (chunk mean, chunk sum of
+// squared deviations from it) of group g.
+__global__ __launch_bounds__(8 * kChPLN) void gn_chunk_stats_kernel(const GnArgs p,
+                                                                   float2* __restrict__ cs,
+                                                                   int nchunk) {
+  __shared__ float red[(kChPLN / 8) * 8 * 2];
+  __shared__ float hs[16];
+  const int n = blockIdx.y, chunk = blockIdx.z;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
+  uint4 v[1][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<1>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  float f[kChU][8];
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) unpack8(v[0][u], f[u]);
+
+  float sm[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kChU; ++u)
+    if (ok[u]) {
+      sm[0] += (f[u][0] + f[u][1]) + (f[u][2] + f[u][3]);
+      sm[1] += (f[u][4] + f[u][5]) + (f[u][6] + f[u][7]);
+    }
+  slab_reduce<2, kChPLN>(sm, red);
+  if (pl == 0) {
+    hs[2 * gq] = sm[0];
+    hs[2 * gq + 1] = sm[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)(chunk_pixels(p.HW, chunk) * p.cpg);
+  const float mu[2] = {group_sum(hs, 2 * gq, p.cpg) * inv_cnt,
+                       group_sum(hs, 2 * gq + 1, p.cpg) * inv_cnt};
+  __syncthreads();
+  float q[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kChU; ++u)
+    if (ok[u]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = f[u][e] - mu[e >> 2];
+        q[e >> 2] += d * d;
+      }
+    }
+  slab_reduce<2, kChPLN>(q, red);
+  if (pl == 0) {
+    hs[2 * gq] = q[0];
+    hs[2 * gq + 1] = q[1];
+  }
+  __syncthreads();
+  if (pl == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int cc = ch + 4 * h;
+      if (cc % p.cpg == 0)
+        cs[((int64_t)n * nchunk + chunk) * p.G + cc / p.cpg] =
+            float2{mu[h], group_sum(hs, 2 * gq + h, p.cpg)};
+    }
+  }
+}
+
+// Forward, launch 2: merge the chunk statistics of the slab's groups in chunk order, then
+// normalise, affine, FiLM, SiLU, bf16 for this workgroup's chunk. Chunk 0 writes mean/rstd.
+__global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs p,
+                                                                   const float2* __restrict__ cs,
+                                                                   int nchunk) {
+  __shared__ float2 gstat[kSlab / 4];
+  __shared__ float2 lcs[kMaxChunks * (kSlab / 4)];
+  const int n = blockIdx.y, chunk = blockIdx.z;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
+  uint4 v[1][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<1>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+
+  // the slab's chunk statistics, all loads in flight at once, then merged from LDS
+  const int ngs = kSlab / p.cpg;
+  const int g0 = c0 / p.cpg;
+  for (int i = threadIdx.x; i < ngs * nchunk; i += 8 * kChPLN) {
+    const int k = i / ngs;
+    lcs[i] = cs[((int64_t)n * nchunk + k) * p.G + g0 + (i - k * ngs)];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < ngs) {
+    const int g = g0 + threadIdx.x;
+    float na = 0.f, mean = 0.f, m2 = 0.f;
+    for (int k = 0; k < nchunk; ++k) {
+      const float2 b = lcs[k * ngs + threadIdx.x];
+      const float nb = (float)(chunk_pixels(p.HW, k) * p.cpg);
+      const float nt = na + nb;
+      const float d = b.x - mean;
+      mean += d * (nb / nt);
+      m2 += b.y + d * d * (na * nb / nt);
+      na = nt;
+    }
+    const float rs = 1.0f / sqrtf(m2 / na + p.eps);
+    gstat[threadIdx.x] = float2{mean, rs};
+    if (chunk == 0) {
+      p.mean[n * p.G + g] = mean;
+      p.rstd[n * p.G + g] = rs;
+    }
+  }
+  __syncthreads();
+  float mu[2], rs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float2 st = gstat[(ch + 4 * h - c0) / p.cpg];
+    mu[h] = st.x;
+    rs[h] = st.y;
+  }
+  float a[8], b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = p.gamma[ch + e];
+    b[e] = p.beta[ch + e];
+  }
+  float fsc[8], fsh[8];
+  const bool film = load_film(p, n, ch, fsc, fsh);
+  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    float f[8];
+    unpack8(v[0][u], f);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float z[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        float t = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
+        if (film) t = fsc[ee] * t + fsh[ee];
+        z[k] = t * sigmoid_hw(t);
+      }
+      o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
+    }
+    if (ok[u]) st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+  }
+}
+
+// The backward terms of one pixel's 8 channels (see gn_silu_bwd_kernel): g = d u / d zp
+// times dout, z = GN output; returns xhat, g and gz = g * fs.
+__device__ __forceinline__ void bwd_terms(const float (&f)[8], const float (&d)[8],
+                                          const float (&mu)[2], const float (&rs)[2],
+                                          const float (&gm)[8], const float (&bt)[8],
+                                          const float (&fsc)[8], const float (&fsh)[8],
+                                          float (&xh)[8], float (&z)[8], float (&g)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xh[e] = (f[e] - mu[e >> 2]) * rs[e >> 2];
+    z[e] = xh[e] * gm[e] + bt[e];
+    const float zp = fsc[e] * z[e] + fsh[e];
+    const float sg = sigmoid_hw(zp);
+    g[e] = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
+  }
+}
+
+struct GnBwdSetup {
+  float mu[2], rs[2], gm[8], bt[8], fsc[8], fsh[8];
+};
+
+__device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnBwdSetup& st) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int g = (ch + 4 * h) / p.cpg;
+    st.mu[h] = p.mean[n * p.G + g];
+    st.rs[h] = p.rstd[n * p.G + g];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    st.gm[e] = p.gamma[ch + e];
+    st.bt[e] = p.beta[ch + e];
+  }
+  load_film(p, n, ch, st.fsc, st.fsh);
+}
+
+// Backward, launch 1: grid (C / 64, N, chunks). cp[chunk][n][c] = chunk sums of
+// (gz, gz * xhat, g * z, g) of channel c.
+__global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnArgs p,
+                                                                      float4* __restrict__ cp) {
+  __shared__ float red[(kChPLN / 8) * 8 * 32];
+  const int n = blockIdx.y, chunk = blockIdx.z;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const uint16_t* const src[2] = {p.x + base, p.dout + base};
+  uint4 v[2][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  GnBwdSetup st;
+  gn_bwd_setup(p, n, ch, st);
+  float acc[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    float f[8], d[8], xh[8], z[8], g[8];
+    unpack8(v[0][u], f);
+    unpack8(v[1][u], d);
+    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    if (ok[u]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gz = g[e] * st.fsc[e];
+        acc[e] += gz;
+        acc[8 + e] += gz * xh[e];
+        acc[16 + e] += g[e] * z[e];
+        acc[24 + e] += g[e];
+      }
+    }
+  }
+  slab_reduce<32, kChPLN>(acc, red);
+  if (pl == 0) {
+    float4* o = cp + ((int64_t)chunk * p.N + n) * p.C + ch;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = float4{acc[e], acc[8 + e], acc[16 + e], acc[24 + e]};
+  }
+}
+
+// Backward, launch 2: per-channel totals over the chunks in order, group means of
+// gxh = gz * gamma and gxh * xhat, then dx for this chunk. Chunk 0 writes the per-image
+// channel partials of dgamma/dbeta and the FiLM gradients.
+__global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const GnArgs p,
+                                                                       const float4* __restrict__ cp,
+                                                                       int nchunk) {
+  __shared__ float4 tot[kSlab];
+  __shared__ float4 slice[4][kSlab];
+  __shared__ float hs[2][16];
+  const int n = blockIdx.y, chunk = blockIdx.z;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const uint16_t* const src[2] = {p.x + base, p.dout + base};
+  uint4 v[2][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  GnBwdSetup st;
+  gn_bwd_setup(p, n, ch, st);
+
+  // channel totals over the chunks: four interleaved slices of chunks per channel (loads
+  // in flight together), then the slices in order (deterministic)
+  {
+    const int cl = threadIdx.x & (kSlab - 1), sl = threadIdx.x >> 6;
+    const float4* q = cp + (int64_t)n * p.C + c0 + cl;
+    const int64_t stride = (int64_t)p.N * p.C;
+    float4 t = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = sl; k < nchunk; k += 4) {
+      const float4 b = q[k * stride];
+      t.x += b.x;
+      t.y += b.y;
+      t.z += b.z;
+      t.w += b.w;
+    }
+    slice[sl][cl] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < kSlab) {
+    const int c = c0 + threadIdx.x;
+    float4 t = slice[0][threadIdx.x];
+#pragma unroll
+    for (int sl = 1; sl < 4; ++sl) {
+      const float4 b = slice[sl][threadIdx.x];
+      t.x += b.x;
+      t.y += b.y;
+      t.z += b.z;
+      t.w += b.w;
+    }
+    tot[threadIdx.x] = t;
+    if (chunk == 0) {
+      const int64_t nc = (int64_t)p.N * p.C;
+      const int64_t o = (int64_t)n * p.C + c;
+      p.part[o] = t.y;       // dgamma partial
+      p.part[nc + o] = t.x;  // dbeta partial
+      if (p.dfs) {
+        p.dfs[o] = t.z;
+        p.dfb[o] = t.w;
+      } else if (p.dwb) {
+        const int64_t ob = (int64_t)n * 2 * p.C + c;
+        p.dwb[ob] = (uint16_t)f32_to_bf16_bits(t.z);
+        p.dwb[ob + p.C] = (uint16_t)f32_to_bf16_bits(t.w);
+      }
+    }
+  }
+  __syncthreads();
+  if (pl == 0) {
+    float h1[2] = {0.f, 0.f}, h2[2] = {0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float4 t = tot[gq * 8 + e];
+      h1[e >> 2] += t.x * st.gm[e];
+      h2[e >> 2] += t.y * st.gm[e];
+    }
+    hs[0][2 * gq] = h1[0];
+    hs[0][2 * gq + 1] = h1[1];
+    hs[1][2 * gq] = h2[0];
+    hs[1][2 * gq + 1] = h2[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)((int64_t)p.HW * p.cpg);
+  float m1[2], m2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    m1[h] = group_sum(hs[0], 2 * gq + h, p.cpg) * inv_cnt;
+    m2[h] = group_sum(hs[1], 2 * gq + h, p.cpg) * inv_cnt;
+  }
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    float f[8], d[8], xh[8], z[8], g[8];
+    unpack8(v[0][u], f);
+    unpack8(v[1][u], d);
+    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float r2[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        const int h = ee >> 2;
+        const float gxh = g[ee] * st.fsc[ee] * st.gm[ee];
+        r2[k] = st.rs[h] * (gxh - m1[h] - xh[ee] * m2[h]);
+      }
+      o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
+    }
+    if (ok[u]) st_nt16(p.out + base + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+  }
+}
+
+static int gn_chunks(int HW) {
+  const int k = (int)ceil_div(HW, kChunkPx);
+  return HW >= kChunkMinHW && k <= kMaxChunks ? k : 0;
+}
+
 // Pixel lanes per workgroup: enough that every lane has a few pixels to stream.
 static int gn_pixel_lanes(int HW) { return HW >= 1024 ? 128 : (HW >= 256 ? 64 : 32); }
 
@@ -425,9 +826,14 @@ static bool gn_shape_ok(int N, int HW, int C, int G) {
 
 using namespace dpa;
 
+static int64_t gn_fwd_workspace(int N, int HW, int G) {
+  return (int64_t)N * gn_chunks(HW) * G * (int64_t)sizeof(float2);
+}
+
 static int gn_fwd(const void* x, const float* gamma, const float* beta, const float* film_scale,
                   const float* film_shift, const void* film_wb, void* out, float* mean,
-                  float* rstd, int N, int HW, int C, int G, float eps, void* stream) {
+                  float* rstd, int N, int HW, int C, int G, float eps, void* stream,
+                  void* workspace = nullptr, int64_t workspace_bytes = 0) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
@@ -443,6 +849,17 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   a.mean = mean;
   a.rstd = rstd;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = eps;
+  const int nchunk = gn_chunks(HW);
+  if (nchunk > 0 && workspace && workspace_bytes >= gn_fwd_workspace(N, HW, G) &&
+      aligned(workspace, 8)) {
+    dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
+    float2* cs = (float2*)workspace;
+    gn_chunk_stats_kernel<<<cgrid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a, cs, nchunk);
+    int st = launch_status();
+    if (st != DPA_OK) return st;
+    gn_chunk_apply_kernel<<<cgrid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a, cs, nchunk);
+    return launch_status();
+  }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
   const int pln = gn_pixel_lanes(HW);
   if (pln == 128)
@@ -470,10 +887,34 @@ extern "C" int dpa_gn_silu_film_fwd_bf16(const void* x, const float* gamma, cons
                 stream);
 }
 
+extern "C" int64_t dpa_gn_silu_fwd_workspace_bytes(int N, int HW, int C, int G) {
+  if (!gn_shape_ok(N, HW, C, G)) return 0;
+  return gn_fwd_workspace(N, HW, G);
+}
+
+extern "C" int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const float* beta,
+                                       const float* film_scale, const float* film_shift,
+                                       const void* film_wb, void* out, float* mean, float* rstd,
+                                       void* workspace, int64_t workspace_bytes, int N, int HW,
+                                       int C, int G, float eps, void* stream) {
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;  // one FiLM form at a time
+  if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
+    return DPA_ERR_WORKSPACE;
+  if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
+                eps, stream, workspace, workspace_bytes);
+}
+
+// per-image channel partials of dgamma/dbeta, then (chunked form) the chunk sums
+static int64_t gn_bwd_workspace(int N, int HW, int C) {
+  return (int64_t)2 * N * C * 4 + (int64_t)gn_chunks(HW) * N * C * (int64_t)sizeof(float4);
+}
+
 extern "C" int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G) {
-  (void)HW;
   (void)G;
-  return (int64_t)2 * N * C * 4;
+  if (N <= 0 || HW <= 0 || C <= 0) return 0;
+  return gn_bwd_workspace(N, HW, C);
 }
 
 static int gn_bwd(const void* x, const void* dout, const float* gamma, const float* beta,
@@ -487,8 +928,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   if (film_scale && (!dfilm_scale || !dfilm_shift)) return DPA_ERR_NULL;
   if (film_wb && !dfilm_wb) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
-  if (!workspace || workspace_bytes < dpa_gn_silu_bwd_workspace_bytes(N, HW, C, G))
-    return DPA_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < (int64_t)2 * N * C * 4) return DPA_ERR_WORKSPACE;
   if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4) ||
       !aligned(film_wb, 2) || !aligned(dfilm_wb, 2))
     return DPA_ERR_ALIGN;
@@ -509,15 +949,27 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   a.dwb = film_wb ? (uint16_t*)dfilm_wb : nullptr;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  const int pln = gn_pixel_lanes(HW);
-  if (pln == 128)
-    gn_silu_bwd_kernel<128><<<grid, 8 * 128, 0, s>>>(a);
-  else if (pln == 64)
-    gn_silu_bwd_kernel<64><<<grid, 8 * 64, 0, s>>>(a);
-  else
-    gn_silu_bwd_kernel<32><<<grid, 8 * 32, 0, s>>>(a);
-  int st = launch_status();
+  const int nchunk = gn_chunks(HW);
+  int st = DPA_OK;
+  if (nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16)) {
+    // chunk sums after the 2*N*C per-image partials (16-B aligned: 8*N*C bytes, C % 64 == 0)
+    float4* cp = (float4*)((float*)workspace + (int64_t)2 * N * C);
+    dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
+    gn_chunk_bwd_sums_kernel<<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    st = launch_status();
+    if (st != DPA_OK) return st;
+    gn_chunk_bwd_apply_kernel<<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+  } else {
+    dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+    const int pln = gn_pixel_lanes(HW);
+    if (pln == 128)
+      gn_silu_bwd_kernel<128><<<grid, 8 * 128, 0, s>>>(a);
+    else if (pln == 64)
+      gn_silu_bwd_kernel<64><<<grid, 8 * 64, 0, s>>>(a);
+    else
+      gn_silu_bwd_kernel<32><<<grid, 8 * 32, 0, s>>>(a);
+  }
+  st = launch_status();
   if (st != DPA_OK) return st;
   gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 256, 0, s>>>((const float*)workspace,
                                                                     dgamma, dbeta, N, C);

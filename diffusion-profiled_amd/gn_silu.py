@@ -39,14 +39,22 @@ def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
     if film_scale is not None:
         fs = film_scale.float().reshape(n, c).contiguous()
         fb = film_shift.float().reshape(n, c).contiguous()
+    _fwd_call(x, gamma, beta, fs, fb, None, out, mean, rstd, groups, eps)
+    return out, mean, rstd
+
+
+def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps):
+    """The workspace form of the forward (chunked for images of 256+ pixels)."""
+    n, c, h, w = x.shape
+    ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     _lib.call(
-        "dpa_gn_silu_fwd_bf16",
-        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
-        None if fs is None else fs.data_ptr(), None if fb is None else fb.data_ptr(),
-        out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), n, h * w, c, groups, float(eps),
+        "dpa_gn_silu_fwd_ws_bf16",
+        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
+        mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c, groups, float(eps),
         _stream(x),
     )
-    return out, mean, rstd
 
 
 def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None):
@@ -120,11 +128,7 @@ class GroupNormSiLUFilm(torch.autograd.Function):
         mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
-        _lib.call(
-            "dpa_gn_silu_film_fwd_bf16",
-            xb.data_ptr(), g32.data_ptr(), b32.data_ptr(), wb.data_ptr(), out.data_ptr(),
-            mean.data_ptr(), rstd.data_ptr(), n, h * w, c, groups, float(eps), _stream(xb),
-        )
+        _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps)
         ctx.groups = groups
         ctx.x_dtype = x.dtype
         ctx.wb_shape = film_wb.shape

@@ -193,7 +193,22 @@ int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
                          float* mean, float* rstd, int N, int HW, int C, int G, float eps,
                          void* stream);
 
-/* Bytes of workspace dpa_gn_silu_bwd_bf16 needs (per-image channel partial sums). */
+/* The same forward with a workspace (size from dpa_gn_silu_fwd_workspace_bytes; 0 for
+ * images under 256 pixels). For images of 256+ pixels it runs the chunked form: two
+ * launches, each (image, 64-channel slab) spread over workgroups of 128 pixels whose group
+ * statistics (chunk mean and squared deviations, merged in chunk order) cross through the
+ * workspace. The FiLM is either film_scale/film_shift (fp32 [N, C]) or film_wb (the bf16 time
+ * projection [N, 2C], as in dpa_gn_silu_film_fwd_bf16) or neither. */
+int64_t dpa_gn_silu_fwd_workspace_bytes(int N, int HW, int C, int G);
+int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const float* beta,
+                            const float* film_scale, const float* film_shift, const void* film_wb,
+                            void* out, float* mean, float* rstd, void* workspace,
+                            int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
+                            void* stream);
+
+/* Bytes of workspace dpa_gn_silu_bwd_bf16 needs: per-image channel partial sums (2*N*C fp32)
+ * and, for images of 256+ pixels, the chunk sums of the chunked backward (two launches like
+ * the forward). A workspace of only 2*N*C floats runs the one-launch form. */
 int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G);
 
 /* Backward of dpa_gn_silu_fwd_bf16 given dout (bf16, same layout as out). Writes dx (bf16)

@@ -64,6 +64,9 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_conv2d_fwd_fp8(fake, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 1, 1, 2, 0, nul) == -4
     assert lib.dpa_gemm_fp8(fake, fake, fake, fake, nul, fake, 16, 100, 128, nul) == -4
     assert lib.dpa_gn_silu_fwd_bf16(fake, fake, fake, nul, nul, fake, fake, fake, 1, 16, 96, 32, 1e-5, nul) == -4
+    assert lib.dpa_gn_silu_fwd_ws_bf16(fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 8, 2, 1024, 128, 32, 1e-5, nul) == -5
+    assert lib.dpa_gn_silu_fwd_ws_bf16(fake, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 96, 32, 1e-5, nul) == -4
+    assert lib.dpa_gn_silu_fwd_ws_bf16(nul, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 128, 32, 1e-5, nul) == -1
     assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, nul, fake, 4, 0,
                                                     fake, 4096, nul) == -1
     assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, fake, fake, 0, 0,
@@ -93,6 +96,16 @@ def test_workspace_queries(lib):
     assert ws > 0 and ws % (128 * 128 * 9 * 4) == 0
     assert lib.dpa_conv2d_wgrad_workspace_bytes(128, 32, 32, 128, 128, 3, 3, 1, 1, 4) == 4 * 128 * 128 * 9 * 4
     assert lib.dpa_conv2d_wgrad_workspace_bytes(128, 32, 32, 100, 128, 3, 3, 1, 1, 0) == 0
+
+
+def test_gn_workspace_queries(lib):
+    """Chunked GroupNorm for images of 256+ pixels: (mean, M2) per (image, chunk of 128
+    pixels, group) forward; per-image partials plus per-chunk channel sums backward."""
+    assert lib.dpa_gn_silu_fwd_workspace_bytes(128, 1024, 128, 32) == 128 * 8 * 32 * 8
+    assert lib.dpa_gn_silu_fwd_workspace_bytes(128, 64, 256, 32) == 0
+    assert lib.dpa_gn_silu_fwd_workspace_bytes(2, 323, 128, 32) == 2 * 3 * 32 * 8
+    assert lib.dpa_gn_silu_bwd_workspace_bytes(128, 1024, 128, 32) == 2 * 128 * 128 * 4 + 8 * 128 * 128 * 16
+    assert lib.dpa_gn_silu_bwd_workspace_bytes(128, 64, 256, 32) == 2 * 128 * 256 * 4
 
 
 def test_split_workspace_queries(lib):

@@ -66,6 +66,7 @@ CASES = [
     (2, 512, 8, 8, False),
     (3, 256, 4, 4, True),
     (2, 256, 7, 9, True),    # ragged pixel count
+    (2, 128, 17, 19, True),  # chunked form with a ragged last chunk (323 = 128 + 128 + 67)
     (1, 128, 5, 3, False),
 ]
 
@@ -178,3 +179,57 @@ def test_gn_silu_film_from_time_projection_matches_split_form(G, n, c, h, w):
                            (ba.grad, bb.grad, "dbeta"), (wba.grad, wbb.grad, "dwb")):
         assert got.dtype == ref.dtype and got.shape == ref.shape, what
         assert torch.equal(got.detach(), ref.detach()), what
+
+
+@pytest.mark.parametrize("n,c,h,w,film", [(2, 128, 32, 32, True), (3, 256, 16, 16, False)])
+def test_one_launch_and_chunked_forms_agree(G, n, c, h, w, film):
+    """Images of 256+ pixels run the chunked kernels when given the full workspace; the
+    one-launch kernels (no forward workspace, a backward workspace of only the per-image
+    partials) compute the same quantities with another summation order."""
+    L = dpa_mod("_lib")
+    x = cl(randn_bf16((n, c, h, w), seed=n + c, std=2.0))
+    dout = cl(randn_bf16((n, c, h, w), seed=n + c + 1, std=1e-2))
+    gamma, beta, fs, fb = params(c, n, c, film)
+    gamma, beta = gamma.cuda(), beta.cuda()
+    fs = None if fs is None else fs.cuda().contiguous()
+    fb = None if fb is None else fb.cuda().contiguous()
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    s = torch.cuda.current_stream().cuda_stream
+    hw = h * w
+    assert L.query("dpa_gn_silu_fwd_workspace_bytes", n, hw, c, GROUPS) > 0
+    res = {}
+    for form in ("chunked", "one"):
+        out = torch.empty_like(x)
+        mean = torch.empty(n * GROUPS, device="cuda")
+        rstd = torch.empty(n * GROUPS, device="cuda")
+        if form == "chunked":
+            wsb = L.query("dpa_gn_silu_fwd_workspace_bytes", n, hw, c, GROUPS)
+            ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+            L.call("dpa_gn_silu_fwd_ws_bf16", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+                   p(fs), p(fb), None, out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                   ws.data_ptr(), wsb, n, hw, c, GROUPS, 1e-5, s)
+            bws = L.query("dpa_gn_silu_bwd_workspace_bytes", n, hw, c, GROUPS)
+        else:
+            L.call("dpa_gn_silu_fwd_bf16", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+                   p(fs), p(fb), out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), n, hw, c,
+                   GROUPS, 1e-5, s)
+            bws = 2 * n * c * 4
+        dx = torch.empty_like(x)
+        dg = torch.empty(c, device="cuda")
+        db = torch.empty(c, device="cuda")
+        dfs = torch.empty((n, c), device="cuda") if film else None
+        dfb = torch.empty((n, c), device="cuda") if film else None
+        ws = torch.empty(bws, device="cuda", dtype=torch.uint8)
+        L.call("dpa_gn_silu_bwd_bf16", x.data_ptr(), dout.data_ptr(), gamma.data_ptr(),
+               beta.data_ptr(), p(fs), p(fb), mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+               dg.data_ptr(), db.data_ptr(), p(dfs), p(dfb), ws.data_ptr(), bws, n, hw, c,
+               GROUPS, s)
+        torch.cuda.synchronize()
+        res[form] = [t.cpu() for t in (out, mean, rstd, dx, dg, db)] + (
+            [dfs.cpu(), dfb.cpu()] if film else [])
+    a, b = res["chunked"], res["one"]
+    assert_fwd_close(nhwc_bits(a[0]), nhwc_bits(b[0]), "out")
+    assert rel(a[1].numpy(), b[1].numpy()) < 1e-5 and rel(a[2].numpy(), b[2].numpy()) < 1e-5
+    assert_bf16_close(nhwc_bits(a[3]), nhwc_bits(b[3]), "dx")
+    for k in range(4, len(a)):
+        assert rel(a[k].numpy(), b[k].numpy()) < 1e-4, k
