@@ -49,6 +49,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 6 + [c_int64] + [c_int] * 10 + [c_void_p],
     ),
     "dpa_gemm_fp8": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_weight_prep_plan": (c_int, [c_void_p, c_int]),
+    "dpa_weight_prep_workspace_bytes": (c_int64, [c_int]),
+    "dpa_weight_prep_run": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),
+    "dpa_window_max_grouped_f32": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p]),
+    "dpa_conv2d_wgrad_fp8_f32": (
+        c_int,
+        [c_void_p] * 6 + [c_int64] + [c_int] * 10 + [c_void_p],
+    ),
     "dpa_conv2d_fwd_split_workspace_bytes": (c_int64, [c_int] * 9),
     "dpa_conv2d_fwd_fp8_split": (
         c_int,

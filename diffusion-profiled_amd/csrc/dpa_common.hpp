@@ -157,6 +157,19 @@ __device__ __forceinline__ us2 absmax8(us2 acc, uint4 v) {
   return acc;
 }
 
+// Amax-window state of a delayed-scaling module (diffusion/unet.py:82-91 and
+// diffusion/fp8_kernels.py:888-889): window[pos] = scale and, for the last tensor of the
+// forward, pos = (pos + 1) % len. A pos outside [0, len) (never produced by this update)
+// leaves both untouched. Called by one thread.
+__device__ __forceinline__ void window_record(float scale, float* window, int64_t* pos,
+                                              int64_t len, int advance) {
+  if (!window) return;
+  const int64_t p = *pos;
+  if (p < 0 || p >= len) return;
+  window[p] = scale;
+  if (advance) *pos = p + 1 == len ? 0 : p + 1;
+}
+
 // Wave-level max of a u32 (64 lanes).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll

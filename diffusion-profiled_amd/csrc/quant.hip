@@ -161,19 +161,6 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
-// Amax-window state of a delayed-scaling module (diffusion/unet.py:82-91 and
-// diffusion/fp8_kernels.py:888-889): window[pos] = scale and, for the last tensor of the
-// forward, pos = (pos + 1) % len. A pos outside [0, len) (never produced by this update)
-// leaves both untouched. Called by one thread.
-__device__ __forceinline__ void window_record(float scale, float* window, int64_t* pos,
-                                              int64_t len, int advance) {
-  if (!window) return;
-  const int64_t p = *pos;
-  if (p < 0 || p >= len) return;
-  window[p] = scale;
-  if (advance) *pos = p + 1 == len ? 0 : p + 1;
-}
-
 // Delayed scaling, finalize: cur_scale = scale(max(partials))  (finalize_amax_kernel), and
 // the optional window update.
 __global__ __launch_bounds__(kQThreads) void finalize_scale_kernel(

@@ -292,8 +292,10 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
 constexpr int kRedLanes = 64;
 constexpr int kRedGroups = 4;
 constexpr int kRedThreads = kRedLanes * kRedGroups;
+// kF32: dw is fp32 holding the bf16-rounded values.
+template <bool kF32>
 __global__ __launch_bounds__(kRedThreads) void wgrad_reduce_kernel(const float* __restrict__ partial,
-                                                                  uint16_t* __restrict__ dw,
+                                                                  void* __restrict__ dw,
                                                                   const float* __restrict__ sx,
                                                                   const float* __restrict__ sdy,
                                                                   int64_t total, int splits) {
@@ -319,10 +321,14 @@ __global__ __launch_bounds__(kRedThreads) void wgrad_reduce_kernel(const float* 
 #pragma unroll
   for (int g = 0; g < kRedGroups - 1; ++g) acc = acc + part[g][lane];
   const float scale = sx[0] * sdy[0];
-  uint2 o;
-  o.x = f32_to_bf16_bits(acc[0] * scale) | (f32_to_bf16_bits(acc[1] * scale) << 16);
-  o.y = f32_to_bf16_bits(acc[2] * scale) | (f32_to_bf16_bits(acc[3] * scale) << 16);
-  *reinterpret_cast<uint2*>(dw + i) = o;
+  uint32_t b[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) b[k] = f32_to_bf16_bits(acc[k] * scale);
+  if (kF32) {
+    *reinterpret_cast<uint4*>((float*)dw + i) = uint4{b[0] << 16, b[1] << 16, b[2] << 16, b[3] << 16};
+  } else {
+    *reinterpret_cast<uint2*>((uint16_t*)dw + i) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+  }
 }
 
 static bool wgrad_shape_ok(int N, int H, int W, int Cin, int Cout, int R, int S, int stride,
@@ -391,26 +397,30 @@ extern "C" int64_t dpa_conv2d_wgrad_workspace_bytes(int N, int H, int W, int Cin
   return (int64_t)splits * Cout * R * S * Cin * 4;
 }
 
-extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float* x_scale,
-                                    const float* dy_scale, void* dw, void* workspace,
-                                    int64_t workspace_bytes, int N, int H, int W, int Cin,
-                                    int Cout, int R, int S, int stride, int pad, int split_k,
-                                    void* stream) {
+static int wgrad_run(const void* xq, const void* dyq, const float* x_scale,
+                     const float* dy_scale, void* dw, bool f32out, void* workspace,
+                     int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout, int R,
+                     int S, int stride, int pad, int split_k, void* stream) {
   if (!xq || !dyq || !x_scale || !dy_scale || !dw) return DPA_ERR_NULL;
   if (!wgrad_shape_ok(N, H, W, Cin, Cout, R, S, stride, pad)) return DPA_ERR_SHAPE;
   if (split_k < 0) return DPA_ERR_SIZE;
   const int splits = wgrad_splits(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
   const int64_t need = (int64_t)splits * Cout * R * S * Cin * 4;
   if (!workspace || workspace_bytes < need) return DPA_ERR_WORKSPACE;
-  if (!aligned(xq, 16) || !aligned(dyq, 16) || !aligned(workspace, 16) || !aligned(dw, 8))
+  if (!aligned(xq, 16) || !aligned(dyq, 16) || !aligned(workspace, 16) ||
+      !aligned(dw, f32out ? 16 : 8))
     return DPA_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   const int64_t total = (int64_t)Cout * R * S * Cin;
   if (use_hwgrad(N, H, W, Cin, Cout, R, S, stride, pad)) {
     int st = hwgrad_partial_run(xq, dyq, (float*)workspace, N, H, W, Cin, Cout, splits, s);
     if (st != DPA_OK) return st;
-    wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
-        (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, splits);
+    if (f32out)
+      wgrad_reduce_kernel<true><<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
+          (const float*)workspace, dw, x_scale, dy_scale, total, splits);
+    else
+      wgrad_reduce_kernel<false><<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
+          (const float*)workspace, dw, x_scale, dy_scale, total, splits);
     return launch_status();
   }
   WgradPlan pl = plan_wgrad(N, H, W, Cin, Cout, R, S, stride, pad, split_k);
@@ -443,7 +453,29 @@ extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float
   wgrad_partial_kernel<<<(unsigned)(a.per_xcd * 8), kWgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK) return st;
-  wgrad_reduce_kernel<<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
-      (const float*)workspace, (uint16_t*)dw, x_scale, dy_scale, total, pl.splits);
+  if (f32out)
+    wgrad_reduce_kernel<true><<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
+        (const float*)workspace, dw, x_scale, dy_scale, total, pl.splits);
+  else
+    wgrad_reduce_kernel<false><<<(unsigned)ceil_div(total, 4 * kRedLanes), kRedThreads, 0, s>>>(
+        (const float*)workspace, dw, x_scale, dy_scale, total, pl.splits);
   return launch_status();
+}
+
+extern "C" int dpa_conv2d_wgrad_fp8(const void* xq, const void* dyq, const float* x_scale,
+                                    const float* dy_scale, void* dw, void* workspace,
+                                    int64_t workspace_bytes, int N, int H, int W, int Cin,
+                                    int Cout, int R, int S, int stride, int pad, int split_k,
+                                    void* stream) {
+  return wgrad_run(xq, dyq, x_scale, dy_scale, dw, false, workspace, workspace_bytes, N, H, W,
+                   Cin, Cout, R, S, stride, pad, split_k, stream);
+}
+
+extern "C" int dpa_conv2d_wgrad_fp8_f32(const void* xq, const void* dyq, const float* x_scale,
+                                        const float* dy_scale, float* dw, void* workspace,
+                                        int64_t workspace_bytes, int N, int H, int W, int Cin,
+                                        int Cout, int R, int S, int stride, int pad, int split_k,
+                                        void* stream) {
+  return wgrad_run(xq, dyq, x_scale, dy_scale, dw, true, workspace, workspace_bytes, N, H, W,
+                   Cin, Cout, R, S, stride, pad, split_k, stream);
 }

@@ -1,0 +1,207 @@
+// Grouped FP8 weight preparation: every FP8 weight of a model quantized in three launches per
+// training step, straight from the fp32 master weights.
+//
+// Reference: per conv/linear call, diffusion/fp8_kernels.py casts the (autocast) bf16 weight
+// and quantizes it (quantize_fp8 :518-546 or quantize_fp8_delayed :549-601, kernels :54-120),
+// with the delayed-scaling window bookkeeping of diffusion/unet.py:69-91; the data gradient
+// reads the weight with its channel axes swapped. Done per layer that is a bf16 cast, one or
+// two quantization launches, a window-maximum reduction and, in the backward, a transpose:
+// a few microseconds of launch overhead each on tensors of at most a few MB.
+//
+// Here, once per step for the whole weight set (a table of DpaWeightEntry in device memory):
+//   window_max_grouped_kernel   hist[i] = max(window i)            (torch.max of each window)
+//   wprep_amax_kernel           per-block |bf16(w)| maxima         (partial_amax_kernel)
+//   wprep_cast_kernel           q = e4m3(clamp(bf16(w) / scale)), the transposed copy, the
+//                               scale used, this amax's scale and its window record
+// with scale = *prev_scale (delayed scaling: the window maximum) or the scale of this
+// weight's own amax (current scaling). bf16(w) is the round-to-nearest-even cast autocast
+// performs, so every byte and scale equals the per-layer path's.
+#include "dpa_common.hpp"
+
+namespace dpa {
+
+constexpr int kWpThreads = 256;
+constexpr int kWpElems = kWpThreads * 8 * 4;  // elements per block: 4 rounds of 8 per thread
+
+// Entry of block b: the last entry with blk0 <= b (entries are in blk0 order).
+__device__ __forceinline__ int wp_entry_of(const DpaWeightEntry* __restrict__ e, int count,
+                                           int b) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (e[mid].blk0 <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// 8 fp32 -> 8 bf16 (RNE) packed as one uint4.
+__device__ __forceinline__ uint4 wp_bf16x8(const float* p) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  uint4 o;
+  o.x = f32_to_bf16_bits(a.x) | (f32_to_bf16_bits(a.y) << 16);
+  o.y = f32_to_bf16_bits(a.z) | (f32_to_bf16_bits(a.w) << 16);
+  o.z = f32_to_bf16_bits(b.x) | (f32_to_bf16_bits(b.y) << 16);
+  o.w = f32_to_bf16_bits(b.z) | (f32_to_bf16_bits(b.w) << 16);
+  return o;
+}
+
+__device__ __forceinline__ uint32_t wp_block_max(uint32_t v, uint32_t* red) {
+  v = wave_max_u32(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < kWpThreads / 64; ++i) r = r > red[i] ? r : red[i];
+  return r;
+}
+
+__global__ __launch_bounds__(kWpThreads) void wprep_amax_kernel(
+    const DpaWeightEntry* __restrict__ e, int count, uint32_t* __restrict__ partials) {
+  __shared__ uint32_t red[kWpThreads / 64];
+  __shared__ int s_t;
+  if (threadIdx.x == 0) s_t = wp_entry_of(e, count, blockIdx.x);
+  __syncthreads();
+  const DpaWeightEntry& E = e[s_t];
+  const int64_t i0 = (int64_t)(blockIdx.x - E.blk0) * kWpElems;
+  const int64_t i1 = i0 + kWpElems < E.n ? i0 + kWpElems : E.n;
+  us2 acc = {0, 0};
+  for (int64_t i = i0 + threadIdx.x * 8; i < i1; i += kWpThreads * 8)
+    acc = absmax8(acc, wp_bf16x8(E.w + i));
+  const uint32_t m = wp_block_max(acc.x > acc.y ? acc.x : acc.y, red);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
+    const DpaWeightEntry* __restrict__ e, int count, const uint32_t* __restrict__ partials) {
+  __shared__ uint32_t red[kWpThreads / 64];
+  __shared__ int s_t;
+  if (threadIdx.x == 0) s_t = wp_entry_of(e, count, blockIdx.x);
+  __syncthreads();
+  const DpaWeightEntry& E = e[s_t];
+  // this weight's amax from its blocks' partials (every block re-reduces them)
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < E.nblk; i += kWpThreads) {
+    const uint32_t v = partials[E.blk0 + i];
+    m = m > v ? m : v;
+  }
+  const uint32_t amax = wp_block_max(m, red);
+  const float cur = scale_from_amax_bits(amax);
+  const float scale = E.prev_scale ? *E.prev_scale : cur;
+  if (blockIdx.x == (unsigned)E.blk0 && threadIdx.x == 0) {
+    *E.scale_used = scale;
+    if (E.cur_scale) *E.cur_scale = cur;
+    window_record(cur, E.window, E.pos, E.window_len, 0);
+  }
+  const float r = quant_recip(scale);
+  const int64_t i0 = (int64_t)(blockIdx.x - E.blk0) * kWpElems;
+  const int64_t i1 = i0 + kWpElems < E.n ? i0 + kWpElems : E.n;
+  uint8_t* q = (uint8_t*)E.q;
+  uint8_t* qt = (uint8_t*)E.qt;
+  const int64_t tc = (int64_t)E.taps * E.cin;
+  for (int64_t i = i0 + threadIdx.x * 8; i < i1; i += kWpThreads * 8) {
+    const uint4 v = wp_bf16x8(E.w + i);
+    const uint2 o = r != 0.0f ? quant8_rcp(v, scale, r) : quant8(v, scale);
+    *reinterpret_cast<uint2*>(q + i) = o;
+    if (qt) {
+      // element i = (co, tap, ci): qt[(ci * taps + tap) * cout + co]; 8 consecutive ci
+      const int64_t co = i / tc;
+      const int64_t rem = i - co * tc;
+      const int64_t tap = rem / E.cin;
+      const int64_t ci = rem - tap * E.cin;
+      uint8_t* dst = qt + (ci * E.taps + tap) * E.cout + co;
+      const int64_t step = (int64_t)E.taps * E.cout;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dst[k * step] = (uint8_t)((k < 4 ? o.x : o.y) >> (8 * (k & 3)));
+    }
+  }
+}
+
+// hist[i] = torch.max(window i) over len floats; NaN if the window holds a NaN.
+__global__ __launch_bounds__(kWpThreads) void window_max_grouped_kernel(
+    const float* const* __restrict__ windows, int64_t len, float* __restrict__ hist) {
+  __shared__ float redm[kWpThreads / 64];
+  __shared__ int redn[kWpThreads / 64];
+  const float* w = windows[blockIdx.x];
+  float m = -INFINITY;
+  int nan = 0;
+  for (int64_t i = threadIdx.x; i < len; i += kWpThreads) {
+    const float v = w[i];
+    nan |= v != v;
+    m = fmaxf(m, v);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, o, 64));
+    nan |= __shfl_xor(nan, o, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    redm[threadIdx.x >> 6] = m;
+    redn[threadIdx.x >> 6] = nan;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = redm[0];
+    int rn = redn[0];
+    for (int k = 1; k < kWpThreads / 64; ++k) {
+      r = fmaxf(r, redm[k]);
+      rn |= redn[k];
+    }
+    hist[blockIdx.x] = rn ? __builtin_nanf("") : r;
+  }
+}
+
+}  // namespace dpa
+
+using namespace dpa;
+
+extern "C" int dpa_weight_prep_plan(DpaWeightEntry* entries, int count) {
+  if (!entries) return DPA_ERR_NULL;
+  if (count <= 0) return DPA_ERR_SIZE;
+  int64_t blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    DpaWeightEntry& E = entries[i];
+    if (!E.w || !E.q || !E.scale_used) return DPA_ERR_NULL;
+    if (E.window && !E.pos) return DPA_ERR_NULL;
+    if (E.cout <= 0 || E.taps <= 0 || E.cin <= 0 || E.n <= 0) return DPA_ERR_SIZE;
+    if (E.n != (int64_t)E.cout * E.taps * E.cin || E.cin % 8 != 0) return DPA_ERR_SHAPE;
+    if (!aligned(E.w, 16) || !aligned(E.q, 8)) return DPA_ERR_ALIGN;
+    E.blk0 = (int32_t)blocks;
+    E.nblk = (int32_t)ceil_div(E.n, (int64_t)kWpElems);
+    blocks += E.nblk;
+    if (blocks > 0x7fffffff) return DPA_ERR_SIZE;
+  }
+  return (int)blocks;
+}
+
+extern "C" int64_t dpa_weight_prep_workspace_bytes(int total_blocks) {
+  return total_blocks > 0 ? (int64_t)total_blocks * 4 : 0;
+}
+
+extern "C" int dpa_weight_prep_run(const DpaWeightEntry* entries_dev, int count,
+                                   int total_blocks, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  if (!entries_dev) return DPA_ERR_NULL;
+  if (count <= 0 || total_blocks <= 0) return DPA_ERR_SIZE;
+  if (!workspace || workspace_bytes < dpa_weight_prep_workspace_bytes(total_blocks))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 4) || !aligned(entries_dev, 8)) return DPA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  wprep_amax_kernel<<<(unsigned)total_blocks, kWpThreads, 0, s>>>(entries_dev, count,
+                                                                  (uint32_t*)workspace);
+  int st = launch_status();
+  if (st != DPA_OK) return st;
+  wprep_cast_kernel<<<(unsigned)total_blocks, kWpThreads, 0, s>>>(entries_dev, count,
+                                                                  (const uint32_t*)workspace);
+  return launch_status();
+}
+
+extern "C" int dpa_window_max_grouped_f32(const float* const* windows_dev, int count,
+                                          int64_t len, float* hist, void* stream) {
+  if (!windows_dev || !hist) return DPA_ERR_NULL;
+  if (count <= 0 || len <= 0) return DPA_ERR_SIZE;
+  window_max_grouped_kernel<<<(unsigned)count, kWpThreads, 0, (hipStream_t)stream>>>(
+      windows_dev, len, hist);
+  return launch_status();
+}

@@ -329,8 +329,10 @@ def conv2d_fp8_wgrad_general(
     stride: int = 1,
     padding: int = 1,
     split_k: int | None = None,
+    out_f32: bool = False,
 ) -> torch.Tensor:
-    """FP8 weight gradient -> bf16 (Cout, Cin, k, k) in channels-last memory."""
+    """FP8 weight gradient -> bf16 (Cout, Cin, k, k) in channels-last memory; ``out_f32``
+    gives the same values as fp32 (the gradient of a channels-last fp32 master weight)."""
     assert x.dtype == FP8_DTYPE and dy.dtype == FP8_DTYPE
     torch_checks_scale(x_scale, x.device)
     torch_checks_scale(dy_scale, x.device)
@@ -344,10 +346,11 @@ def conv2d_fp8_wgrad_general(
     if ws_bytes <= 0:
         raise RuntimeError(f"dpa_conv2d_wgrad_fp8: unsupported shape {(batch, cin, cout, height, width, kernel_size, stride)}")
     workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-    dw = torch.empty((cout, cin, kernel_size, kernel_size), device=x.device, dtype=torch.bfloat16,
+    dw = torch.empty((cout, cin, kernel_size, kernel_size), device=x.device,
+                     dtype=torch.float32 if out_f32 else torch.bfloat16,
                      memory_format=torch.channels_last)
     _lib.call(
-        "dpa_conv2d_wgrad_fp8",
+        "dpa_conv2d_wgrad_fp8_f32" if out_f32 else "dpa_conv2d_wgrad_fp8",
         x.data_ptr(), dy.data_ptr(), x_scale.data_ptr(), dy_scale.data_ptr(), dw.data_ptr(),
         workspace.data_ptr(), ws_bytes, batch, height, width, cin, cout, kernel_size,
         kernel_size, stride, padding, sk, _stream(x),
@@ -407,8 +410,10 @@ def conv2d_bwd_weight_fp8_prequantized(
     x_scale: torch.Tensor,
     dy_scale: torch.Tensor,
     split_k: int | None = None,
+    out_f32: bool = False,
 ) -> torch.Tensor:
-    """diffusion/fp8_kernels.py:723-808. Returns bf16 (Cout, Cin, 3, 3), channels-last."""
+    """diffusion/fp8_kernels.py:723-808. Returns bf16 (Cout, Cin, 3, 3), channels-last
+    (``out_f32``: the same values in fp32)."""
     batch, cin, cout, height, width = wgrad_shapes(x, dy, FP8_DTYPE)
     torch_checks_scale(x_scale, x.device)
     torch_checks_scale(dy_scale, x.device)
@@ -417,7 +422,7 @@ def conv2d_bwd_weight_fp8_prequantized(
     if not (x.is_contiguous(memory_format=torch.channels_last)
             and dy.is_contiguous(memory_format=torch.channels_last)):
         raise NotImplementedError
-    return conv2d_fp8_wgrad_general(x, dy, x_scale, dy_scale, 3, 1, 1, split_k)
+    return conv2d_fp8_wgrad_general(x, dy, x_scale, dy_scale, 3, 1, 1, split_k, out_f32)
 
 
 def conv2d_bwd_weight_fp8(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
@@ -686,8 +691,10 @@ def linear_fp8_wgrad_prequantized(
     dy: torch.Tensor,
     x_scale: torch.Tensor,
     dy_scale: torch.Tensor,
+    out_f32: bool = False,
 ) -> torch.Tensor:
-    """dw[N, K] = bf16(dy[M, N]^T @ x[M, K] * x_scale * dy_scale); e4m3 inputs.
+    """dw[N, K] = bf16(dy[M, N]^T @ x[M, K] * x_scale * dy_scale); e4m3 inputs (``out_f32``:
+    the same values in fp32).
 
     Runs the 1x1 weight-gradient kernel on M one-pixel images."""
     assert x.dtype == FP8_DTYPE and dy.dtype == FP8_DTYPE and x.ndim == dy.ndim == 2
@@ -702,9 +709,9 @@ def linear_fp8_wgrad_prequantized(
     if ws_bytes <= 0:
         raise RuntimeError(f"dpa_conv2d_wgrad_fp8: unsupported linear shape {(m, k, n)}")
     workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-    dw = torch.empty((n, k), device=x.device, dtype=torch.bfloat16)
+    dw = torch.empty((n, k), device=x.device, dtype=torch.float32 if out_f32 else torch.bfloat16)
     _lib.call(
-        "dpa_conv2d_wgrad_fp8",
+        "dpa_conv2d_wgrad_fp8_f32" if out_f32 else "dpa_conv2d_wgrad_fp8",
         x.data_ptr(), dy.data_ptr(), x_scale.data_ptr(), dy_scale.data_ptr(), dw.data_ptr(),
         workspace.data_ptr(), ws_bytes, m, 1, 1, k, n, 1, 1, 1, 0, 0, _stream(x),
     )
@@ -755,6 +762,131 @@ class LinearFP8Function(torch.autograd.Function):
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = dy2.float().sum(0)
         return dx, dw, db
+
+
+# --------------------------------------------------------------------------------------
+# layers whose weight was prepared for the step by weight_prep.WeightPrep (grouped launches):
+# same arithmetic and window updates as the per-call Functions above; the weight arrives as
+# e4m3 bytes, its transpose and the scale it was cast with, and the gradient of the fp32
+# master weight is returned in fp32 directly
+# --------------------------------------------------------------------------------------
+class Conv2dFP8DelayedPrepared(torch.autograd.Function):
+    """Conv2dFP8DelayedWindowed with the weight prepared: hist = the step's three window maxima
+    (acts, weights, dy) taken before any of this step's window writes; the x quantization
+    records its scale and advances the window position (the weight's record was written by the
+    preparation without advancing), so the window state after the step is the same."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, wq: torch.Tensor,
+                wq_t: torch.Tensor, w_scale: torch.Tensor, hist: torch.Tensor,
+                win_acts: torch.Tensor, win_dy: torch.Tensor,
+                window_pos: torch.Tensor) -> torch.Tensor:
+        x = x.to(torch.bfloat16)
+        assert x.is_contiguous(memory_format=torch.channels_last)
+        x_scale, dy_scale = hist[0], hist[2]
+        x_fp8, _ = quantize_fp8_delayed_window(x, x_scale, win_acts, window_pos, advance=True)
+        ctx.dy_window = win_dy
+        ctx.window_pos = window_pos
+        ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale, dy_scale)
+        return conv2d_fwd_fp8_prequantized(x_fp8, wq, x_scale, w_scale)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor) -> Any:
+        dy = dy.contiguous(memory_format=torch.channels_last)
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+        x_fp8, wq, wq_t, x_scale, w_scale, dy_scale = ctx.saved_tensors
+        dy_fp8, _ = quantize_fp8_delayed_window(dy, dy_scale, ctx.dy_window, ctx.window_pos,
+                                                advance=False)
+        batch, cin, cout, height, width = xgrad_shapes(dy_fp8, wq, FP8_DTYPE)
+        dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, (height, width), 1, 1,
+                                      weight_t=wq_t)
+        dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale, out_f32=True)
+        return dx, dw, None, None, None, None, None, None, None
+
+
+class Conv2dFP8GeneralPrepared(torch.autograd.Function):
+    """Conv2dFP8General (current scaling) with the weight prepared for the step."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, wq: torch.Tensor,
+                wq_t: torch.Tensor, w_scale: torch.Tensor, stride: int,
+                padding: int) -> torch.Tensor:
+        x = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        x_fp8, x_scale = quantize_fp8(x)
+        ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale)
+        ctx.stride, ctx.padding = stride, padding
+        ctx.input_hw = (x.shape[2], x.shape[3])
+        return conv2d_fp8_fwd_general(x_fp8, wq, x_scale, w_scale, stride, padding)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor) -> Any:
+        x_fp8, wq, wq_t, x_scale, w_scale = ctx.saved_tensors
+        dy = dy.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        dy_fp8, dy_scale = quantize_fp8(dy)
+        k = wq.shape[2]
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, ctx.input_hw,
+                                          ctx.stride, ctx.padding, weight_t=wq_t)
+        dw = conv2d_fp8_wgrad_general(x_fp8, dy_fp8, x_scale, dy_scale, k, ctx.stride,
+                                      ctx.padding, out_f32=True)
+        return dx, dw, None, None, None, None, None
+
+
+def _linear_dgrad_wt(dy: torch.Tensor, wq: torch.Tensor, wq_t: torch.Tensor, dy_scale, w_scale):
+    """linear_fp8_dgrad_prequantized with the transposed weight [K][N] given."""
+    m, n = dy.shape
+    k = wq.shape[1]
+    dx = torch.empty((m, k), device=dy.device, dtype=torch.bfloat16)
+    geom = (m, 1, 1, k, n, 1, 1, 1, 0)
+    ws_bytes = _lib.query("dpa_conv2d_dgrad_split_workspace_bytes", *geom)
+    workspace = _workspace(ws_bytes, dy.device)
+    _lib.call(
+        "dpa_conv2d_dgrad_fp8_wt_split",
+        dy.data_ptr(), wq_t.data_ptr(), dy_scale.data_ptr(), w_scale.data_ptr(), dx.data_ptr(),
+        _ptr(workspace), ws_bytes, *geom, _stream(dy),
+    )
+    return dx
+
+
+class LinearFP8Prepared(torch.autograd.Function):
+    """LinearFP8Function with the weight prepared for the step."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                wq: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor):
+        lead = x.shape[:-1]
+        n, k = weight.shape
+        x2 = x.to(torch.bfloat16).reshape(-1, k).contiguous()
+        xq, xs = quantize_fp8_tensor(x2)
+        b32 = None if bias is None else bias.detach().float().contiguous()
+        y = linear_fp8_prequantized(xq, wq, xs, w_scale, b32)
+        ctx.save_for_backward(xq, wq, wq_t, xs, w_scale)
+        ctx.lead = lead
+        ctx.has_bias = bias is not None
+        return y.reshape(*lead, n)
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    def backward(ctx: Any, dy: torch.Tensor):
+        xq, wq, wq_t, xs, wsc = ctx.saved_tensors
+        n, k = wq.shape
+        dy2 = dy.to(torch.bfloat16).reshape(-1, n).contiguous()
+        dyq, dys = quantize_fp8_tensor(dy2)
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = _linear_dgrad_wt(dyq, wq, wq_t, dys, wsc).reshape(*ctx.lead, k)
+        if ctx.needs_input_grad[1]:
+            dw = linear_fp8_wgrad_prequantized(xq, dyq, xs, dys, out_f32=True)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy2.float().sum(0)
+        return dx, dw, db, None, None, None
 
 
 def linear_fp8_autograd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:

@@ -76,6 +76,8 @@ class TrainState:
         self.ema_ddpm = DiffusionWrapper(EWMAWrapper(self.model, beta=ema_beta),
                                          schedule_type=schedule_type, max_t=max_t,
                                          in_dim=config.in_resolution, device=device)
+        # after the EMA copy: only the trained model prepares its FP8 weights per step
+        self.model.weight_prep_enabled = device == "cuda" or str(device).startswith("cuda")
         shape = (batch, config.in_channels, config.in_resolution, config.in_resolution)
         self.static_batch = torch.empty(shape, device=device).contiguous(
             memory_format=torch.channels_last)

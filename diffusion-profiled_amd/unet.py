@@ -62,7 +62,31 @@ def _on_gpu(x: torch.Tensor) -> bool:
     return x.is_cuda
 
 
-class Conv2dFP8(nn.Module):
+class _PreparedFP8Weight:
+    """Mixin of the FP8 layers: records the FP8 path a layer takes on the GPU (so a
+    weight_prep.WeightPrep plan can cover it) and hands out the step's prepared weight while
+    that plan is active (between its run() at the start of UNet.forward and the forward's end)."""
+
+    _fp8_mode: str | None = None
+    _fp8_prepared = None
+    _fp8_plan = None
+
+    def _note_fp8_mode(self, mode: str, w: torch.Tensor) -> None:
+        if self._fp8_mode is not None or not w.is_cuda or w.dtype != torch.float32:
+            return
+        dense = (w.is_contiguous(memory_format=torch.channels_last) if w.ndim == 4
+                 else w.is_contiguous())
+        if dense:
+            self._fp8_mode = mode
+
+    def _prepared(self, mode: str):
+        plan = self._fp8_plan
+        if self._fp8_prepared is None or self._fp8_mode != mode or plan is None or not plan.active:
+            return None
+        return self._fp8_prepared
+
+
+class Conv2dFP8(_PreparedFP8Weight, nn.Module):
     """3x3 / stride 1 / pad 1 conv, FP8 when the shape allows (diffusion/unet.py:32-94).
 
     In delayed mode the window maxima and window/position updates run inside
@@ -109,6 +133,12 @@ class Conv2dFP8(nn.Module):
             if self.scaling_type == "current":
                 return K.triton_conv2d_fp8(x, self.conv.weight)
             if self.fused_window_update:
+                pw = self._prepared("delayed")
+                if pw is not None:
+                    return K.Conv2dFP8DelayedPrepared.apply(
+                        x, self.conv.weight, pw.q, pw.qt, pw.scale, pw.hist,
+                        self.amax_window_acts, self.amax_window_dy, self.window_pos)
+                self._note_fp8_mode("delayed", self.conv.weight)
                 return K.Conv2dFP8DelayedWindowed.apply(
                     x, self.conv.weight, self.amax_window_acts, self.amax_window_weights,
                     self.amax_window_dy, self.window_pos)
@@ -126,11 +156,16 @@ class Conv2dFP8(nn.Module):
                 self.window_pos.add_(1).remainder_(self.amax_history)
             return out
         if self.conv_fp8_general(x, self.conv.weight):
+            pw = self._prepared("current")
+            if pw is not None:
+                return K.Conv2dFP8GeneralPrepared.apply(x, self.conv.weight, pw.q, pw.qt,
+                                                        pw.scale, 1, 1)
+            self._note_fp8_mode("current", self.conv.weight)
             return K.conv2d_fp8(x, self.conv.weight, 1, 1)
         return self.conv(x)
 
 
-class Conv1x1FP8(nn.Conv2d):
+class Conv1x1FP8(_PreparedFP8Weight, nn.Conv2d):
     """The bias-free 1x1 skip projection (diffusion/unet.py:137-139) with an FP8 path; the
     parameter is the nn.Conv2d ``weight`` so checkpoints are unchanged."""
 
@@ -140,11 +175,15 @@ class Conv1x1FP8(nn.Conv2d):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.fp8 and _on_gpu(x) and self.in_channels % 128 == 0 and self.out_channels % 128 == 0:
+            pw = self._prepared("current")
+            if pw is not None:
+                return K.Conv2dFP8GeneralPrepared.apply(x, self.weight, pw.q, pw.qt, pw.scale, 1, 0)
+            self._note_fp8_mode("current", self.weight)
             return K.conv2d_fp8(x, self.weight, 1, 0)
         return super().forward(x)
 
 
-class LinearFP8(nn.Linear):
+class LinearFP8(_PreparedFP8Weight, nn.Linear):
     """nn.Linear with the FP8 GEMM (forward and both gradients) when enabled and shaped for it."""
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True, fp8: bool = False):
@@ -153,6 +192,10 @@ class LinearFP8(nn.Linear):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.fp8 and _on_gpu(x) and K.linear_fp8_supported(self.in_features, self.out_features):
+            pw = self._prepared("linear")
+            if pw is not None:
+                return K.LinearFP8Prepared.apply(x, self.weight, self.bias, pw.q, pw.qt, pw.scale)
+            self._note_fp8_mode("linear", self.weight)
             return K.LinearFP8Function.apply(x, self.weight, self.bias)
         return super().forward(x)
 
@@ -410,7 +453,38 @@ class UNet(nn.Module):
         assert isinstance(self.out[-1], nn.Conv2d)
         torch.nn.init.zeros_(self.out[-1].weight)
 
+    # Grouped FP8 weight preparation (weight_prep.WeightPrep): when enabled, the first GPU
+    # forward records which layers run in FP8, the next builds the plan (outside graph capture)
+    # and every forward from then on starts with the plan's three launches.
+    weight_prep_enabled = False
+    _wprep = None
+    _fp8_seen = False
+
+    def _weight_prep(self, x: torch.Tensor):
+        if not self.weight_prep_enabled or not x.is_cuda:
+            return None
+        if self._wprep is None:
+            if not self._fp8_seen or torch.cuda.is_current_stream_capturing():
+                self._fp8_seen = True
+                return None
+            from .weight_prep import WeightPrep
+            self._wprep = WeightPrep.from_model(self)
+            if self._wprep is None:
+                self.weight_prep_enabled = False
+                return None
+        self._wprep.run()
+        self._wprep.active = True
+        return self._wprep
+
     def forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+        plan = self._weight_prep(x)
+        try:
+            return self._forward(x, t)
+        finally:
+            if plan is not None:
+                plan.active = False
+
+    def _forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
         t_emb = self.time_embed(self._timestep(t))
         act = self.conv_in(x)
         hs = []

@@ -1,0 +1,135 @@
+"""Grouped FP8 weight preparation for a model's FP8 layers.
+
+The reference quantizes each FP8 layer's weight inside the layer call (diffusion/unet.py:69-91
+-> diffusion/fp8_kernels.py:822-889: autocast bf16 cast, quantize_fp8 or quantize_fp8_delayed,
+window bookkeeping; the data gradient then reads the weight transposed). ``WeightPrep`` does
+the same for every FP8 layer of a model in three launches at the start of each forward
+(``dpa_window_max_grouped_f32`` + ``dpa_weight_prep_run``), straight from the fp32 master
+weights, into persistent buffers; the layers then run the ``*Prepared`` autograd Functions of
+``fp8_kernels`` and return fp32 weight gradients directly. Bytes, scales and window states are
+identical to the per-call path (tests/test_gpu_weight_prep.py).
+
+Each layer records the FP8 path it took (``_fp8_mode``: "delayed", "current" or "linear") on
+its first GPU call, so a plan covers exactly the layers the model runs in FP8 at its shapes.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int32, c_int64, c_void_p
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .fp8_kernels import FP8_DTYPE
+
+
+class DpaWeightEntry(ctypes.Structure):
+    """include/dpa_fp8.h ``DpaWeightEntry``."""
+
+    _fields_ = [
+        ("w", c_void_p), ("q", c_void_p), ("qt", c_void_p), ("scale_used", c_void_p),
+        ("cur_scale", c_void_p), ("prev_scale", c_void_p), ("window", c_void_p), ("pos", c_void_p),
+        ("window_len", c_int64), ("n", c_int64), ("cout", c_int32), ("taps", c_int32),
+        ("cin", c_int32), ("blk0", c_int32), ("nblk", c_int32), ("reserved", c_int32),
+    ]
+
+
+@dataclass
+class PreparedWeight:
+    """The step's prepared weight of one layer (views into persistent buffers)."""
+
+    q: torch.Tensor        # e4m3, the layer's weight shape and memory format
+    qt: torch.Tensor       # e4m3 [Cin][R][S][Cout] / [K][N]
+    scale: torch.Tensor    # [1] fp32: the scale q was cast with
+    hist: torch.Tensor | None  # [3] fp32 window maxima (acts, weights, dy), delayed layers
+
+
+def _fp8_weight(module) -> torch.Tensor:
+    return module.conv.weight if hasattr(module, "conv") else module.weight
+
+
+class WeightPrep:
+    """Persistent buffers and the device entry table for a list of FP8 layers."""
+
+    def __init__(self, layers: list):
+        assert layers, "no FP8 layers"
+        self.layers = layers
+        dev = _fp8_weight(layers[0]).device
+        delayed = [m for m in layers if m._fp8_mode == "delayed"]
+        self.n_delayed = len(delayed)
+        self.scales = torch.zeros(2 * len(layers), device=dev, dtype=torch.float32)
+        self.hist = torch.zeros(max(3 * self.n_delayed, 1), device=dev, dtype=torch.float32)
+        window_ptrs = []
+        self.window_len = 0
+        entries = (DpaWeightEntry * len(layers))()
+        self._keep = []
+        d = 0
+        for i, m in enumerate(layers):
+            w = _fp8_weight(m)
+            assert w.dtype == torch.float32 and w.device == dev
+            if w.ndim == 4:
+                cout, cin, kh, kw = w.shape
+                assert w.is_contiguous(memory_format=torch.channels_last)
+                q = torch.empty((cout, cin, kh, kw), device=dev, dtype=FP8_DTYPE,
+                                memory_format=torch.channels_last)
+                qt = torch.empty((cin, kh, kw, cout), device=dev, dtype=FP8_DTYPE)
+                taps = kh * kw
+            else:
+                cout, cin = w.shape
+                assert w.is_contiguous()
+                q = torch.empty((cout, cin), device=dev, dtype=FP8_DTYPE)
+                qt = torch.empty((cin, cout), device=dev, dtype=FP8_DTYPE)
+                taps = 1
+            e = entries[i]
+            e.w, e.q, e.qt = w.data_ptr(), q.data_ptr(), qt.data_ptr()
+            e.scale_used = self.scales[2 * i].data_ptr()
+            e.cur_scale = self.scales[2 * i + 1].data_ptr()
+            e.n, e.cout, e.taps, e.cin = w.numel(), cout, taps, cin
+            hist = None
+            if m._fp8_mode == "delayed":
+                hist = self.hist[3 * d:3 * d + 3]
+                e.prev_scale = hist[1].data_ptr()
+                e.window = m.amax_window_weights.data_ptr()
+                e.pos = m.window_pos.data_ptr()
+                e.window_len = m.amax_window_weights.numel()
+                for win in (m.amax_window_acts, m.amax_window_weights, m.amax_window_dy):
+                    assert win.dtype == torch.float32 and win.is_contiguous()
+                    if self.window_len == 0:
+                        self.window_len = win.numel()
+                    assert win.numel() == self.window_len, "one amax history length per model"
+                    window_ptrs.append(win.data_ptr())
+                d += 1
+            m._fp8_prepared = PreparedWeight(q, qt, self.scales[2 * i:2 * i + 1], hist)
+            m._fp8_plan = self
+            self._keep += [q, qt]
+        self.active = False
+        blocks = _lib.load().dpa_weight_prep_plan(ctypes.addressof(entries), len(layers))
+        _lib.check(min(blocks, 0), "dpa_weight_prep_plan")
+        self.blocks = int(blocks)
+        self.count = len(layers)
+        raw = bytes(entries)
+        self.table = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+        self.ws_bytes = _lib.query("dpa_weight_prep_workspace_bytes", self.blocks)
+        self.workspace = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+        self.windows = (torch.tensor(window_ptrs, dtype=torch.int64).to(dev)
+                        if window_ptrs else None)
+
+    def run(self) -> None:
+        """The step's weights: window maxima (delayed layers), then amax + cast of every weight."""
+        stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        if self.windows is not None:
+            _lib.call("dpa_window_max_grouped_f32", self.windows.data_ptr(), 3 * self.n_delayed,
+                      self.window_len, self.hist.data_ptr(), stream)
+        _lib.call("dpa_weight_prep_run", self.table.data_ptr(), self.count, self.blocks,
+                  self.workspace.data_ptr(), self.ws_bytes, stream)
+
+    def detach_layers(self) -> None:
+        for m in self.layers:
+            m._fp8_prepared = None
+            m._fp8_plan = None
+
+    @staticmethod
+    def from_model(model: torch.nn.Module) -> "WeightPrep | None":
+        layers = [m for m in model.modules() if getattr(m, "_fp8_mode", None) is not None]
+        return WeightPrep(layers) if layers else None

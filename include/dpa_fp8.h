@@ -235,6 +235,53 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
                               void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N,
                               int HW, int C, int G, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Grouped FP8 weight preparation. No single counterpart in the reference: it performs, for a
+ * model's whole FP8 weight set in three launches per step, what the reference does per layer
+ * call (autocast bf16 cast of the fp32 weight, quantize_fp8 / quantize_fp8_delayed of
+ * diffusion/fp8_kernels.py:518-601, the amax-window updates of diffusion/unet.py:69-91, and
+ * the weight transpose the data gradient needs). Bytes and scales are identical to the
+ * per-layer path: bf16(w) is the round-to-nearest-even cast, then the same scale and e4m3
+ * rule as dpa_quantize_fp8_bf16 (current scaling) or dpa_quantize_fp8_delayed_bf16 (delayed).
+ * ---------------------------------------------------------------------------------------- */
+typedef struct DpaWeightEntry {
+  const float* w;           /* fp32 weight, FP8 memory order: [Cout][R][S][Cin] or [N][K] */
+  void* q;                  /* e4m3 out, same order (8-B aligned) */
+  void* qt;                 /* e4m3 out [Cin][R][S][Cout] (data-gradient operand) or NULL */
+  float* scale_used;        /* the scale q was cast with */
+  float* cur_scale;         /* scale of this weight's own amax, or NULL */
+  const float* prev_scale;  /* delayed scaling: the scale to cast with; NULL: current */
+  float* window;            /* delayed: amax window, cur_scale recorded at *pos, or NULL */
+  int64_t* pos;             /*   (pos itself is not advanced) */
+  int64_t window_len;
+  int64_t n;                /* elements = cout * taps * cin (cin % 8 == 0) */
+  int32_t cout, taps, cin;  /* taps = R * S (1 for a linear) */
+  int32_t blk0, nblk;       /* filled in by dpa_weight_prep_plan */
+  int32_t reserved;
+} DpaWeightEntry;
+
+/* Assigns each entry its blocks (host array, in place); returns the total block count (> 0)
+ * or a negative status. Copy the planned array to device memory for dpa_weight_prep_run. */
+int dpa_weight_prep_plan(DpaWeightEntry* entries, int count);
+int64_t dpa_weight_prep_workspace_bytes(int total_blocks);
+/* Two launches: per-block amax of bf16(w), then cast + transposed cast + scales + window
+ * records. Entries whose prev_scale points at dpa_window_max_grouped_f32 output must follow
+ * that call on the same stream. */
+int dpa_weight_prep_run(const DpaWeightEntry* entries_dev, int count, int total_blocks,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+/* hist[i] = max over window i of len floats (torch.max; NaN if the window holds one);
+ * windows_dev: device array of count window pointers. One launch for every window. */
+int dpa_window_max_grouped_f32(const float* const* windows_dev, int count, int64_t len,
+                               float* hist, void* stream);
+
+/* dpa_conv2d_wgrad_fp8 writing fp32 dw holding the bf16-rounded values (what autograd's cast
+ * of the reference's bf16 gradient to an fp32 parameter produces), in the same
+ * [Cout][R][S][Cin] order: the gradient of a channels-last fp32 master weight directly. */
+int dpa_conv2d_wgrad_fp8_f32(const void* xq, const void* dyq, const float* x_scale,
+                             const float* dy_scale, float* dw, void* workspace,
+                             int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout,
+                             int R, int S, int stride, int pad, int split_k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

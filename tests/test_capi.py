@@ -127,3 +127,33 @@ def test_split_workspace_queries(lib):
     assert lib.dpa_gemm_split_workspace_bytes(128, 512, 128) == 0
     assert lib.dpa_gemm_split_workspace_bytes(128, 500, 1024) == 0
     assert lib.dpa_conv2d_fwd_split_workspace_bytes(128, 4, 4, 96, 256, 3, 3, 1, 1) == 0
+
+
+def test_weight_prep_plan_on_host(lib):
+    """dpa_weight_prep_plan reads the ctypes DpaWeightEntry array (layout of
+    include/dpa_fp8.h) and assigns blocks of 8192 elements per weight, in order."""
+    import ctypes
+    WP = dpa_mod("weight_prep")
+    shapes = [(128, 9, 128), (256, 1, 512), (512, 1, 128)]
+    entries = (WP.DpaWeightEntry * len(shapes))()
+    for e, (co, taps, ci) in zip(entries, shapes):
+        e.w, e.q, e.qt, e.scale_used = 0x10000, 0x20000, 0x30000, 0x40000
+        e.n, e.cout, e.taps, e.cin = co * taps * ci, co, taps, ci
+    total = lib.dpa_weight_prep_plan(ctypes.addressof(entries), len(shapes))
+    nblk = [-(-co * taps * ci // 8192) for co, taps, ci in shapes]
+    assert total == sum(nblk)
+    assert [e.nblk for e in entries] == nblk
+    assert [e.blk0 for e in entries] == [0, nblk[0], nblk[0] + nblk[1]]
+    assert lib.dpa_weight_prep_workspace_bytes(total) == 4 * total
+    entries[1].cin = 500                      # n no longer cout * taps * cin
+    assert lib.dpa_weight_prep_plan(ctypes.addressof(entries), len(shapes)) == -4
+    entries[1].cin = 512
+    entries[2].w = 0x10004                    # fp32 weights must be 16-B aligned
+    assert lib.dpa_weight_prep_plan(ctypes.addressof(entries), len(shapes)) == -3
+    nul = None
+    assert lib.dpa_weight_prep_run(nul, 3, total, ctypes.c_void_p(0x1000), 4 * total, nul) == -1
+    assert lib.dpa_weight_prep_run(ctypes.c_void_p(0x1000), 3, total, ctypes.c_void_p(0x1000), 8, nul) == -5
+    assert lib.dpa_window_max_grouped_f32(nul, 3, 1024, ctypes.c_void_p(0x1000), nul) == -1
+    assert lib.dpa_conv2d_wgrad_fp8_f32(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000),
+                                        ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1008), ctypes.c_void_p(0x1000),
+                                        1 << 30, 2, 8, 8, 128, 128, 3, 3, 1, 1, 0, nul) == -3
