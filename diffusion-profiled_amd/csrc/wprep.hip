@@ -15,13 +15,15 @@
 //                               scale used, this amax's scale and its window record
 // with scale = *prev_scale (delayed scaling: the window maximum) or the scale of this
 // weight's own amax (current scaling). bf16(w) is the round-to-nearest-even cast autocast
-// performs, so every byte and scale equals the per-layer path's.
+// performs, so every byte and scale equals the per-layer path's. Each block takes one tile
+// of 64 output x 64 input channels of one tap; the transposed copy goes through LDS, so both
+// copies are written in 64-B runs.
 #include "dpa_common.hpp"
 
 namespace dpa {
 
 constexpr int kWpThreads = 256;
-constexpr int kWpElems = kWpThreads * 8 * 4;  // elements per block: 4 rounds of 8 per thread
+constexpr int kWpTile = 64;  // a block's tile: 64 output x 64 input channels of one tap
 
 // Entry of block b: the last entry with blk0 <= b (entries are in blk0 order).
 __device__ __forceinline__ int wp_entry_of(const DpaWeightEntry* __restrict__ e, int count,
@@ -33,6 +35,31 @@ __device__ __forceinline__ int wp_entry_of(const DpaWeightEntry* __restrict__ e,
     else hi = mid - 1;
   }
   return lo;
+}
+
+// Tile t of an entry: (co tile, tap, ci tile) with ci tiles fastest.
+struct WpTile {
+  int co0, tap, ci0;
+};
+__device__ __forceinline__ WpTile wp_tile(const DpaWeightEntry& E, int t) {
+  const int nci = (E.cin + kWpTile - 1) / kWpTile;
+  WpTile r;
+  r.ci0 = (t % nci) * kWpTile;
+  t /= nci;
+  r.tap = t % E.taps;
+  r.co0 = (t / E.taps) * kWpTile;
+  return r;
+}
+
+// Thread's part of a tile: row co0 + (threadIdx / 8) + 32 h (h = 0, 1), 8 consecutive
+// channels ci0 + 8 (threadIdx % 8). Returns false where the row or channels fall outside.
+__device__ __forceinline__ bool wp_slot(const DpaWeightEntry& E, const WpTile& T, int h,
+                                        int64_t& off, int& row, int& c8) {
+  row = (threadIdx.x >> 3) + 32 * h;
+  c8 = (threadIdx.x & 7) * 8;
+  const int co = T.co0 + row, ci = T.ci0 + c8;
+  off = ((int64_t)co * E.taps + T.tap) * E.cin + ci;
+  return co < E.cout && ci < E.cin;  // cin % 8 == 0: a group of 8 is all in or all out
 }
 
 // 8 fp32 -> 8 bf16 (RNE) packed as one uint4.
@@ -64,27 +91,43 @@ __global__ __launch_bounds__(kWpThreads) void wprep_amax_kernel(
   if (threadIdx.x == 0) s_t = wp_entry_of(e, count, blockIdx.x);
   __syncthreads();
   const DpaWeightEntry& E = e[s_t];
-  const int64_t i0 = (int64_t)(blockIdx.x - E.blk0) * kWpElems;
-  const int64_t i1 = i0 + kWpElems < E.n ? i0 + kWpElems : E.n;
+  const WpTile T = wp_tile(E, blockIdx.x - E.blk0);
   us2 acc = {0, 0};
-  for (int64_t i = i0 + threadIdx.x * 8; i < i1; i += kWpThreads * 8)
-    acc = absmax8(acc, wp_bf16x8(E.w + i));
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int64_t off;
+    int row, c8;
+    if (wp_slot(E, T, h, off, row, c8)) acc = absmax8(acc, wp_bf16x8(E.w + off));
+  }
   const uint32_t m = wp_block_max(acc.x > acc.y ? acc.x : acc.y, red);
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
 }
 
+// Cast of one tile: q rows out directly (64 B per row), the transposed copy through an LDS
+// tile so that its rows (64 output channels of one input channel) leave as 64-B runs too.
 __global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
     const DpaWeightEntry* __restrict__ e, int count, const uint32_t* __restrict__ partials) {
   __shared__ uint32_t red[kWpThreads / 64];
+  __shared__ uint32_t tile[kWpTile][kWpTile / 4 + 1];  // [co row][ci / 4], padded
   __shared__ int s_t;
   if (threadIdx.x == 0) s_t = wp_entry_of(e, count, blockIdx.x);
   __syncthreads();
   const DpaWeightEntry& E = e[s_t];
+  const WpTile T = wp_tile(E, blockIdx.x - E.blk0);
+  uint4 v[2];
+  bool ok[2];
+  int64_t off[2];
+  int row[2], c8[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    ok[h] = wp_slot(E, T, h, off[h], row[h], c8[h]);
+    if (ok[h]) v[h] = wp_bf16x8(E.w + off[h]);
+  }
   // this weight's amax from its blocks' partials (every block re-reduces them)
   uint32_t m = 0;
   for (int i = threadIdx.x; i < E.nblk; i += kWpThreads) {
-    const uint32_t v = partials[E.blk0 + i];
-    m = m > v ? m : v;
+    const uint32_t pv = partials[E.blk0 + i];
+    m = m > pv ? m : pv;
   }
   const uint32_t amax = wp_block_max(m, red);
   const float cur = scale_from_amax_bits(amax);
@@ -95,25 +138,39 @@ __global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
     window_record(cur, E.window, E.pos, E.window_len, 0);
   }
   const float r = quant_recip(scale);
-  const int64_t i0 = (int64_t)(blockIdx.x - E.blk0) * kWpElems;
-  const int64_t i1 = i0 + kWpElems < E.n ? i0 + kWpElems : E.n;
   uint8_t* q = (uint8_t*)E.q;
-  uint8_t* qt = (uint8_t*)E.qt;
-  const int64_t tc = (int64_t)E.taps * E.cin;
-  for (int64_t i = i0 + threadIdx.x * 8; i < i1; i += kWpThreads * 8) {
-    const uint4 v = wp_bf16x8(E.w + i);
-    const uint2 o = r != 0.0f ? quant8_rcp(v, scale, r) : quant8(v, scale);
-    *reinterpret_cast<uint2*>(q + i) = o;
-    if (qt) {
-      // element i = (co, tap, ci): qt[(ci * taps + tap) * cout + co]; 8 consecutive ci
-      const int64_t co = i / tc;
-      const int64_t rem = i - co * tc;
-      const int64_t tap = rem / E.cin;
-      const int64_t ci = rem - tap * E.cin;
-      uint8_t* dst = qt + (ci * E.taps + tap) * E.cout + co;
-      const int64_t step = (int64_t)E.taps * E.cout;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) dst[k * step] = (uint8_t)((k < 4 ? o.x : o.y) >> (8 * (k & 3)));
+  for (int h = 0; h < 2; ++h) {
+    uint2 o = uint2{0u, 0u};
+    if (ok[h]) {
+      o = r != 0.0f ? quant8_rcp(v[h], scale, r) : quant8(v[h], scale);
+      *reinterpret_cast<uint2*>(q + off[h]) = o;
+    }
+    tile[row[h]][c8[h] / 4] = o.x;
+    tile[row[h]][c8[h] / 4 + 1] = o.y;
+  }
+  if (!E.qt) return;
+  __syncthreads();
+  // qt[(ci * taps + tap) * cout + co]: thread -> input channel ci0 + (tid / 16) + 16 k, output
+  // channels co0 + 4 (tid % 16) .. +3 (one u32)
+  uint8_t* qt = (uint8_t*)E.qt;
+  const int cc = (threadIdx.x & 15) * 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int cr = (threadIdx.x >> 4) + 16 * k;  // input channel within the tile
+    const int ci = T.ci0 + cr, co = T.co0 + cc;
+    if (ci >= E.cin || co >= E.cout) continue;
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t word = tile[cc + j][cr >> 2];
+      w |= ((word >> (8 * (cr & 3))) & 0xffu) << (8 * j);
+    }
+    uint8_t* dst = qt + ((int64_t)ci * E.taps + T.tap) * E.cout + co;
+    if (co + 4 <= E.cout && (E.cout & 3) == 0) {
+      *reinterpret_cast<uint32_t*>(dst) = w;
+    } else {
+      for (int j = 0; j < 4 && co + j < E.cout; ++j) dst[j] = (uint8_t)(w >> (8 * j));
     }
   }
 }
@@ -168,7 +225,7 @@ extern "C" int dpa_weight_prep_plan(DpaWeightEntry* entries, int count) {
     if (E.n != (int64_t)E.cout * E.taps * E.cin || E.cin % 8 != 0) return DPA_ERR_SHAPE;
     if (!aligned(E.w, 16) || !aligned(E.q, 8)) return DPA_ERR_ALIGN;
     E.blk0 = (int32_t)blocks;
-    E.nblk = (int32_t)ceil_div(E.n, (int64_t)kWpElems);
+    E.nblk = (int32_t)(ceil_div(E.cout, kWpTile) * E.taps * ceil_div(E.cin, kWpTile));
     blocks += E.nblk;
     if (blocks > 0x7fffffff) return DPA_ERR_SIZE;
   }

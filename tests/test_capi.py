@@ -131,7 +131,8 @@ def test_split_workspace_queries(lib):
 
 def test_weight_prep_plan_on_host(lib):
     """dpa_weight_prep_plan reads the ctypes DpaWeightEntry array (layout of
-    include/dpa_fp8.h) and assigns blocks of 8192 elements per weight, in order."""
+    include/dpa_fp8.h) and assigns one block per tile of 64 x 64 channels of one tap, in
+    order."""
     import ctypes
     WP = dpa_mod("weight_prep")
     shapes = [(128, 9, 128), (256, 1, 512), (512, 1, 128)]
@@ -140,7 +141,8 @@ def test_weight_prep_plan_on_host(lib):
         e.w, e.q, e.qt, e.scale_used = 0x10000, 0x20000, 0x30000, 0x40000
         e.n, e.cout, e.taps, e.cin = co * taps * ci, co, taps, ci
     total = lib.dpa_weight_prep_plan(ctypes.addressof(entries), len(shapes))
-    nblk = [-(-co * taps * ci // 8192) for co, taps, ci in shapes]
+    nblk = [-(-co // 64) * taps * -(-ci // 64) for co, taps, ci in shapes]
+    assert nblk == [36, 32, 16]
     assert total == sum(nblk)
     assert [e.nblk for e in entries] == nblk
     assert [e.blk0 for e in entries] == [0, nblk[0], nblk[0] + nblk[1]]
