@@ -183,14 +183,17 @@ def test_graph_captured_step_matches_eager_steps():
         la, lb = float(a.loss_acc), float(b.loss_acc)
         assert math.isfinite(la) and la == pytest.approx(lb, rel=1e-5), (i, la, lb)
         for (name, p), q in zip(a.model.named_parameters(), b.model.parameters()):
-            # the bf16 input/output convs run MIOpen, whose weight gradient is not
-            # bit-reproducible; AdamW turns that into small relative parameter differences
-            rtol = 1e-2 if name in ("conv_in.weight", "out.2.weight") else 1e-4
-            torch.testing.assert_close(p, q, rtol=rtol, atol=1e-6, msg=f"replay {i}: {name}")
+            # per tensor, normwise: the attention backward (atomics) and the bf16 input/output
+            # convs (MIOpen) are not bit-reproducible, and AdamW turns gradient noise into
+            # relative differences of single small-gradient elements
+            assert nerr(p, q) < 1e-4, (i, name, nerr(p, q))
     for (name, p), q in zip(a.ema_ddpm.model.model.named_parameters(), b.ema_ddpm.model.model.parameters()):
-        torch.testing.assert_close(p, q, rtol=1e-4, atol=1e-6, msg=f"ema {name}")
+        assert nerr(p, q) < 1e-4, ("ema", name, nerr(p, q))
     for (name, buf), q in zip(a.model.named_buffers(), b.model.buffers()):
-        torch.testing.assert_close(buf, q, rtol=1e-5, atol=0, msg=name)
+        if buf.dtype == torch.long:                  # window positions: exact
+            assert torch.equal(buf, q), name
+        else:                                        # amax windows: scales of bf16 amaxes
+            torch.testing.assert_close(buf, q, rtol=2**-7, atol=0, msg=name)
 
 
 def _conv_by_matmul(x: torch.Tensor, w: torch.Tensor, pad: int) -> torch.Tensor:
