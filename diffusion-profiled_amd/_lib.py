@@ -49,6 +49,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 6 + [c_int64] + [c_int] * 10 + [c_void_p],
     ),
     "dpa_gemm_fp8": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_quant_partials_count": (c_int, [c_int64]),
+    "dpa_quantize_fp8_delayed_deferred_bf16": (
+        c_int,
+        [c_void_p, c_int64] + [c_void_p] * 3 + [c_int, c_void_p, c_void_p],
+    ),
+    "dpa_delayed_windows_finalize": (c_int, [c_void_p, c_int, c_void_p]),
     "dpa_weight_prep_plan": (c_int, [c_void_p, c_int]),
     "dpa_weight_prep_workspace_bytes": (c_int64, [c_int]),
     "dpa_weight_prep_run": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),

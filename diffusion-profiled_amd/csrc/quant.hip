@@ -123,11 +123,12 @@ __global__ __launch_bounds__(kQThreads) void cast_current_kernel(
   if (blockIdx.x == 0) cast_tail(x, tail, n, scale, q);
 }
 
-// Delayed scaling, one pass: q = cast(x, *prev_scale) and per-block amax of x.
+// Delayed scaling, one pass: q = cast(x, *prev_scale) and per-block amax of x. count (if
+// given) receives the number of partials, for a finalize in a later launch.
 template <bool kVec>
 __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
     const uint16_t* __restrict__ x, int64_t n, const float* __restrict__ prev_scale,
-    uint8_t* __restrict__ q, uint32_t* __restrict__ partials) {
+    uint8_t* __restrict__ q, uint32_t* __restrict__ partials, uint32_t* __restrict__ count) {
   __shared__ uint32_t red[kQThreads / 64];
   const float scale = *prev_scale;
   us2 acc = {0, 0};
@@ -159,6 +160,33 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
   m = m > accs ? m : accs;
   m = block_max_u32(m, red);
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
+  if (count && blockIdx.x == 0 && threadIdx.x == 0) *count = gridDim.x;
+}
+
+// Deferred window records of delayed-scaling layers (one workgroup per layer), run at the
+// start of the next step: the step's x and dy quantizations left their block maxima and
+// counts; window_acts[pos] = scale(max x partials), window_dy[pos + 1] = scale(max dy
+// partials), pos = pos + 1 (mod len) when x was quantized -- the state the per-call update
+// (diffusion/unet.py:82-91, fp8_kernels.py:888-889) leaves after the step. Counts go back to 0.
+__global__ __launch_bounds__(kQThreads) void deferred_windows_kernel(
+    const DpaDeferredWindow* __restrict__ layers) {
+  __shared__ uint32_t red[kQThreads / 64];
+  const DpaDeferredWindow& L = layers[blockIdx.x];
+  const uint32_t nx = *L.x_count, ndy = *L.dy_count;
+  const uint32_t ax = reduce_partials(L.x_partials, (int)nx, red);
+  __syncthreads();
+  const uint32_t ady = reduce_partials(L.dy_partials, (int)ndy, red);
+  if (threadIdx.x == 0) {
+    const int64_t p = *L.pos;
+    if (p >= 0 && p < L.len) {
+      const int64_t p1 = p + 1 == L.len ? 0 : p + 1;
+      if (nx > 0) L.window_acts[p] = scale_from_amax_bits(ax);
+      if (ndy > 0) L.window_dy[p1] = scale_from_amax_bits(ady);
+      if (nx > 0) *L.pos = p1;
+    }
+    *L.x_count = 0;
+    *L.dy_count = 0;
+  }
 }
 
 // Delayed scaling, finalize: cur_scale = scale(max(partials))  (finalize_amax_kernel), and
@@ -330,9 +358,11 @@ static int quantize_delayed(const void* x, int64_t n, const float* prev_scale, v
     return launch_status();
   }
   if (vec)
-    cast_delayed_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part);
+    cast_delayed_kernel<true><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part,
+                                                       nullptr);
   else
-    cast_delayed_kernel<false><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part);
+    cast_delayed_kernel<false><<<np, kQThreads, 0, s>>>(xp, n, prev_scale, (uint8_t*)q, part,
+                                                        nullptr);
   finalize_scale_kernel<<<1, kQThreads, 0, s>>>(part, np, cur_scale_out, window, window_pos,
                                                  window_len, advance);
   return launch_status();
@@ -356,6 +386,34 @@ extern "C" int dpa_quantize_fp8_delayed_window_bf16(const void* x, int64_t n,
   if (!aligned(window, 4) || !aligned(window_pos, 8)) return DPA_ERR_ALIGN;
   return quantize_delayed(x, n, prev_scale, q, cur_scale_out, window, window_pos, window_len,
                           advance_pos ? 1 : 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dpa_quant_partials_count(int64_t n) {
+  return n > 0 ? grid_for(n, kAmaxBlocks) : 0;
+}
+
+extern "C" int dpa_quantize_fp8_delayed_deferred_bf16(const void* x, int64_t n,
+                                                      const float* prev_scale, void* q,
+                                                      uint32_t* partials, int partials_cap,
+                                                      uint32_t* count, void* stream) {
+  if (!x || !q || !prev_scale || !partials || !count) return DPA_ERR_NULL;
+  if (n <= 0) return DPA_ERR_SIZE;
+  const int np = grid_for(n, kAmaxBlocks);
+  if (partials_cap < np) return DPA_ERR_WORKSPACE;
+  if (!aligned(x, 16) || !aligned(q, 8) || !aligned(prev_scale, 4) || !aligned(partials, 4) ||
+      !aligned(count, 4))
+    return DPA_ERR_ALIGN;
+  cast_delayed_kernel<true><<<np, kQThreads, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, n, prev_scale, (uint8_t*)q, partials, count);
+  return launch_status();
+}
+
+extern "C" int dpa_delayed_windows_finalize(const DpaDeferredWindow* layers_dev, int count,
+                                            void* stream) {
+  if (!layers_dev) return DPA_ERR_NULL;
+  if (count <= 0) return DPA_ERR_SIZE;
+  deferred_windows_kernel<<<(unsigned)count, kQThreads, 0, (hipStream_t)stream>>>(layers_dev);
+  return launch_status();
 }
 
 extern "C" int dpa_window_max3_f32(const float* w0, const float* w1, const float* w2, int64_t n,

@@ -167,6 +167,23 @@ def quantize_fp8_delayed_window(tensor: torch.Tensor, prev_scale: torch.Tensor,
     return quantized, scale
 
 
+def quantize_fp8_delayed_deferred(tensor: torch.Tensor, prev_scale: torch.Tensor,
+                                  partials: torch.Tensor, count: torch.Tensor) -> torch.Tensor:
+    """``quantize_fp8_delayed``'s cast (scale ``prev_scale``) leaving the block maxima of this
+    tensor and their count in persistent buffers for a later ``dpa_delayed_windows_finalize``
+    (the window record of the step, written at the start of the next one)."""
+    assert tensor.dtype == torch.bfloat16 and tensor.is_cuda
+    if not _dense(tensor):
+        tensor = tensor.contiguous()
+    quantized = torch.empty_like(tensor, dtype=FP8_DTYPE, memory_format=torch.preserve_format)
+    _lib.call(
+        "dpa_quantize_fp8_delayed_deferred_bf16",
+        tensor.data_ptr(), tensor.numel(), prev_scale.data_ptr(), quantized.data_ptr(),
+        partials.data_ptr(), partials.numel(), count.data_ptr(), _stream(tensor),
+    )
+    return quantized
+
+
 def window_max3(w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
     """``torch.stack([w0.max(), w1.max(), w2.max()])`` for three equal-length fp32 windows in
     one launch (diffusion/unet.py:72-73, fp8_kernels.py:849)."""
@@ -772,22 +789,22 @@ class LinearFP8Function(torch.autograd.Function):
 # --------------------------------------------------------------------------------------
 class Conv2dFP8DelayedPrepared(torch.autograd.Function):
     """Conv2dFP8DelayedWindowed with the weight prepared: hist = the step's three window maxima
-    (acts, weights, dy) taken before any of this step's window writes; the x quantization
-    records its scale and advances the window position (the weight's record was written by the
-    preparation without advancing), so the window state after the step is the same."""
+    (acts, weights, dy) taken before any of this step's window writes. The x and dy
+    quantizations cast with hist[0] / hist[2] and leave their block maxima in the layer's
+    persistent buffers (``parts`` = x partials, x count, dy partials, dy count); the weight
+    preparation of the next step (or ``WeightPrep.flush``) writes their window records and
+    advances the position, which gives the per-call path's window state."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, wq: torch.Tensor,
                 wq_t: torch.Tensor, w_scale: torch.Tensor, hist: torch.Tensor,
-                win_acts: torch.Tensor, win_dy: torch.Tensor,
-                window_pos: torch.Tensor) -> torch.Tensor:
+                parts: tuple) -> torch.Tensor:
         x = x.to(torch.bfloat16)
         assert x.is_contiguous(memory_format=torch.channels_last)
         x_scale, dy_scale = hist[0], hist[2]
-        x_fp8, _ = quantize_fp8_delayed_window(x, x_scale, win_acts, window_pos, advance=True)
-        ctx.dy_window = win_dy
-        ctx.window_pos = window_pos
+        x_fp8 = quantize_fp8_delayed_deferred(x, x_scale, parts[0], parts[1])
+        ctx.parts = parts
         ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale, dy_scale)
         return conv2d_fwd_fp8_prequantized(x_fp8, wq, x_scale, w_scale)
 
@@ -798,13 +815,12 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
         x_fp8, wq, wq_t, x_scale, w_scale, dy_scale = ctx.saved_tensors
-        dy_fp8, _ = quantize_fp8_delayed_window(dy, dy_scale, ctx.dy_window, ctx.window_pos,
-                                                advance=False)
+        dy_fp8 = quantize_fp8_delayed_deferred(dy, dy_scale, ctx.parts[2], ctx.parts[3])
         batch, cin, cout, height, width = xgrad_shapes(dy_fp8, wq, FP8_DTYPE)
         dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, (height, width), 1, 1,
                                       weight_t=wq_t)
         dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale, out_f32=True)
-        return dx, dw, None, None, None, None, None, None, None
+        return dx, dw, None, None, None, None, None
 
 
 class Conv2dFP8GeneralPrepared(torch.autograd.Function):

@@ -136,8 +136,7 @@ class Conv2dFP8(_PreparedFP8Weight, nn.Module):
                 pw = self._prepared("delayed")
                 if pw is not None:
                     return K.Conv2dFP8DelayedPrepared.apply(
-                        x, self.conv.weight, pw.q, pw.qt, pw.scale, pw.hist,
-                        self.amax_window_acts, self.amax_window_dy, self.window_pos)
+                        x, self.conv.weight, pw.q, pw.qt, pw.scale, pw.hist, pw.parts)
                 self._note_fp8_mode("delayed", self.conv.weight)
                 return K.Conv2dFP8DelayedWindowed.apply(
                     x, self.conv.weight, self.amax_window_acts, self.amax_window_weights,

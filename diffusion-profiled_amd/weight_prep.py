@@ -24,6 +24,16 @@ from . import _lib
 from .fp8_kernels import FP8_DTYPE
 
 
+class DpaDeferredWindow(ctypes.Structure):
+    """include/dpa_fp8.h ``DpaDeferredWindow``."""
+
+    _fields_ = [
+        ("x_partials", c_void_p), ("x_count", c_void_p), ("dy_partials", c_void_p),
+        ("dy_count", c_void_p), ("window_acts", c_void_p), ("window_dy", c_void_p),
+        ("pos", c_void_p), ("len", c_int64),
+    ]
+
+
 class DpaWeightEntry(ctypes.Structure):
     """include/dpa_fp8.h ``DpaWeightEntry``."""
 
@@ -43,6 +53,7 @@ class PreparedWeight:
     qt: torch.Tensor       # e4m3 [Cin][R][S][Cout] / [K][N]
     scale: torch.Tensor    # [1] fp32: the scale q was cast with
     hist: torch.Tensor | None  # [3] fp32 window maxima (acts, weights, dy), delayed layers
+    parts: tuple | None = None  # delayed layers: (x partials, x count, dy partials, dy count)
 
 
 def _fp8_weight(module) -> torch.Tensor:
@@ -60,6 +71,11 @@ class WeightPrep:
         self.n_delayed = len(delayed)
         self.scales = torch.zeros(2 * len(layers), device=dev, dtype=torch.float32)
         self.hist = torch.zeros(max(3 * self.n_delayed, 1), device=dev, dtype=torch.float32)
+        # deferred window records of the delayed layers' x / dy quantizations
+        cap = _lib.query("dpa_quant_partials_count", 1 << 40)   # the partial-count cap
+        self.dparts = torch.zeros((max(self.n_delayed, 1), 2, cap), device=dev, dtype=torch.int32)
+        self.dcounts = torch.zeros((max(self.n_delayed, 1), 2), device=dev, dtype=torch.int32)
+        deferred = (DpaDeferredWindow * max(self.n_delayed, 1))()
         window_ptrs = []
         self.window_len = 0
         entries = (DpaWeightEntry * len(layers))()
@@ -86,7 +102,7 @@ class WeightPrep:
             e.scale_used = self.scales[2 * i].data_ptr()
             e.cur_scale = self.scales[2 * i + 1].data_ptr()
             e.n, e.cout, e.taps, e.cin = w.numel(), cout, taps, cin
-            hist = None
+            hist = parts = None
             if m._fp8_mode == "delayed":
                 hist = self.hist[3 * d:3 * d + 3]
                 e.prev_scale = hist[1].data_ptr()
@@ -99,8 +115,17 @@ class WeightPrep:
                         self.window_len = win.numel()
                     assert win.numel() == self.window_len, "one amax history length per model"
                     window_ptrs.append(win.data_ptr())
+                parts = (self.dparts[d, 0], self.dcounts[d, 0:1], self.dparts[d, 1],
+                         self.dcounts[d, 1:2])
+                dw = deferred[d]
+                dw.x_partials, dw.x_count = parts[0].data_ptr(), parts[1].data_ptr()
+                dw.dy_partials, dw.dy_count = parts[2].data_ptr(), parts[3].data_ptr()
+                dw.window_acts = m.amax_window_acts.data_ptr()
+                dw.window_dy = m.amax_window_dy.data_ptr()
+                dw.pos = m.window_pos.data_ptr()
+                dw.len = m.amax_window_acts.numel()
                 d += 1
-            m._fp8_prepared = PreparedWeight(q, qt, self.scales[2 * i:2 * i + 1], hist)
+            m._fp8_prepared = PreparedWeight(q, qt, self.scales[2 * i:2 * i + 1], hist, parts)
             m._fp8_plan = self
             self._keep += [q, qt]
         self.active = False
@@ -114,10 +139,21 @@ class WeightPrep:
         self.workspace = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
         self.windows = (torch.tensor(window_ptrs, dtype=torch.int64).to(dev)
                         if window_ptrs else None)
+        self.deferred = torch.frombuffer(bytearray(bytes(deferred)), dtype=torch.uint8).to(dev)
+
+    def flush(self) -> None:
+        """Write the window records the delayed layers' last x / dy quantizations left pending
+        (run() does this first; call it before reading or saving the windows)."""
+        if self.n_delayed:
+            stream = torch.cuda.current_stream(self.table.device).cuda_stream
+            _lib.call("dpa_delayed_windows_finalize", self.deferred.data_ptr(), self.n_delayed,
+                      stream)
 
     def run(self) -> None:
-        """The step's weights: window maxima (delayed layers), then amax + cast of every weight."""
+        """The step's weights: the previous step's pending window records, the window maxima
+        (delayed layers), then amax + cast of every weight."""
         stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        self.flush()
         if self.windows is not None:
             _lib.call("dpa_window_max_grouped_f32", self.windows.data_ptr(), 3 * self.n_delayed,
                       self.window_len, self.hist.data_ptr(), stream)

@@ -274,6 +274,32 @@ int dpa_weight_prep_run(const DpaWeightEntry* entries_dev, int count, int total_
 int dpa_window_max_grouped_f32(const float* const* windows_dev, int count, int64_t len,
                                float* hist, void* stream);
 
+/* Deferred window records for layers whose weights are prepared per step. No counterpart in
+ * the reference (which records each scale in its own finalize, diffusion/fp8_kernels.py:
+ * 90-102, and the module's scatter_, diffusion/unet.py:82-91): the x and dy quantizations of
+ * a delayed-scaling layer cast with their window scale (as dpa_quantize_fp8_delayed_bf16) and
+ * leave their block maxima and count in caller-owned persistent buffers; one launch at the
+ * start of the next step writes every layer's records (window_acts[pos] from x,
+ * window_dy[pos + 1] from dy, pos + 1 if x was quantized), which is the window state the
+ * per-call path leaves after the step. Counts must be zero before the first use; the
+ * finalize sets them back to zero. */
+typedef struct DpaDeferredWindow {
+  const uint32_t* x_partials;   /* >= dpa_quant_partials_count(numel(x)) u32 */
+  uint32_t* x_count;
+  const uint32_t* dy_partials;
+  uint32_t* dy_count;
+  float* window_acts;
+  float* window_dy;
+  int64_t* pos;
+  int64_t len;
+} DpaDeferredWindow;
+
+int dpa_quant_partials_count(int64_t n);
+int dpa_quantize_fp8_delayed_deferred_bf16(const void* x, int64_t n, const float* prev_scale,
+                                           void* q, uint32_t* partials, int partials_cap,
+                                           uint32_t* count, void* stream);
+int dpa_delayed_windows_finalize(const DpaDeferredWindow* layers_dev, int count, void* stream);
+
 /* dpa_conv2d_wgrad_fp8 writing fp32 dw holding the bf16-rounded values (what autograd's cast
  * of the reference's bf16 gradient to an fp32 parameter produces), in the same
  * [Cout][R][S][Cin] order: the gradient of a channels-last fp32 master weight directly. */

@@ -159,3 +159,19 @@ def test_weight_prep_plan_on_host(lib):
     assert lib.dpa_conv2d_wgrad_fp8_f32(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1000),
                                         ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1008), ctypes.c_void_p(0x1000),
                                         1 << 30, 2, 8, 8, 128, 128, 3, 3, 1, 1, 0, nul) == -3
+
+
+def test_deferred_window_entries(lib):
+    import ctypes
+    WP = dpa_mod("weight_prep")
+    assert ctypes.sizeof(WP.DpaDeferredWindow) == 64
+    assert lib.dpa_quant_partials_count(0) == 0
+    assert lib.dpa_quant_partials_count(8) == 1
+    assert lib.dpa_quant_partials_count(1 << 30) == 512
+    fake, nul = ctypes.c_void_p(0x1000), None
+    assert lib.dpa_quantize_fp8_delayed_deferred_bf16(nul, 16, fake, fake, fake, 512, fake, nul) == -1
+    assert lib.dpa_quantize_fp8_delayed_deferred_bf16(fake, 0, fake, fake, fake, 512, fake, nul) == -2
+    assert lib.dpa_quantize_fp8_delayed_deferred_bf16(fake, 1 << 30, fake, fake, fake, 100, fake, nul) == -5
+    assert lib.dpa_quantize_fp8_delayed_deferred_bf16(ctypes.c_void_p(0x1008), 16, fake, fake, fake, 512, fake, nul) == -3
+    assert lib.dpa_delayed_windows_finalize(nul, 3, nul) == -1
+    assert lib.dpa_delayed_windows_finalize(fake, 0, nul) == -2

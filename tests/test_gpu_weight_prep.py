@@ -3,8 +3,9 @@ dpa_weight_prep_* / dpa_window_max_grouped_f32 entries): every FP8 layer type wi
 prepared for the step gives the same bytes as the per-call path (the reference's per-layer
 quantization, diffusion/unet.py:69-91 and fp8_kernels.py:822-913): outputs, input gradients,
 fp32 weight gradients (autograd's cast of the bf16 gradient), amax windows and positions, over
-steps that wrap the window; and the prepared e4m3 weights and transposes equal the per-layer
-quantization and weight transpose.
+steps that wrap the window (the prepared path writes a step's x / dy window records at the
+start of the next step, or at flush()); and the prepared e4m3 weights and transposes equal the
+per-layer quantization and weight transpose.
 """
 from __future__ import annotations
 
@@ -76,6 +77,8 @@ def test_prepared_layer_matches_per_call_path(kind):
                     gy = gy.contiguous(memory_format=torch.channels_last)
             y.backward(gy)
             outs.append((y.detach(), xd.grad, _weight(mod).grad.clone()))
+        if plan is not None:
+            plan.flush()                             # the step's deferred window records
         torch.cuda.synchronize()
         if plan is None:
             assert a._fp8_mode is not None, kind     # recorded on the first GPU call
@@ -142,6 +145,8 @@ def test_unet_steps_with_and_without_weight_prep():
         for st in (a, b):
             torch.manual_seed(100 + i)
             st.eager_step()
+        if a.model._wprep is not None:
+            a.model._wprep.flush()                   # the step's deferred window records
         torch.cuda.synchronize()
         la, lb = float(a.loss_acc), float(b.loss_acc)
         assert math.isfinite(la) and la == lb, (i, la, lb)
