@@ -96,21 +96,26 @@ class ConvWorkload:
             "wgrad": n * h * w * cin + n * self.p * self.q * cout + 2 * cout * k * k * cin,
         }
         self.quant_bytes = 3 * (n * h * w * cin + cout * k * k * cin + n * self.p * self.q * cout)
+        self.wprep = None
 
     def quantize(self):
+        """x and dy: quantize_fp8 (amax + cast each). The weight: its e4m3 copy, scale and the
+        data gradient's transposed copy in one grouped weight preparation (two launches, in
+        place of quantize_fp8's two and the transpose)."""
         K = self.K
+        if self.wprep is None:
+            WP = importlib.import_module("diffusion-profiled_amd.weight_prep")
+            self.wprep = WP.TensorPrep([self.wt])
         self.xq, self.xs = K.quantize_fp8(self.x)
-        self.wq, self.ws = K.quantize_fp8(self.wt)
+        self.wprep.run()
+        self.wq, self.wq_t, self.ws = self.wprep.q[0], self.wprep.qt[0], self.wprep.scale(0)
         self.dyq, self.dys = K.quantize_fp8(self.dy)
 
     def fwd(self):
         return self.K.conv2d_fp8_fwd_general(self.xq, self.wq, self.xs, self.ws, self.stride, self.pad)
 
-    def wtrans(self):
-        self.wq_t = self.K.weight_transpose_fp8(self.wq)
-
     def dgrad(self):
-        """The data-gradient GEMM kernel alone (the weight transpose is its own part)."""
+        """The data-gradient GEMM kernel alone (the transposed weight comes from quantize)."""
         return self.K.conv2d_fp8_dgrad_general(self.dyq, self.wq, self.dys, self.ws, (self.h, self.w),
                                                self.stride, self.pad, weight_t=self.wq_t)
 
@@ -121,13 +126,12 @@ class ConvWorkload:
     def step(self):
         self.quantize()
         self.fwd()
-        self.wtrans()
         self.dgrad()
         self.wgrad()
 
     def parts(self):
-        return {"quantize": self.quantize, "fwd": self.fwd, "wtrans": self.wtrans,
-                "dgrad": self.dgrad, "wgrad": self.wgrad}
+        return {"quantize": self.quantize, "fwd": self.fwd, "dgrad": self.dgrad,
+                "wgrad": self.wgrad}
 
     def step_flop(self):
         return 3 * self.flop
@@ -460,8 +464,6 @@ def main():
     if args.part:
         wl = make_workload(K, args.workload)
         wl.quantize()
-        if hasattr(wl, "wtrans"):
-            wl.wtrans()
         fn = wl.parts()[args.part]
         for _ in range(args.reps):
             fn()
@@ -474,8 +476,6 @@ def main():
 
     # per-part device times (HIP events on the launch stream)
     wl.quantize()
-    if hasattr(wl, "wtrans"):
-        wl.wtrans()
     parts = {}
     for name, fn in wl.parts().items():
         parts[name] = time_part(fn, args.kernel_reps)
@@ -511,8 +511,6 @@ def main():
     for k, us in parts.items():
         if k == "quantize":
             kernels[k] = {"us": round(us, 2), "GB/s": round(wl.quant_bytes / (us * 1e-6) / 1e9, 1)}
-        elif k == "wtrans":
-            kernels[k] = {"us": round(us, 2)}
         else:
             kernels[k] = {"us": round(us, 2), "TFLOP/s": round(wl.flop / (us * 1e-6) / 1e12, 1),
                           "frac_fp8_peak": round(wl.flop / (us * 1e-6) / 1e12 / PEAK_FP8_TFLOPS, 4),

@@ -62,8 +62,12 @@ __device__ __forceinline__ bool wp_slot(const DpaWeightEntry& E, const WpTile& T
   return co < E.cout && ci < E.cin;  // cin % 8 == 0: a group of 8 is all in or all out
 }
 
-// 8 fp32 -> 8 bf16 (RNE) packed as one uint4.
-__device__ __forceinline__ uint4 wp_bf16x8(const float* p) {
+// Elements off .. off+7 of the weight as 8 bf16 packed in one uint4: fp32 weights rounded
+// (RNE), bf16 weights (DPA_WP_BF16) as they are.
+__device__ __forceinline__ uint4 wp_bf16x8(const DpaWeightEntry& E, int64_t off) {
+  if (E.flags & DPA_WP_BF16)
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(E.w) + off);
+  const float* p = E.w + off;
   const float4 a = *reinterpret_cast<const float4*>(p);
   const float4 b = *reinterpret_cast<const float4*>(p + 4);
   uint4 o;
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(kWpThreads) void wprep_amax_kernel(
   for (int h = 0; h < 2; ++h) {
     int64_t off;
     int row, c8;
-    if (wp_slot(E, T, h, off, row, c8)) acc = absmax8(acc, wp_bf16x8(E.w + off));
+    if (wp_slot(E, T, h, off, row, c8)) acc = absmax8(acc, wp_bf16x8(E, off));
   }
   const uint32_t m = wp_block_max(acc.x > acc.y ? acc.x : acc.y, red);
   if (threadIdx.x == 0) partials[blockIdx.x] = m;
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     ok[h] = wp_slot(E, T, h, off[h], row[h], c8[h]);
-    if (ok[h]) v[h] = wp_bf16x8(E.w + off[h]);
+    if (ok[h]) v[h] = wp_bf16x8(E, off[h]);
   }
   // this weight's amax from its blocks' partials (every block re-reduces them)
   uint32_t m = 0;

@@ -41,7 +41,7 @@ class DpaWeightEntry(ctypes.Structure):
         ("w", c_void_p), ("q", c_void_p), ("qt", c_void_p), ("scale_used", c_void_p),
         ("cur_scale", c_void_p), ("prev_scale", c_void_p), ("window", c_void_p), ("pos", c_void_p),
         ("window_len", c_int64), ("n", c_int64), ("cout", c_int32), ("taps", c_int32),
-        ("cin", c_int32), ("blk0", c_int32), ("nblk", c_int32), ("reserved", c_int32),
+        ("cin", c_int32), ("blk0", c_int32), ("nblk", c_int32), ("flags", c_int32),
     ]
 
 
@@ -169,3 +169,54 @@ class WeightPrep:
     def from_model(model: torch.nn.Module) -> "WeightPrep | None":
         layers = [m for m in model.modules() if getattr(m, "_fp8_mode", None) is not None]
         return WeightPrep(layers) if layers else None
+
+
+class TensorPrep:
+    """Current-scaling e4m3 copies of fixed weight tensors (fp32 or bf16; 4-D channels-last
+    conv weights or 2-D [N][K]) with their data-gradient transposes and scales, for all of
+    them in two launches: ``quantize_fp8`` of each weight plus ``weight_transpose_fp8``,
+    bit-identical. Buffers are allocated once; run() refreshes them from the weights."""
+
+    def __init__(self, weights: list):
+        assert weights
+        dev = weights[0].device
+        self.weights = weights
+        self.scales = torch.zeros(len(weights), device=dev, dtype=torch.float32)
+        self.q, self.qt = [], []
+        entries = (DpaWeightEntry * len(weights))()
+        for i, w in enumerate(weights):
+            assert w.dtype in (torch.float32, torch.bfloat16) and w.device == dev
+            if w.ndim == 4:
+                cout, cin, kh, kw = w.shape
+                assert w.is_contiguous(memory_format=torch.channels_last)
+                q = torch.empty((cout, cin, kh, kw), device=dev, dtype=FP8_DTYPE,
+                                memory_format=torch.channels_last)
+                qt = torch.empty((cin, kh, kw, cout), device=dev, dtype=FP8_DTYPE)
+                taps = kh * kw
+            else:
+                cout, cin = w.shape
+                assert w.is_contiguous()
+                q = torch.empty((cout, cin), device=dev, dtype=FP8_DTYPE)
+                qt = torch.empty((cin, cout), device=dev, dtype=FP8_DTYPE)
+                taps = 1
+            e = entries[i]
+            e.w, e.q, e.qt = w.data_ptr(), q.data_ptr(), qt.data_ptr()
+            e.scale_used = self.scales[i].data_ptr()
+            e.n, e.cout, e.taps, e.cin = w.numel(), cout, taps, cin
+            e.flags = 1 if w.dtype == torch.bfloat16 else 0       # DPA_WP_BF16
+            self.q.append(q)
+            self.qt.append(qt)
+        blocks = _lib.load().dpa_weight_prep_plan(ctypes.addressof(entries), len(weights))
+        _lib.check(min(blocks, 0), "dpa_weight_prep_plan")
+        self.blocks, self.count = int(blocks), len(weights)
+        self.table = torch.frombuffer(bytearray(bytes(entries)), dtype=torch.uint8).to(dev)
+        self.ws_bytes = _lib.query("dpa_weight_prep_workspace_bytes", self.blocks)
+        self.workspace = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+
+    def scale(self, i: int) -> torch.Tensor:
+        return self.scales[i]
+
+    def run(self) -> None:
+        stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        _lib.call("dpa_weight_prep_run", self.table.data_ptr(), self.count, self.blocks,
+                  self.workspace.data_ptr(), self.ws_bytes, stream)

@@ -244,8 +244,10 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * per-layer path: bf16(w) is the round-to-nearest-even cast, then the same scale and e4m3
  * rule as dpa_quantize_fp8_bf16 (current scaling) or dpa_quantize_fp8_delayed_bf16 (delayed).
  * ---------------------------------------------------------------------------------------- */
+#define DPA_WP_BF16 1          /* DpaWeightEntry.flags: w holds bf16, not fp32 */
 typedef struct DpaWeightEntry {
-  const float* w;           /* fp32 weight, FP8 memory order: [Cout][R][S][Cin] or [N][K] */
+  const float* w;           /* weight (fp32, or bf16 with DPA_WP_BF16), FP8 memory order:
+                               [Cout][R][S][Cin] or [N][K] */
   void* q;                  /* e4m3 out, same order (8-B aligned) */
   void* qt;                 /* e4m3 out [Cin][R][S][Cout] (data-gradient operand) or NULL */
   float* scale_used;        /* the scale q was cast with */
@@ -257,7 +259,7 @@ typedef struct DpaWeightEntry {
   int64_t n;                /* elements = cout * taps * cin (cin % 8 == 0) */
   int32_t cout, taps, cin;  /* taps = R * S (1 for a linear) */
   int32_t blk0, nblk;       /* filled in by dpa_weight_prep_plan */
-  int32_t reserved;
+  int32_t flags;            /* DPA_WP_BF16 or 0 */
 } DpaWeightEntry;
 
 /* Assigns each entry its blocks (host array, in place); returns the total block count (> 0)

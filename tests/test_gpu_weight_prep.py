@@ -159,3 +159,30 @@ def test_unet_steps_with_and_without_weight_prep():
             assert torch.equal(buf, q), (i, name)
     assert a.model._wprep is not None and a.model._wprep.count > 50
     assert b.model._wprep is None
+
+
+def test_tensor_prep_bf16_weights_equal_quantize_and_transpose():
+    """TensorPrep on bf16 weights (cfg2's weight is bf16): q == quantize_fp8(w), the same
+    scale, qt == weight_transpose_fp8(q); 3x3, 1x1 and 2-D weights in one plan, ragged
+    tiles (Cout 192 is three 64-row tiles), two runs after an in-place weight update."""
+    g = torch.Generator().manual_seed(7)
+    ws = [(torch.randn((128, 128, 3, 3), generator=g) * 0.05).to(torch.bfloat16),
+          (torch.randn((192, 256, 1, 1), generator=g) * 3.0).to(torch.bfloat16),
+          (torch.randn((768, 256), generator=g)).to(torch.bfloat16)]
+    ws = [w.cuda().contiguous(memory_format=torch.channels_last) if w.ndim == 4 else w.cuda()
+          for w in ws]
+    tp = WP.TensorPrep(ws)
+    for rnd in range(2):
+        if rnd:
+            for w in ws:
+                w.mul_(1.5)
+        tp.run()
+        torch.cuda.synchronize()
+        for i, w in enumerate(ws):
+            q_ref, s_ref = K.quantize_fp8_tensor(w)
+            assert torch.equal(tp.q[i].view(torch.uint8), q_ref.view(torch.uint8)), (rnd, i)
+            assert float(tp.scale(i)) == float(s_ref), (rnd, i)
+            q4 = tp.q[i] if w.ndim == 4 else tp.q[i][:, :, None, None]
+            qt_ref = K.weight_transpose_fp8(q4)
+            assert torch.equal(tp.qt[i].view(torch.uint8).flatten(),
+                               qt_ref.view(torch.uint8).flatten()), (rnd, i)
