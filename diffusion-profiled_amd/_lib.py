@@ -79,6 +79,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p] * 8 + [c_int] * 4 + [c_float, c_void_p],
     ),
+    "dpa_layernorm_fwd_bf16": (
+        c_int,
+        [c_void_p] * 6 + [c_int64, c_int, c_float, c_void_p],
+    ),
+    "dpa_layernorm_bwd_workspace_bytes": (c_int64, [c_int64, c_int]),
+    "dpa_layernorm_bwd_bf16": (
+        c_int,
+        [c_void_p] * 9 + [c_int64, c_int64, c_int, c_void_p],
+    ),
     "dpa_gn_silu_fwd_workspace_bytes": (c_int64, [c_int] * 4),
     "dpa_gn_silu_fwd_ws_bf16": (
         c_int,

@@ -1,0 +1,64 @@
+"""LayerNorm on bf16 token rows with fp32 statistics, as an autograd Function (the HIP
+library's dpa_layernorm_*).
+
+Replaces the attention block's ``self.norm(seq)`` (diffusion/unet.py:182, :186), which
+autocast runs in fp32 on an fp32 copy of the bf16 tokens and whose result the qkv projection
+rounds back to bf16: here the kernel reads the bf16 tokens and writes that bf16 result.
+"""
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _lib
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def supported(c: int) -> bool:
+    return c % 64 == 0 and c // 64 in (1, 2, 4, 8, 16)
+
+
+class LayerNormBF16(torch.autograd.Function):
+    """y = bf16(LayerNorm(x)) over the last axis; x bf16 (rows contiguous), gamma/beta fp32."""
+
+    @staticmethod
+    def forward(ctx: Any, x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float):
+        c = x.shape[-1]
+        xb = x.to(torch.bfloat16).contiguous()
+        rows = xb.numel() // c
+        out = torch.empty_like(xb)
+        mean = torch.empty(rows, device=x.device, dtype=torch.float32)
+        rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+        g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
+        _lib.call("dpa_layernorm_fwd_bf16", xb.data_ptr(), g32.data_ptr(), b32.data_ptr(),
+                  out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, c, float(eps),
+                  _stream(xb))
+        ctx.save_for_backward(xb, g32, mean, rstd)
+        ctx.x_dtype = x.dtype
+        ctx.param_dtypes = (gamma.dtype, beta.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout: torch.Tensor):
+        xb, g32, mean, rstd = ctx.saved_tensors
+        c = xb.shape[-1]
+        rows = xb.numel() // c
+        dout = dout.to(torch.bfloat16).contiguous()
+        dx = torch.empty_like(xb)
+        dgamma = torch.empty(c, device=xb.device, dtype=torch.float32)
+        dbeta = torch.empty(c, device=xb.device, dtype=torch.float32)
+        ws_bytes = _lib.query("dpa_layernorm_bwd_workspace_bytes", rows, c)
+        ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
+        _lib.call("dpa_layernorm_bwd_bf16", xb.data_ptr(), dout.data_ptr(), g32.data_ptr(),
+                  mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(),
+                  dbeta.data_ptr(), ws.data_ptr(), ws_bytes, rows, c, _stream(xb))
+        return (dx.to(ctx.x_dtype), dgamma.to(ctx.param_dtypes[0]),
+                dbeta.to(ctx.param_dtypes[1]), None)
+
+
+def layer_norm_bf16(x: torch.Tensor, norm: torch.nn.LayerNorm) -> torch.Tensor:
+    return LayerNormBF16.apply(x, norm.weight, norm.bias, norm.eps)

@@ -32,6 +32,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import fp8_kernels as K
+from .layer_norm import layer_norm_bf16
+from .layer_norm import supported as ln_supported
 from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
 
@@ -330,7 +332,11 @@ class CHWAttention(nn.Module):
         resid = x
         b, c, h, w = x.shape
         seq = x.permute(0, 2, 3, 1).reshape(b, h * w, c)           # b (h w) c
-        seq = self.norm(seq)
+        if _on_gpu(x) and ln_supported(c):
+            # the bf16 tokens in, the bf16 the qkv projection would round to out (fp32 stats)
+            seq = layer_norm_bf16(seq, self.norm)
+        else:
+            seq = self.norm(seq)
         qkv = self.qkv(seq)
         q, k, v = torch.chunk(qkv, chunks=3, dim=-1)
         hd = c // self.nh

@@ -310,6 +310,24 @@ int dpa_conv2d_wgrad_fp8_f32(const void* xq, const void* dyq, const float* x_sca
                              int64_t workspace_bytes, int N, int H, int W, int Cin, int Cout,
                              int R, int S, int stride, int pad, int split_k, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * LayerNorm over the channel axis of bf16 token rows [rows][C], fp32 statistics (biased
+ * variance), bf16 out: the attention block's nn.LayerNorm (diffusion/unet.py:182, applied at
+ * :186 to the [B, H*W, C] view of the channels-last activation; autocast runs it in fp32 and
+ * the qkv projection rounds its output to bf16, which is what `out` stores).
+ *   out = bf16((x - mean) * rstd * gamma + beta);  mean/rstd [rows] saved for the backward.
+ * Backward: dx (bf16), dgamma/dbeta (fp32, summed over rows in a fixed order).
+ * C % 64 == 0 with C / 64 in {1, 2, 4, 8, 16}.
+ * ---------------------------------------------------------------------------------------- */
+int dpa_layernorm_fwd_bf16(const void* x, const float* gamma, const float* beta, void* out,
+                           float* mean, float* rstd, int64_t rows, int C, float eps,
+                           void* stream);
+int64_t dpa_layernorm_bwd_workspace_bytes(int64_t rows, int C);
+int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                           const float* mean, const float* rstd, void* dx, float* dgamma,
+                           float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
+                           int C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

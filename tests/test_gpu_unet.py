@@ -183,12 +183,17 @@ def test_graph_captured_step_matches_eager_steps():
         la, lb = float(a.loss_acc), float(b.loss_acc)
         assert math.isfinite(la) and la == pytest.approx(lb, rel=1e-5), (i, la, lb)
         for (name, p), q in zip(a.model.named_parameters(), b.model.parameters()):
-            # per tensor, normwise: the attention backward (atomics) and the bf16 input/output
-            # convs (MIOpen) are not bit-reproducible, and AdamW turns gradient noise into
-            # relative differences of single small-gradient elements
-            assert nerr(p, q) < 1e-4, (i, name, nerr(p, q))
+            # per tensor, normwise, with an absolute floor of 1e-5 per element (5 % of one
+            # AdamW step at lr 2e-4): the bf16 input/output convs (MIOpen) are not
+            # bit-reproducible, and AdamW turns that gradient noise into relative differences
+            # of small-gradient elements, all of them in the zero-initialised projections
+            d = float((p.detach() - q.detach()).float().norm())
+            bound = 1e-4 * float(q.detach().float().norm()) + 1e-5 * math.sqrt(q.numel())
+            assert d <= bound, (i, name, d, bound)
     for (name, p), q in zip(a.ema_ddpm.model.model.named_parameters(), b.ema_ddpm.model.model.parameters()):
-        assert nerr(p, q) < 1e-4, ("ema", name, nerr(p, q))
+        d = float((p.detach() - q.detach()).float().norm())
+        bound = 1e-4 * float(q.detach().float().norm()) + 1e-5 * math.sqrt(q.numel())
+        assert d <= bound, ("ema", name, d, bound)
     for (name, buf), q in zip(a.model.named_buffers(), b.model.buffers()):
         if buf.dtype == torch.long:                  # window positions: exact
             assert torch.equal(buf, q), name
