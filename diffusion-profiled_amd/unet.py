@@ -33,6 +33,7 @@ import torch.nn.functional as F
 
 from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
+from .residual import residual_join
 from .layer_norm import supported as ln_supported
 from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
@@ -260,7 +261,7 @@ class ResidualBlock(nn.Module):
             w, b = torch.chunk(wb, chunks=2, dim=1)
             h = norm_silu(self.norm2, x, self.fused, w + 1, b)
         x = self.conv_2(self.dropout(h))
-        return (self.skip_connection(resid) + x) / math.sqrt(2.0)
+        return residual_join(self.skip_connection(resid), x)
 
 
 class _Attention(torch.autograd.Function):
@@ -358,8 +359,7 @@ class CHWAttention(nn.Module):
             o = _Attention.apply(heads(q).to(dt), heads(k).to(dt), heads(v).to(dt))
             o = o.reshape(b, self.nh, h * w, hd).transpose(1, 2).reshape(b, h * w, c)
         o = self.out(o)
-        out = o.reshape(b, h, w, c).permute(0, 3, 1, 2) + resid
-        return out / math.sqrt(2.0)
+        return residual_join(o.reshape(b, h, w, c).permute(0, 3, 1, 2), resid)
 
 
 class Stage(nn.Module):

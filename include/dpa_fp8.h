@@ -328,6 +328,13 @@ int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
                            float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
                            int C, void* stream);
 
+/* Residual join y = (a + b) / sqrt(2) of bf16 tensors in one pass (diffusion/unet.py:161 and
+ * :203, under autocast), with torch's roundings: bf16(bf16(a + b) * inv), inv = RN32(1/sqrt 2)
+ * passed by the caller. b == NULL gives y = bf16(a * inv) (the backward). n % 8 == 0,
+ * pointers 16-B aligned, same memory order for a, b and y. */
+int dpa_residual_scale_bf16(const void* a, const void* b, void* y, int64_t n, float inv,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

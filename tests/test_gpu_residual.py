@@ -1,0 +1,35 @@
+"""The fused residual join (a + b) / sqrt(2) (residual.residual_join, dpa_residual_scale_bf16)
+equals torch's bf16 expression of diffusion/unet.py:161 / :203 bit for bit, forward and
+backward, on channels-last and contiguous tensors."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from conftest import dpa_mod
+
+pytestmark = pytest.mark.gpu
+
+R = dpa_mod("residual")
+
+
+@pytest.mark.parametrize("shape,cl", [((4, 128, 32, 32), True), ((3, 256, 8, 8), True),
+                                      ((128, 512), False), ((2, 256, 4, 4), True)])
+def test_residual_join_bit_exact(shape, cl):
+    g = torch.Generator().manual_seed(sum(shape))
+    a = (torch.randn(shape, generator=g) * 3).to(torch.bfloat16).cuda()
+    b = (torch.randn(shape, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    gy = (torch.randn(shape, generator=g) * 1e-2).to(torch.bfloat16).cuda()
+    if cl:
+        a, b, gy = (t.contiguous(memory_format=torch.channels_last) for t in (a, b, gy))
+    a1, b1 = a.clone().requires_grad_(), b.clone().requires_grad_()
+    a2, b2 = a.clone().requires_grad_(), b.clone().requires_grad_()
+    y1 = R.residual_join(a1, b1)
+    y2 = (a2 + b2) / math.sqrt(2.0)
+    y1.backward(gy)
+    y2.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(a1.grad, a2.grad) and torch.equal(b1.grad, b2.grad)
