@@ -633,6 +633,7 @@ struct GnBwdSetup {
   float mu[2], rs[2], gm[8], bt[8], fsc[8], fsh[8];
 };
 
+template <bool kFilm>
 __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnBwdSetup& st) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -645,14 +646,25 @@ __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnB
     st.gm[e] = p.gamma[ch + e];
     st.bt[e] = p.beta[ch + e];
   }
-  load_film(p, n, ch, st.fsc, st.fsh);
+  if (kFilm) {
+    load_film(p, n, ch, st.fsc, st.fsh);
+  } else {  // compile-time identity: the FiLM terms fold away
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      st.fsc[e] = 1.0f;
+      st.fsh[e] = 0.0f;
+    }
+  }
 }
 
 // Backward, launch 1: grid (C / 64, N, chunks). cp[chunk][n][c] = chunk sums of
-// (gz, gz * xhat, g * z, g) of channel c.
+// (gz, gz * xhat, g * z, g) of channel c; without FiLM only the first two (the others are the
+// FiLM gradients), which halves the sums and the registers they hold.
+template <bool kFilm>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnArgs p,
                                                                       float4* __restrict__ cp) {
-  __shared__ float red[(kChPLN / 8) * 8 * 32];
+  constexpr int NS = kFilm ? 32 : 16;
+  __shared__ float red[(kChPLN / 8) * 8 * NS];
   const int n = blockIdx.y, chunk = blockIdx.z;
   const int c0 = blockIdx.x * kSlab;
   const int gq = threadIdx.x & 7;
@@ -665,10 +677,10 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   int pxs[kChU];
   chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
-  gn_bwd_setup(p, n, ch, st);
-  float acc[32];
+  gn_bwd_setup<kFilm>(p, n, ch, st);
+  float acc[NS];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) acc[k] = 0.f;
+  for (int k = 0; k < NS; ++k) acc[k] = 0.f;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8], d[8], xh[8], z[8], g[8];
@@ -681,22 +693,27 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
         const float gz = g[e] * st.fsc[e];
         acc[e] += gz;
         acc[8 + e] += gz * xh[e];
-        acc[16 + e] += g[e] * z[e];
-        acc[24 + e] += g[e];
+        if (kFilm) {
+          acc[(16 % NS) + e] += g[e] * z[e];
+          acc[(24 % NS) + e] += g[e];
+        }
       }
     }
   }
-  slab_reduce<32, kChPLN>(acc, red);
+  slab_reduce<NS, kChPLN>(acc, red);
   if (pl == 0) {
     float4* o = cp + ((int64_t)chunk * p.N + n) * p.C + ch;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = float4{acc[e], acc[8 + e], acc[16 + e], acc[24 + e]};
+    for (int e = 0; e < 8; ++e)
+      o[e] = kFilm ? float4{acc[e], acc[8 + e], acc[(16 % NS) + e], acc[(24 % NS) + e]}
+                   : float4{acc[e], acc[8 + e], 0.f, 0.f};
   }
 }
 
 // Backward, launch 2: per-channel totals over the chunks in order, group means of
 // gxh = gz * gamma and gxh * xhat, then dx for this chunk. Chunk 0 writes the per-image
 // channel partials of dgamma/dbeta and the FiLM gradients.
+template <bool kFilm>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const GnArgs p,
                                                                        const float4* __restrict__ cp,
                                                                        int nchunk) {
@@ -715,7 +732,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   int pxs[kChU];
   chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
-  gn_bwd_setup(p, n, ch, st);
+  gn_bwd_setup<kFilm>(p, n, ch, st);
 
   // channel totals over the chunks: four interleaved slices of chunks per channel (loads
   // in flight together), then the slices in order (deterministic)
@@ -955,10 +972,17 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
     // chunk sums after the 2*N*C per-image partials (16-B aligned: 8*N*C bytes, C % 64 == 0)
     float4* cp = (float4*)((float*)workspace + (int64_t)2 * N * C);
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
-    gn_chunk_bwd_sums_kernel<<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-    st = launch_status();
-    if (st != DPA_OK) return st;
-    gn_chunk_bwd_apply_kernel<<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    if (a.fs || a.wb) {
+      gn_chunk_bwd_sums_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+      st = launch_status();
+      if (st != DPA_OK) return st;
+      gn_chunk_bwd_apply_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    } else {
+      gn_chunk_bwd_sums_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+      st = launch_status();
+      if (st != DPA_OK) return st;
+      gn_chunk_bwd_apply_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    }
   } else {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
     const int pln = gn_pixel_lanes(HW);
