@@ -658,12 +658,13 @@ __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnB
 }
 
 // Backward, launch 1: grid (C / 64, N, chunks). cp[chunk][n][c] = chunk sums of
-// (gz, gz * xhat, g * z, g) of channel c; without FiLM only the first two (the others are the
-// FiLM gradients), which halves the sums and the registers they hold.
+// (gz, gz * xhat, g * z, g) of channel c. FiLM scale/shift, gamma and beta are constant per
+// (image, channel), so all four follow from S1 = sum g and S2 = sum g * xhat:
+// (fs S1, fs S2, gamma S2 + beta S1, S1); only those two sums are accumulated.
 template <bool kFilm>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnArgs p,
                                                                       float4* __restrict__ cp) {
-  constexpr int NS = kFilm ? 32 : 16;
+  constexpr int NS = 16;
   __shared__ float red[(kChPLN / 8) * 8 * NS];
   const int n = blockIdx.y, chunk = blockIdx.z;
   const int c0 = blockIdx.x * kSlab;
@@ -690,13 +691,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
     if (ok[u]) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float gz = g[e] * st.fsc[e];
-        acc[e] += gz;
-        acc[8 + e] += gz * xh[e];
-        if (kFilm) {
-          acc[(16 % NS) + e] += g[e] * z[e];
-          acc[(24 % NS) + e] += g[e];
-        }
+        acc[e] += g[e];
+        acc[8 + e] += g[e] * xh[e];
       }
     }
   }
@@ -704,9 +700,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   if (pl == 0) {
     float4* o = cp + ((int64_t)chunk * p.N + n) * p.C + ch;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o[e] = kFilm ? float4{acc[e], acc[8 + e], acc[(16 % NS) + e], acc[(24 % NS) + e]}
-                   : float4{acc[e], acc[8 + e], 0.f, 0.f};
+    for (int e = 0; e < 8; ++e) {
+      const float s1 = acc[e], s2 = acc[8 + e];
+      o[e] = kFilm ? float4{st.fsc[e] * s1, st.fsc[e] * s2, st.gm[e] * s2 + st.bt[e] * s1, s1}
+                   : float4{s1, s2, 0.f, 0.f};
+    }
   }
 }
 
