@@ -822,6 +822,205 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   }
 }
 
+// ---- small images (HW <= 128 pixels: the 8x8 and 4x4 levels): one workgroup per (image,
+// slab) holds all of its pixels in registers, so the forward and the backward each read their
+// inputs once (the one-launch form's passes re-read them) ----
+constexpr int kSmallMaxHW = kChunkPx;
+
+template <bool kFilm>
+__global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p) {
+  __shared__ float red[(kChPLN / 8) * 8 * 2];
+  __shared__ float hs[16];
+  const int n = blockIdx.y;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
+  uint4 v[1][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<1>(src, p.C, 0, pl, p.HW, v, ok, pxs);
+  float f[kChU][8];
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) unpack8(v[0][u], f[u]);
+  float sm[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kChU; ++u)
+    if (ok[u]) {
+      sm[0] += (f[u][0] + f[u][1]) + (f[u][2] + f[u][3]);
+      sm[1] += (f[u][4] + f[u][5]) + (f[u][6] + f[u][7]);
+    }
+  slab_reduce<2, kChPLN>(sm, red);
+  if (pl == 0) {
+    hs[2 * gq] = sm[0];
+    hs[2 * gq + 1] = sm[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)(p.HW * p.cpg);
+  const float mu[2] = {group_sum(hs, 2 * gq, p.cpg) * inv_cnt,
+                       group_sum(hs, 2 * gq + 1, p.cpg) * inv_cnt};
+  __syncthreads();
+  float q[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kChU; ++u)
+    if (ok[u]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = f[u][e] - mu[e >> 2];
+        q[e >> 2] += d * d;
+      }
+    }
+  slab_reduce<2, kChPLN>(q, red);
+  if (pl == 0) {
+    hs[2 * gq] = q[0];
+    hs[2 * gq + 1] = q[1];
+  }
+  __syncthreads();
+  float rs[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) rs[h] = 1.0f / sqrtf(group_sum(hs, 2 * gq + h, p.cpg) * inv_cnt + p.eps);
+  if (pl == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int cc = ch + 4 * h;
+      if (cc % p.cpg == 0) {
+        p.mean[n * p.G + cc / p.cpg] = mu[h];
+        p.rstd[n * p.G + cc / p.cpg] = rs[h];
+      }
+    }
+  }
+  float a[8], b[8], fsc[8], fsh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = p.gamma[ch + e];
+    b[e] = p.beta[ch + e];
+  }
+  if (kFilm) {
+    load_film(p, n, ch, fsc, fsh);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      fsc[e] = 1.0f;
+      fsh[e] = 0.0f;
+    }
+  }
+  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float z[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        float t = (f[u][ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
+        if (kFilm) t = fsc[ee] * t + fsh[ee];
+        z[k] = t * sigmoid_hw(t);
+      }
+      o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
+    }
+    if (ok[u]) st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+  }
+}
+
+template <bool kFilm>
+__global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p) {
+  __shared__ float red[(kChPLN / 8) * 8 * 16];
+  __shared__ float hs[2][16];
+  const int n = blockIdx.y;
+  const int c0 = blockIdx.x * kSlab;
+  const int gq = threadIdx.x & 7;
+  const int pl = threadIdx.x >> 3;
+  const int ch = c0 + gq * 8;
+  const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const uint16_t* const src[2] = {p.x + base, p.dout + base};
+  uint4 v[2][kChU];
+  bool ok[kChU];
+  int pxs[kChU];
+  chunk_load<2>(src, p.C, 0, pl, p.HW, v, ok, pxs);
+  GnBwdSetup st;
+  gn_bwd_setup<kFilm>(p, n, ch, st);
+  // per-channel S1 = sum g, S2 = sum g * xhat over the image (every lane gets the totals)
+  float acc[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    float f[8], d[8], xh[8], z[8], g[8];
+    unpack8(v[0][u], f);
+    unpack8(v[1][u], d);
+    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    if (ok[u]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[e] += g[e];
+        acc[8 + e] += g[e] * xh[e];
+      }
+    }
+  }
+  slab_reduce<16, kChPLN>(acc, red);
+  if (pl == 0) {
+    const int64_t nc = (int64_t)p.N * p.C;
+    float h1[2] = {0.f, 0.f}, h2[2] = {0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float s1 = acc[e], s2 = acc[8 + e];
+      const float gz = st.fsc[e] * s1, gzx = st.fsc[e] * s2;  // sums of gz and gz * xhat
+      const int64_t o = (int64_t)n * p.C + ch + e;
+      p.part[o] = gzx;       // dgamma partial
+      p.part[nc + o] = gz;   // dbeta partial
+      if (kFilm) {
+        const float gzs = st.gm[e] * s2 + st.bt[e] * s1;  // sum g * z
+        if (p.dfs) {
+          p.dfs[o] = gzs;
+          p.dfb[o] = s1;
+        } else if (p.dwb) {
+          const int64_t ob = (int64_t)n * 2 * p.C + ch + e;
+          p.dwb[ob] = (uint16_t)f32_to_bf16_bits(gzs);
+          p.dwb[ob + p.C] = (uint16_t)f32_to_bf16_bits(s1);
+        }
+      }
+      h1[e >> 2] += gz * st.gm[e];
+      h2[e >> 2] += gzx * st.gm[e];
+    }
+    hs[0][2 * gq] = h1[0];
+    hs[0][2 * gq + 1] = h1[1];
+    hs[1][2 * gq] = h2[0];
+    hs[1][2 * gq + 1] = h2[1];
+  }
+  __syncthreads();
+  const float inv_cnt = 1.0f / (float)(p.HW * p.cpg);
+  float m1[2], m2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    m1[h] = group_sum(hs[0], 2 * gq + h, p.cpg) * inv_cnt;
+    m2[h] = group_sum(hs[1], 2 * gq + h, p.cpg) * inv_cnt;
+  }
+#pragma unroll
+  for (int u = 0; u < kChU; ++u) {
+    float f[8], d[8], xh[8], z[8], g[8];
+    unpack8(v[0][u], f);
+    unpack8(v[1][u], d);
+    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float r2[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int ee = e + k;
+        const int h = ee >> 2;
+        const float gxh = g[ee] * st.fsc[ee] * st.gm[ee];
+        r2[k] = st.rs[h] * (gxh - m1[h] - xh[ee] * m2[h]);
+      }
+      o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
+    }
+    if (ok[u]) st_nt16(p.out + base + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+  }
+}
+
 static int gn_chunks(int HW) {
   const int k = (int)ceil_div(HW, kChunkPx);
   return HW >= kChunkMinHW && k <= kMaxChunks ? k : 0;
@@ -876,6 +1075,13 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
     return launch_status();
   }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+  if (HW <= kSmallMaxHW) {
+    if (a.fs || a.wb)
+      gn_small_fwd_kernel<true><<<grid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a);
+    else
+      gn_small_fwd_kernel<false><<<grid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a);
+    return launch_status();
+  }
   const int pln = gn_pixel_lanes(HW);
   if (pln == 128)
     gn_silu_fwd_kernel<128><<<grid, 8 * 128, 0, (hipStream_t)stream>>>(a);
@@ -981,6 +1187,12 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
       if (st != DPA_OK) return st;
       gn_chunk_bwd_apply_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
     }
+  } else if (HW <= kSmallMaxHW) {
+    dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+    if (a.fs || a.wb)
+      gn_small_bwd_kernel<true><<<grid, 8 * kChPLN, 0, s>>>(a);
+    else
+      gn_small_bwd_kernel<false><<<grid, 8 * kChPLN, 0, s>>>(a);
   } else {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
     const int pln = gn_pixel_lanes(HW);
