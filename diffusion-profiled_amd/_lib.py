@@ -89,6 +89,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 9 + [c_int64, c_int64, c_int, c_void_p],
     ),
     "dpa_residual_scale_bf16": (c_int, [c_void_p] * 3 + [c_int64, c_float, c_void_p]),
+    "dpa_adamw_ema_workspace_bytes": (c_int64, [c_void_p, c_int]),
+    "dpa_adamw_ema_step": (
+        c_int,
+        [c_void_p, c_int, c_void_p] + [c_float] * 7 + [c_void_p, c_int64, c_void_p],
+    ),
     "dpa_gn_silu_fwd_workspace_bytes": (c_int64, [c_int] * 4),
     "dpa_gn_silu_fwd_ws_bf16": (
         c_int,

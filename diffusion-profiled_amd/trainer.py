@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from .ddpm import DiffusionWrapper, EWMAWrapper
+from .optim import FusedAdamWEMA
 from .unet import UNet, UNetConfig
 
 
@@ -28,9 +29,12 @@ def _one_step(ddpm: DiffusionWrapper, model: torch.nn.Module, ema_ddpm: Diffusio
     if loss_acc is not None:
         loss_acc.add_(loss.detach())
     loss.backward()
-    torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=max_norm)
-    optimizer.step()
-    ema_ddpm.model.update(ddpm.model)
+    if getattr(optimizer, "fuses_clip_and_ema", False):
+        optimizer.step()       # clip_grad_norm_ + AdamW + EMA in one pass (optim.FusedAdamWEMA)
+    else:
+        torch.nn.utils.clip_grad_norm_(model.parameters(), max_norm=max_norm)
+        optimizer.step()
+        ema_ddpm.model.update(ddpm.model)
     return loss
 
 
@@ -65,7 +69,7 @@ class TrainState:
 
     def __init__(self, config: UNetConfig, batch: int, lr: float = 2e-4, max_t: int = 1000,
                  schedule_type: str = "linear", ema_beta: float = 0.9999, device: str = "cuda",
-                 seed: int = 0, fixed_noise: bool = False):
+                 seed: int = 0, fixed_noise: bool = False, fused_tail: bool = True):
         torch.manual_seed(seed)
         model = UNet(config).to(memory_format=torch.channels_last)
         self.model = model.to(device)
@@ -77,7 +81,12 @@ class TrainState:
                                          schedule_type=schedule_type, max_t=max_t,
                                          in_dim=config.in_resolution, device=device)
         # after the EMA copy: only the trained model prepares its FP8 weights per step
-        self.model.weight_prep_enabled = device == "cuda" or str(device).startswith("cuda")
+        on_gpu = device == "cuda" or str(device).startswith("cuda")
+        self.model.weight_prep_enabled = on_gpu
+        if on_gpu and fused_tail:
+            # clip_grad_norm_(1.0) + AdamW (torch defaults) + EMA(ema_beta) in one fused pass
+            self.optimizer = FusedAdamWEMA(self.model, self.ema_ddpm.model.model, lr=lr,
+                                           max_norm=1.0, ema_beta=ema_beta)
         shape = (batch, config.in_channels, config.in_resolution, config.in_resolution)
         self.static_batch = torch.empty(shape, device=device).contiguous(
             memory_format=torch.channels_last)

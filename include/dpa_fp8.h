@@ -335,6 +335,31 @@ int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
 int dpa_residual_scale_bf16(const void* a, const void* b, void* y, int64_t n, float inv,
                             void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Optimizer tail of the training step (diffusion/train.py:104-149): clip_grad_norm_(max_norm),
+ * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,
+ * ddpm.py EWMAWrapper.update) in one gradient-norm pass and one update pass over all
+ * tensors. Entries with a grad get the clipped AdamW update and then, if ema is set,
+ * ema = RN(beta ema) + RN((1 - beta) p); entries without a grad (float buffers) only the EMA.
+ * The global norm is sqrt(sum of fixed-range block sums, in order): deterministic. *step is
+ * the device step count (incremented here, as the capturable optimizer's). All pointers
+ * fp32, 16-B aligned; the tensors array is host memory (pointers go in kernel arguments).
+ * No counterpart entry in the reference (three library calls there).
+ * ---------------------------------------------------------------------------------------- */
+typedef struct DpaOptTensor {
+  float* param;
+  const float* grad;   /* NULL: EMA-only entry */
+  float* exp_avg;
+  float* exp_avg_sq;
+  float* ema;          /* NULL: no EMA copy */
+  int64_t n;
+} DpaOptTensor;
+
+int64_t dpa_adamw_ema_workspace_bytes(const DpaOptTensor* tensors, int count);
+int dpa_adamw_ema_step(const DpaOptTensor* tensors, int count, float* step, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, float max_norm,
+                       float ema_beta, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
