@@ -871,16 +871,29 @@ def _linear_dgrad_wt(dy: torch.Tensor, wq: torch.Tensor, wq_t: torch.Tensor, dy_
 
 
 class LinearFP8Prepared(torch.autograd.Function):
-    """LinearFP8Function with the weight prepared for the step."""
+    """LinearFP8Function with the weight prepared for the step. ``x_cache`` (a dict owned by the
+    step's weight preparation, emptied at the start of every forward) shares the e4m3 copy of an
+    input among the layers that read the same tensor in one forward (the 22 time-embedding
+    projections all read t_emb): the same bytes and scale as quantizing it per layer."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
-                wq: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor):
+                wq: torch.Tensor, wq_t: torch.Tensor, w_scale: torch.Tensor,
+                x_cache: dict | None = None):
         lead = x.shape[:-1]
         n, k = weight.shape
-        x2 = x.to(torch.bfloat16).reshape(-1, k).contiguous()
-        xq, xs = quantize_fp8_tensor(x2)
+        key = None
+        if x_cache is not None:
+            key = (x.data_ptr(), x._version, tuple(x.shape), tuple(x.stride()), x.dtype)
+        hit = x_cache.get(key) if key is not None else None
+        if hit is not None:
+            xq, xs = hit[1], hit[2]
+        else:
+            x2 = x.to(torch.bfloat16).reshape(-1, k).contiguous()
+            xq, xs = quantize_fp8_tensor(x2)
+            if key is not None:
+                x_cache[key] = (x, xq, xs)      # x kept alive: its address is not reused
         b32 = None if bias is None else bias.detach().float().contiguous()
         y = linear_fp8_prequantized(xq, wq, xs, w_scale, b32)
         ctx.save_for_backward(xq, wq, wq_t, xs, w_scale)
@@ -902,7 +915,7 @@ class LinearFP8Prepared(torch.autograd.Function):
             dw = linear_fp8_wgrad_prequantized(xq, dyq, xs, dys, out_f32=True)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = dy2.float().sum(0)
-        return dx, dw, db, None, None, None
+        return dx, dw, db, None, None, None, None
 
 
 def linear_fp8_autograd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:

@@ -196,7 +196,8 @@ class LinearFP8(_PreparedFP8Weight, nn.Linear):
         if self.fp8 and _on_gpu(x) and K.linear_fp8_supported(self.in_features, self.out_features):
             pw = self._prepared("linear")
             if pw is not None:
-                return K.LinearFP8Prepared.apply(x, self.weight, self.bias, pw.q, pw.qt, pw.scale)
+                return K.LinearFP8Prepared.apply(x, self.weight, self.bias, pw.q, pw.qt, pw.scale,
+                                                 self._fp8_plan.x_cache)
             self._note_fp8_mode("linear", self.weight)
             return K.LinearFP8Function.apply(x, self.weight, self.bias)
         return super().forward(x)
@@ -488,6 +489,7 @@ class UNet(nn.Module):
         finally:
             if plan is not None:
                 plan.active = False
+                plan.x_cache.clear()
 
     def _forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
         t_emb = self.time_embed(self._timestep(t))

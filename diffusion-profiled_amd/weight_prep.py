@@ -129,6 +129,7 @@ class WeightPrep:
             m._fp8_plan = self
             self._keep += [q, qt]
         self.active = False
+        self.x_cache: dict = {}     # e4m3 copies of layer inputs shared within one forward
         blocks = _lib.load().dpa_weight_prep_plan(ctypes.addressof(entries), len(layers))
         _lib.check(min(blocks, 0), "dpa_weight_prep_plan")
         self.blocks = int(blocks)
@@ -153,6 +154,7 @@ class WeightPrep:
         """The step's weights: the previous step's pending window records, the window maxima
         (delayed layers), then amax + cast of every weight."""
         stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        self.x_cache.clear()
         self.flush()
         if self.windows is not None:
             _lib.call("dpa_window_max_grouped_f32", self.windows.data_ptr(), 3 * self.n_delayed,
