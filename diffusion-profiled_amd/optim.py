@@ -72,7 +72,12 @@ class FusedAdamWEMA:
         for p, m, v, e in zip(self.params, self.exp_avg, self.exp_avg_sq, self.ema_params):
             g = p.grad
             if g is not None:
-                assert g.dtype == torch.float32 and g.stride() == p.stride()
+                assert g.dtype == torch.float32, "fp32 gradients"
+                if g.stride() != p.stride():
+                    # the kernels walk gradient and parameter as one flat range each: give the
+                    # gradient the parameter's layout (torch's AdamW accepts any strides)
+                    g = torch.empty_like(p).copy_(g)
+                    p.grad = g
                 entries.append((p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
                                 None if e is None else e.data_ptr(), p.numel()))
             elif e is not None:

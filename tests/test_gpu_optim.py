@@ -1,7 +1,8 @@
 """GPU tests of the fused optimizer tail (optim.FusedAdamWEMA, dpa_adamw_ema_step) against
 torch's clip_grad_norm_ + AdamW(fused) + the EWMAWrapper foreach EMA of the reference step
 (diffusion/train.py:104-149, :253, :256): parameters, moments, EMA copies and the float/int
-buffers over several steps, including clipping and an unused parameter (grad None)."""
+buffers over several steps, including clipping, an unused parameter (grad None) and, on odd
+steps, a conv weight gradient in NCHW layout beside its channels-last parameter."""
 from __future__ import annotations
 
 import copy
@@ -43,8 +44,11 @@ def test_fused_tail_matches_torch(max_norm):
                 p.grad, q.grad = None, None
                 continue
             gr = torch.randn(p.shape, generator=g, device="cuda") * (3.0 if step == 1 else 0.05)
-            p.grad = gr.clone().contiguous(memory_format=torch.channels_last) if gr.ndim == 4 else gr.clone()
-            q.grad = p.grad.clone()
+            cl = gr.ndim == 4 and step % 2 == 0
+            p.grad = gr.clone().contiguous(memory_format=torch.channels_last) if cl else gr.clone()
+            # torch's fused AdamW needs the parameter's layout; the fused tail takes either
+            q.grad = gr.clone().contiguous(memory_format=torch.channels_last) if gr.ndim == 4 \
+                else gr.clone()
         with torch.no_grad():
             net.win.mul_(1.1)
             ref.win.mul_(1.1)
