@@ -1,7 +1,7 @@
 // Fused optimizer tail of the training step: gradient-norm clipping, AdamW and the EMA update
 // of every parameter in one norm pass and one update pass.
 //
-// Reference (diffusion/train.py:104-149 step order, :253 optimizer, :256 EMA):
+// Reference (train.py:104-149 step order, :253 optimizer, :256 EMA):
 //   torch.nn.utils.clip_grad_norm_(params, max_norm)      total = ||(||g_t||)_t||, g *= coef
 //   torch.optim.AdamW(fused=True, capturable=True).step() (betas, eps, weight_decay)
 //   EWMAWrapper.update: ema = beta * ema + (1 - beta) * p  (float parameters and buffers)

@@ -1,11 +1,11 @@
 """The training step's optimizer tail as one fused pass (the HIP library's dpa_adamw_ema_step).
 
-The reference step (diffusion/train.py:104-149) ends with
-``clip_grad_norm_(params, max_norm)``, ``AdamW(fused=True, capturable=True).step()`` (:253)
-and the EMA update of ``EWMAWrapper`` (:256, ddpm.py). ``FusedAdamWEMA`` does all three: a
-gradient-norm pass, a one-block finalize (clip coefficient, step count, bias corrections) and
-one update pass that applies the clipped AdamW update and the EMA of every parameter and float
-buffer; integer buffers of the EMA copy are copied as ``EWMAWrapper.update`` does.
+The reference step (train.py:104-149) ends with ``clip_grad_norm_(params, max_norm)``,
+``AdamW(fused=True, capturable=True).step()`` (train.py:253) and the EMA update of
+``EWMAWrapper`` (diffusion/ddpm.py:10-30). ``FusedAdamWEMA`` does all three: a gradient-norm
+pass, a one-block finalize (clip coefficient, step count, bias corrections) and one update
+pass that applies the clipped AdamW update and the EMA of every parameter and float buffer;
+integer buffers of the EMA copy are copied as ``EWMAWrapper.update`` does.
 """
 from __future__ import annotations
 

@@ -336,7 +336,7 @@ int dpa_residual_scale_bf16(const void* a, const void* b, void* y, int64_t n, fl
                             void* stream);
 
 /* ------------------------------------------------------------------------------------------
- * Optimizer tail of the training step (diffusion/train.py:104-149): clip_grad_norm_(max_norm),
+ * Optimizer tail of the training step (train.py:104-149): clip_grad_norm_(max_norm),
  * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,
  * ddpm.py EWMAWrapper.update) in one gradient-norm pass and one update pass over all
  * tensors. Entries with a grad get the clipped AdamW update and then, if ema is set,

@@ -1,6 +1,6 @@
 """GPU tests of the fused optimizer tail (optim.FusedAdamWEMA, dpa_adamw_ema_step) against
 torch's clip_grad_norm_ + AdamW(fused) + the EWMAWrapper foreach EMA of the reference step
-(diffusion/train.py:104-149, :253, :256): parameters, moments, EMA copies and the float/int
+(train.py:104-149, :253, :256): parameters, moments, EMA copies and the float/int
 buffers over several steps, including clipping, an unused parameter (grad None) and, on odd
 steps, a conv weight gradient in NCHW layout beside its channels-last parameter."""
 from __future__ import annotations
