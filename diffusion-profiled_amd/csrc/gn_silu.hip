@@ -31,13 +31,13 @@ constexpr int kGnUnrollFwd = 4;  // pixels per lane per loop iteration (loads in
 constexpr int kGnUnrollBwd = 2;  // (two sources per pixel)
 
 struct GnArgs {
-  const uint16_t* x;
+  const void* x;  // [N][HW][C] bf16, or fp32 for the chunked and small-image forms
   const uint16_t* dout;
   const float* gamma;
   const float* beta;
   const float* fs;  // film scale [N][C] or null
   const float* fb;  // film shift [N][C]
-  uint16_t* out;
+  void* out;  // forward: bf16 output; backward: dx in x's type
   float* mean;
   float* rstd;
   float* part;  // bwd: [2][N][C] per-image channel sums of dgamma / dbeta
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int HW = p.HW;
-  const uint16_t* xb = p.x + (int64_t)n * HW * p.C + ch;
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)n * HW * p.C + ch;
 
   // pass 1: mean
   float s[2] = {0.f, 0.f};
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_fwd_kernel(const GnArgs p) {
   }
   float fsc[8], fsh[8];
   const bool film = load_film(p, n, ch, fsc, fsh);
-  uint16_t* ob = p.out + (int64_t)n * HW * p.C + ch;
+  uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * HW * p.C + ch;
   gn_pixels<PLN, 1, kGnUnrollFwd>(xsrc, p.C, pl, HW, [&](int px, bool ok, uint4 xv, uint4) {
     float f[8];
     unpack8(xv, f);
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
-  const uint16_t* const srcs[2] = {p.x + base, p.dout + base};
+  const uint16_t* const srcs[2] = {static_cast<const uint16_t*>(p.x) + base, p.dout + base};
   gn_pixels<PLN, 2, kGnUnrollBwd>(srcs, p.C, pl, HW, [&](int, bool ok, uint4 xv, uint4 dv) {
     float f[8], d[8];
     unpack8(xv, f);
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
       }
       o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
     }
-    if (ok) st_nt16(p.out + base + (int64_t)px * p.C, uint4{o[0], o[1], o[2], o[3]});
+    if (ok) st_nt16(static_cast<uint16_t*>(p.out) + base + (int64_t)px * p.C, uint4{o[0], o[1], o[2], o[3]});
   });
 }
 
@@ -443,9 +443,10 @@ static_assert(8 * kChPLN == 4 * kSlab, "backward apply: four chunk slices of 64 
 // Lane pl's pixels of the chunk starting at px0: px0 + pl + 32 u; pixels past HW load pixel
 // HW - 1 (a valid address) with ok false.
 template <int NL>
-__device__ __forceinline__ void chunk_load(const uint16_t* const (&src)[NL], int C, int px0,
-                                           int pl, int HW, uint4 (&v)[NL][kChU],
-                                           bool (&ok)[kChU], int (&pxs)[kChU]) {
+__device__ __forceinline__ void chunk_load(const uint8_t* const (&src)[NL],
+                                           const int (&stride)[NL], int px0, int pl, int HW,
+                                           uint4 (&v)[NL][kChU], bool (&ok)[kChU],
+                                           int (&pxs)[kChU]) {
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     const int px = px0 + pl + u * kChPLN;
@@ -456,7 +457,65 @@ __device__ __forceinline__ void chunk_load(const uint16_t* const (&src)[NL], int
   for (int u = 0; u < kChU; ++u)
 #pragma unroll
     for (int l = 0; l < NL; ++l)
-      v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * C);
+      v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * stride[l]);
+}
+
+// Sources of the chunk loop: the 8 channels of x at element offset off (one 16-B part in
+// bf16, two in fp32), then, with kDout, the bf16 gradient of the output.
+template <bool kF32, bool kDout>
+struct GnSrc {
+  static constexpr int kX = kF32 ? 2 : 1;
+  static constexpr int kN = kX + (kDout ? 1 : 0);
+  const uint8_t* src[kN];
+  int stride[kN];  // bytes per pixel
+  __device__ __forceinline__ GnSrc(const GnArgs& p, int64_t off) {
+    constexpr int eb = kF32 ? 4 : 2;
+    const uint8_t* xp = static_cast<const uint8_t*>(p.x) + off * eb;
+#pragma unroll
+    for (int k = 0; k < kX; ++k) {
+      src[k] = xp + 16 * k;
+      stride[k] = p.C * eb;
+    }
+    if (kDout) {
+      src[kN - 1] = reinterpret_cast<const uint8_t*>(p.dout + off);
+      stride[kN - 1] = p.C * 2;
+    }
+  }
+};
+
+// x of pixel u from the loaded parts
+template <bool kF32, int NL>
+__device__ __forceinline__ void unpack_x(const uint4 (&v)[NL][kChU], int u, float (&f)[8]) {
+  if constexpr (kF32) {
+    const uint4 a = v[0][u], b = v[1][u];
+    f[0] = __uint_as_float(a.x);
+    f[1] = __uint_as_float(a.y);
+    f[2] = __uint_as_float(a.z);
+    f[3] = __uint_as_float(a.w);
+    f[4] = __uint_as_float(b.x);
+    f[5] = __uint_as_float(b.y);
+    f[6] = __uint_as_float(b.z);
+    f[7] = __uint_as_float(b.w);
+  } else {
+    unpack8(v[0][u], f);
+  }
+}
+
+// dx of 8 channels at element offset off, in x's type; dx(e) gives channel e's value
+template <bool kF32, typename F>
+__device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
+  if constexpr (kF32) {
+    float* d = static_cast<float*>(p.out) + off;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      st_nt16(d + 4 * h, uint4{__float_as_uint(dx(4 * h)), __float_as_uint(dx(4 * h + 1)),
+                               __float_as_uint(dx(4 * h + 2)), __float_as_uint(dx(4 * h + 3))});
+  } else {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(dx(e)) | (f32_to_bf16_bits(dx(e + 1)) << 16);
+    st_nt16(static_cast<uint16_t*>(p.out) + off, uint4{o[0], o[1], o[2], o[3]});
+  }
 }
 
 __device__ __forceinline__ int chunk_pixels(int HW, int chunk) {
@@ -466,6 +525,7 @@ __device__ __forceinline__ int chunk_pixels(int HW, int chunk) {
 
 // Forward, launch 1: grid (C / 64, N, chunks). cs[n][chunk][g] = (chunk mean, chunk sum of
 // squared deviations from it) of group g.
+template <bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_stats_kernel(const GnArgs p,
                                                                    float2* __restrict__ cs,
                                                                    int nchunk) {
@@ -476,14 +536,14 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_stats_kernel(const GnArgs
   const int gq = threadIdx.x & 7;
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
-  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
-  uint4 v[1][kChU];
+  const GnSrc<kF32, false> in(p, (int64_t)n * p.HW * p.C + ch);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<1>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   float f[kChU][8];
 #pragma unroll
-  for (int u = 0; u < kChU; ++u) unpack8(v[0][u], f[u]);
+  for (int u = 0; u < kChU; ++u) unpack_x<kF32>(v, u, f[u]);
 
   float sm[2] = {0.f, 0.f};
 #pragma unroll
@@ -531,6 +591,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_stats_kernel(const GnArgs
 
 // Forward, launch 2: merge the chunk statistics of the slab's groups in chunk order, then
 // normalise, affine, FiLM, SiLU, bf16 for this workgroup's chunk. Chunk 0 writes mean/rstd.
+template <bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs p,
                                                                    const float2* __restrict__ cs,
                                                                    int nchunk) {
@@ -541,11 +602,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   const int gq = threadIdx.x & 7;
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
-  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
-  uint4 v[1][kChU];
+  const GnSrc<kF32, false> in(p, (int64_t)n * p.HW * p.C + ch);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<1>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
 
   // the slab's chunk statistics, all loads in flight at once, then merged from LDS
   const int ngs = kSlab / p.cpg;
@@ -590,11 +651,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   }
   float fsc[8], fsh[8];
   const bool film = load_film(p, n, ch, fsc, fsh);
-  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
+  uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8];
-    unpack8(v[0][u], f);
+    unpack_x<kF32>(v, u, f);
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -661,7 +722,7 @@ __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnB
 // (gz, gz * xhat, g * z, g) of channel c. FiLM scale/shift, gamma and beta are constant per
 // (image, channel), so all four follow from S1 = sum g and S2 = sum g * xhat:
 // (fs S1, fs S2, gamma S2 + beta S1, S1); only those two sums are accumulated.
-template <bool kFilm>
+template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnArgs p,
                                                                       float4* __restrict__ cp) {
   constexpr int NS = 16;
@@ -672,11 +733,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const uint16_t* const src[2] = {p.x + base, p.dout + base};
-  uint4 v[2][kChU];
+  const GnSrc<kF32, true> in(p, base);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
   float acc[NS];
@@ -685,8 +746,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8], d[8], xh[8], z[8], g[8];
-    unpack8(v[0][u], f);
-    unpack8(v[1][u], d);
+    unpack_x<kF32>(v, u, f);
+    unpack8(v[in.kN - 1][u], d);
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     if (ok[u]) {
 #pragma unroll
@@ -711,7 +772,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
 // Backward, launch 2: per-channel totals over the chunks in order, group means of
 // gxh = gz * gamma and gxh * xhat, then dx for this chunk. Chunk 0 writes the per-image
 // channel partials of dgamma/dbeta and the FiLM gradients.
-template <bool kFilm>
+template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const GnArgs p,
                                                                        const float4* __restrict__ cp,
                                                                        int nchunk) {
@@ -724,11 +785,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const uint16_t* const src[2] = {p.x + base, p.dout + base};
-  uint4 v[2][kChU];
+  const GnSrc<kF32, true> in(p, base);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<2>(src, p.C, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
 
@@ -802,23 +863,15 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8], d[8], xh[8], z[8], g[8];
-    unpack8(v[0][u], f);
-    unpack8(v[1][u], d);
+    unpack_x<kF32>(v, u, f);
+    unpack8(v[in.kN - 1][u], d);
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float r2[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int ee = e + k;
-        const int h = ee >> 2;
-        const float gxh = g[ee] * st.fsc[ee] * st.gm[ee];
-        r2[k] = st.rs[h] * (gxh - m1[h] - xh[ee] * m2[h]);
-      }
-      o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
-    }
-    if (ok[u]) st_nt16(p.out + base + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    auto dx = [&](int e) __attribute__((always_inline)) {
+      const int h = e >> 2;
+      const float gxh = g[e] * st.fsc[e] * st.gm[e];
+      return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
+    };
+    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx);
   }
 }
 
@@ -827,7 +880,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
 // inputs once (the one-launch form's passes re-read them) ----
 constexpr int kSmallMaxHW = kChunkPx;
 
-template <bool kFilm>
+template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p) {
   __shared__ float red[(kChPLN / 8) * 8 * 2];
   __shared__ float hs[16];
@@ -836,14 +889,14 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   const int gq = threadIdx.x & 7;
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
-  const uint16_t* const src[1] = {p.x + (int64_t)n * p.HW * p.C + ch};
-  uint4 v[1][kChU];
+  const GnSrc<kF32, false> in(p, (int64_t)n * p.HW * p.C + ch);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<1>(src, p.C, 0, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, 0, pl, p.HW, v, ok, pxs);
   float f[kChU][8];
 #pragma unroll
-  for (int u = 0; u < kChU; ++u) unpack8(v[0][u], f[u]);
+  for (int u = 0; u < kChU; ++u) unpack_x<kF32>(v, u, f[u]);
   float sm[2] = {0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < kChU; ++u)
@@ -905,7 +958,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
       fsh[e] = 0.0f;
     }
   }
-  uint16_t* ob = p.out + (int64_t)n * p.HW * p.C + ch;
+  uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     uint32_t o[4];
@@ -925,7 +978,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   }
 }
 
-template <bool kFilm>
+template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p) {
   __shared__ float red[(kChPLN / 8) * 8 * 16];
   __shared__ float hs[2][16];
@@ -935,11 +988,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const uint16_t* const src[2] = {p.x + base, p.dout + base};
-  uint4 v[2][kChU];
+  const GnSrc<kF32, true> in(p, base);
+  uint4 v[in.kN][kChU];
   bool ok[kChU];
   int pxs[kChU];
-  chunk_load<2>(src, p.C, 0, pl, p.HW, v, ok, pxs);
+  chunk_load(in.src, in.stride, 0, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
   // per-channel S1 = sum g, S2 = sum g * xhat over the image (every lane gets the totals)
@@ -949,8 +1002,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8], d[8], xh[8], z[8], g[8];
-    unpack8(v[0][u], f);
-    unpack8(v[1][u], d);
+    unpack_x<kF32>(v, u, f);
+    unpack8(v[in.kN - 1][u], d);
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     if (ok[u]) {
 #pragma unroll
@@ -1001,23 +1054,15 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8], d[8], xh[8], z[8], g[8];
-    unpack8(v[0][u], f);
-    unpack8(v[1][u], d);
+    unpack_x<kF32>(v, u, f);
+    unpack8(v[in.kN - 1][u], d);
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float r2[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int ee = e + k;
-        const int h = ee >> 2;
-        const float gxh = g[ee] * st.fsc[ee] * st.gm[ee];
-        r2[k] = st.rs[h] * (gxh - m1[h] - xh[ee] * m2[h]);
-      }
-      o[e >> 1] = f32_to_bf16_bits(r2[0]) | (f32_to_bf16_bits(r2[1]) << 16);
-    }
-    if (ok[u]) st_nt16(p.out + base + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    auto dx = [&](int e) __attribute__((always_inline)) {
+      const int h = e >> 2;
+      const float gxh = g[e] * st.fsc[e] * st.gm[e];
+      return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
+    };
+    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx);
   }
 }
 
@@ -1047,39 +1092,54 @@ static int64_t gn_fwd_workspace(int N, int HW, int G) {
 static int gn_fwd(const void* x, const float* gamma, const float* beta, const float* film_scale,
                   const float* film_shift, const void* film_wb, void* out, float* mean,
                   float* rstd, int N, int HW, int C, int G, float eps, void* stream,
-                  void* workspace = nullptr, int64_t workspace_bytes = 0) {
+                  void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(out, 16) || !aligned(film_wb, 2)) return DPA_ERR_ALIGN;
   GnArgs a{};
-  a.x = (const uint16_t*)x;
+  a.x = x;
   a.gamma = gamma;
   a.beta = beta;
   a.fs = film_scale;
   a.fb = film_shift;
   a.wb = (const uint16_t*)film_wb;
-  a.out = (uint16_t*)out;
+  a.out = out;
   a.mean = mean;
   a.rstd = rstd;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = eps;
   const int nchunk = gn_chunks(HW);
-  if (nchunk > 0 && workspace && workspace_bytes >= gn_fwd_workspace(N, HW, G) &&
-      aligned(workspace, 8)) {
+  const bool chunked = nchunk > 0 && workspace && workspace_bytes >= gn_fwd_workspace(N, HW, G) &&
+                       aligned(workspace, 8);
+  // fp32 x: the chunked form (workspace) or the small-image form
+  if (x_f32 && !chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  if (chunked) {
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
     float2* cs = (float2*)workspace;
-    gn_chunk_stats_kernel<<<cgrid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a, cs, nchunk);
+    if (x_f32)
+      gn_chunk_stats_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
+    else
+      gn_chunk_stats_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
     int st = launch_status();
     if (st != DPA_OK) return st;
-    gn_chunk_apply_kernel<<<cgrid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a, cs, nchunk);
+    if (x_f32)
+      gn_chunk_apply_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
+    else
+      gn_chunk_apply_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
     return launch_status();
   }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
   if (HW <= kSmallMaxHW) {
-    if (a.fs || a.wb)
-      gn_small_fwd_kernel<true><<<grid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a);
+    const bool film = a.fs || a.wb;
+    if (film && x_f32)
+      gn_small_fwd_kernel<true, true><<<grid, 8 * kChPLN, 0, s>>>(a);
+    else if (film)
+      gn_small_fwd_kernel<true, false><<<grid, 8 * kChPLN, 0, s>>>(a);
+    else if (x_f32)
+      gn_small_fwd_kernel<false, true><<<grid, 8 * kChPLN, 0, s>>>(a);
     else
-      gn_small_fwd_kernel<false><<<grid, 8 * kChPLN, 0, (hipStream_t)stream>>>(a);
+      gn_small_fwd_kernel<false, false><<<grid, 8 * kChPLN, 0, s>>>(a);
     return launch_status();
   }
   const int pln = gn_pixel_lanes(HW);
@@ -1127,6 +1187,22 @@ extern "C" int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const 
                 eps, stream, workspace, workspace_bytes);
 }
 
+extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma,
+                                  const float* beta, const float* film_scale,
+                                  const float* film_shift, const void* film_wb, void* out,
+                                  float* mean, float* rstd, void* workspace,
+                                  int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
+                                  void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
+    return DPA_ERR_WORKSPACE;
+  if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
+                eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32);
+}
+
 // per-image channel partials of dgamma/dbeta, then (chunked form) the chunk sums
 static int64_t gn_bwd_workspace(int N, int HW, int C) {
   return (int64_t)2 * N * C * 4 + (int64_t)gn_chunks(HW) * N * C * (int64_t)sizeof(float4);
@@ -1142,7 +1218,8 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
                   const float* film_scale, const float* film_shift, const void* film_wb,
                   const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
-                  int64_t workspace_bytes, int N, int HW, int C, int G, void* stream) {
+                  int64_t workspace_bytes, int N, int HW, int C, int G, void* stream,
+                  bool x_f32 = false) {
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1154,14 +1231,14 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
       !aligned(film_wb, 2) || !aligned(dfilm_wb, 2))
     return DPA_ERR_ALIGN;
   GnArgs a{};
-  a.x = (const uint16_t*)x;
+  a.x = x;
   a.dout = (const uint16_t*)dout;
   a.gamma = gamma;
   a.beta = beta;
   a.fs = film_scale;
   a.fb = film_shift;
   a.wb = (const uint16_t*)film_wb;
-  a.out = (uint16_t*)dx;
+  a.out = dx;
   a.mean = const_cast<float*>(mean);
   a.rstd = const_cast<float*>(rstd);
   a.part = (float*)workspace;
@@ -1171,28 +1248,43 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   const int nchunk = gn_chunks(HW);
+  const bool chunked =
+      nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16);
+  if (x_f32 && !chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  const bool film = a.fs || a.wb;
   int st = DPA_OK;
-  if (nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16)) {
+  if (chunked) {
     // chunk sums after the 2*N*C per-image partials (16-B aligned: 8*N*C bytes, C % 64 == 0)
     float4* cp = (float4*)((float*)workspace + (int64_t)2 * N * C);
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
-    if (a.fs || a.wb) {
-      gn_chunk_bwd_sums_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-      st = launch_status();
-      if (st != DPA_OK) return st;
-      gn_chunk_bwd_apply_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
-    } else {
-      gn_chunk_bwd_sums_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-      st = launch_status();
-      if (st != DPA_OK) return st;
-      gn_chunk_bwd_apply_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
-    }
+    if (film && x_f32)
+      gn_chunk_bwd_sums_kernel<true, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    else if (film)
+      gn_chunk_bwd_sums_kernel<true, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    else if (x_f32)
+      gn_chunk_bwd_sums_kernel<false, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    else
+      gn_chunk_bwd_sums_kernel<false, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    st = launch_status();
+    if (st != DPA_OK) return st;
+    if (film && x_f32)
+      gn_chunk_bwd_apply_kernel<true, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    else if (film)
+      gn_chunk_bwd_apply_kernel<true, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    else if (x_f32)
+      gn_chunk_bwd_apply_kernel<false, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    else
+      gn_chunk_bwd_apply_kernel<false, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
   } else if (HW <= kSmallMaxHW) {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-    if (a.fs || a.wb)
-      gn_small_bwd_kernel<true><<<grid, 8 * kChPLN, 0, s>>>(a);
+    if (film && x_f32)
+      gn_small_bwd_kernel<true, true><<<grid, 8 * kChPLN, 0, s>>>(a);
+    else if (film)
+      gn_small_bwd_kernel<true, false><<<grid, 8 * kChPLN, 0, s>>>(a);
+    else if (x_f32)
+      gn_small_bwd_kernel<false, true><<<grid, 8 * kChPLN, 0, s>>>(a);
     else
-      gn_small_bwd_kernel<false><<<grid, 8 * kChPLN, 0, s>>>(a);
+      gn_small_bwd_kernel<false, false><<<grid, 8 * kChPLN, 0, s>>>(a);
   } else {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
     const int pln = gn_pixel_lanes(HW);
@@ -1231,4 +1323,18 @@ extern "C" int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const 
   if (!film_wb || !dfilm_wb) return DPA_ERR_NULL;
   return gn_bwd(x, dout, gamma, beta, nullptr, nullptr, film_wb, mean, rstd, dx, dgamma, dbeta,
                 nullptr, nullptr, dfilm_wb, workspace, workspace_bytes, N, HW, C, G, stream);
+}
+
+extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
+                                  const float* beta, const float* film_scale,
+                                  const float* film_shift, const void* film_wb, const float* mean,
+                                  const float* rstd, void* dx, float* dgamma, float* dbeta,
+                                  float* dfilm_scale, float* dfilm_shift, void* dfilm_wb,
+                                  void* workspace, int64_t workspace_bytes, int N, int HW, int C,
+                                  int G, void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dx, dgamma,
+                dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
+                stream, x_dtype == DPA_DTYPE_F32);
 }

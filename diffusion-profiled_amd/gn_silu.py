@@ -3,7 +3,11 @@
 Replaces the two Inductor-fused chains of the reference ResidualBlock
 (diffusion/unet.py:151 ``F.silu(self.norm1(x))`` and :157-159
 ``F.silu((w + 1) * self.norm2(x) + b)``). The output is bf16, which is exactly what the FP8
-conv consumes after its ``x.to(torch.bfloat16)`` (diffusion/fp8_kernels.py:835).
+conv consumes after its ``x.to(torch.bfloat16)`` (diffusion/fp8_kernels.py:835). An fp32 input
+(the residual stream below the first level and the decoder's concatenations are fp32 under
+autocast, as in the reference) is normalised as it is, as autocast's fp32 GroupNorm does, and
+its gradient is returned in fp32 by the kernels, for images the chunked (256+ pixels) and
+small-image (<= 128 pixels) forms take; other inputs are cast to bf16 first.
 """
 from __future__ import annotations
 
@@ -18,6 +22,22 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+DTYPE_BF16, DTYPE_F32 = 0, 1  # include/dpa_fp8.h DPA_DTYPE_*
+
+
+def f32_input_ok(x: torch.Tensor) -> bool:
+    """fp32 x that the kernels read directly: chunked form (256..8192 pixels) or small (<= 128)."""
+    hw = x.shape[2] * x.shape[3]
+    return x.dtype == torch.float32 and (hw <= 128 or 256 <= hw <= 64 * 128)
+
+
+def _prep_x(x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """x as the kernels read it (channels-last) and its DTYPE_*."""
+    if f32_input_ok(x):
+        return x.contiguous(memory_format=torch.channels_last), DTYPE_F32
+    return x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last), DTYPE_BF16
+
+
 def supported(c: int, groups: int) -> bool:
     """Shapes the fused kernel implements (all GroupNorms of the reference U-Net)."""
     if c % groups != 0 or c % 64 != 0:
@@ -29,8 +49,8 @@ def supported(c: int, groups: int) -> bool:
 def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
     """Returns (out bf16 channels-last, mean [N*G], rstd [N*G])."""
     n, c, h, w = x.shape
-    x = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
-    out = torch.empty_like(x, memory_format=torch.channels_last)
+    x, _ = _prep_x(x)
+    out = torch.empty_like(x, dtype=torch.bfloat16, memory_format=torch.channels_last)
     mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
     rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
     gamma = gamma.float().contiguous()
@@ -44,21 +64,23 @@ def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
 
 
 def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps):
-    """The workspace form of the forward (chunked for images of 256+ pixels)."""
+    """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32."""
     n, c, h, w = x.shape
     ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    dt = DTYPE_F32 if x.dtype == torch.float32 else DTYPE_BF16
     _lib.call(
-        "dpa_gn_silu_fwd_ws_bf16",
-        x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
+        "dpa_gn_silu_fwd_ex",
+        x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
         mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c, groups, float(eps),
         _stream(x),
     )
 
 
 def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None):
-    """Returns (dx bf16, dgamma, dbeta, dfilm_scale [N,C] | None, dfilm_shift | None)."""
+    """Returns (dx in x's dtype (bf16 or fp32), dgamma, dbeta, dfilm_scale [N,C] | None,
+    dfilm_shift | None)."""
     n, c, h, w = x.shape
     x = x.contiguous(memory_format=torch.channels_last)
     dout = dout.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
@@ -74,12 +96,13 @@ def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_
     ws_bytes = _lib.query("dpa_gn_silu_bwd_workspace_bytes", n, h * w, c, groups)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    dt = DTYPE_F32 if x.dtype == torch.float32 else DTYPE_BF16
     _lib.call(
-        "dpa_gn_silu_bwd_bf16",
-        x.data_ptr(), dout.data_ptr(), gamma.float().contiguous().data_ptr(),
-        beta.float().contiguous().data_ptr(), p(fs), p(fb), mean.data_ptr(), rstd.data_ptr(),
-        dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs), p(dfb), ws.data_ptr(),
-        ws_bytes, n, h * w, c, groups, _stream(x),
+        "dpa_gn_silu_bwd_ex",
+        x.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+        beta.float().contiguous().data_ptr(), p(fs), p(fb), None, mean.data_ptr(),
+        rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs), p(dfb), None,
+        ws.data_ptr(), ws_bytes, n, h * w, c, groups, _stream(x),
     )
     return dx, dgamma, dbeta, dfs, dfb
 
@@ -87,12 +110,12 @@ def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_
 class GroupNormSiLU(torch.autograd.Function):
     """silu(GroupNorm(x)) or silu(film_scale * GroupNorm(x) + film_shift), bf16 out.
 
-    x: bf16 [N, C, H, W] (any memory format; used channels-last). gamma/beta: fp32 [C].
+    x: bf16 or fp32 [N, C, H, W] (any memory format; used channels-last). gamma/beta: fp32 [C].
     film_scale/film_shift: [N, C, 1, 1] or None (the reference's ``w + 1`` and ``b``)."""
 
     @staticmethod
     def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_scale=None, film_shift=None):
-        xb = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        xb, _ = _prep_x(x)
         out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps, film_scale, film_shift)
         ctx.groups = groups
         ctx.has_film = film_scale is not None
@@ -121,10 +144,10 @@ class GroupNormSiLUFilm(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb):
         n, c, h, w = x.shape
-        xb = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        xb, _ = _prep_x(x)
         wb = film_wb.contiguous()
         assert wb.dtype == torch.bfloat16 and wb.numel() == n * 2 * c
-        out = torch.empty_like(xb, memory_format=torch.channels_last)
+        out = torch.empty_like(xb, dtype=torch.bfloat16, memory_format=torch.channels_last)
         mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
@@ -146,12 +169,13 @@ class GroupNormSiLUFilm(torch.autograd.Function):
         dwb = torch.empty(ctx.wb_shape, device=xb.device, dtype=torch.bfloat16)
         ws_bytes = _lib.query("dpa_gn_silu_bwd_workspace_bytes", n, h * w, c, ctx.groups)
         ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
+        dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
         _lib.call(
-            "dpa_gn_silu_film_bwd_bf16",
-            xb.data_ptr(), dout.data_ptr(), gamma.float().contiguous().data_ptr(),
-            beta.float().contiguous().data_ptr(), wb.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
-            dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), dwb.data_ptr(), ws.data_ptr(),
-            ws_bytes, n, h * w, c, ctx.groups, _stream(xb),
+            "dpa_gn_silu_bwd_ex",
+            xb.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+            beta.float().contiguous().data_ptr(), None, None, wb.data_ptr(), mean.data_ptr(),
+            rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), None, None,
+            dwb.data_ptr(), ws.data_ptr(), ws_bytes, n, h * w, c, ctx.groups, _stream(xb),
         )
         return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, dwb
 

@@ -235,6 +235,30 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
                               void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N,
                               int HW, int C, int G, void* stream);
 
+/* Element type of x (and dx) for the *_ex GroupNorm entries. */
+#define DPA_DTYPE_BF16 0
+#define DPA_DTYPE_F32 1
+
+/* GroupNorm + FiLM + SiLU forward / backward with x (and dx) in bf16 or fp32, the other
+ * arguments as in dpa_gn_silu_fwd_ws_bf16 / dpa_gn_silu_bwd_bf16 (one FiLM form at a time:
+ * film_scale/film_shift or film_wb). Under autocast the reference normalises an fp32 input
+ * in fp32 (nn.GroupNorm runs in float32, diffusion/unet.py:151, :157) and returns an fp32
+ * input gradient; with DPA_DTYPE_F32 the kernels read the fp32 x as it is and write dx in
+ * fp32 (the output y stays bf16). fp32 x takes the chunked form (images of 256+ pixels, a
+ * workspace of the *_workspace_bytes size) or the small-image form (<= 128 pixels); other
+ * sizes return DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE. */
+int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
+                       const float* film_scale, const float* film_shift, const void* film_wb,
+                       void* out, float* mean, float* rstd, void* workspace,
+                       int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
+                       void* stream);
+int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
+                       const float* beta, const float* film_scale, const float* film_shift,
+                       const void* film_wb, const float* mean, const float* rstd, void* dx,
+                       float* dgamma, float* dbeta, float* dfilm_scale, float* dfilm_shift,
+                       void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N, int HW,
+                       int C, int G, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Grouped FP8 weight preparation. No single counterpart in the reference: it performs, for a
  * model's whole FP8 weight set in three launches per step, what the reference does per layer

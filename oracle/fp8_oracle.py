@@ -221,12 +221,21 @@ def gemm(aq: np.ndarray, bq: np.ndarray, sa, sb, bias: np.ndarray | None = None)
 # ---------------------------------------------------------------------------------------
 # GroupNorm (+FiLM) + SiLU (diffusion/unet.py:132-133, :151, :157-159)
 # ---------------------------------------------------------------------------------------
+def _gn_input_f64(x: np.ndarray) -> np.ndarray:
+    """GroupNorm input as float64: NHWC bf16 bits (uint16) or fp32 values (the fp32 residual
+    stream, which autocast's float32 GroupNorm reads as it is)."""
+    if x.dtype == np.float32:
+        return x.astype(np.float64)
+    return bf16_bits_to_f32(x).astype(np.float64)
+
+
 def gn_silu_fwd(x_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups: int,
                 eps: float = 1e-5, film_scale: np.ndarray | None = None,
                 film_shift: np.ndarray | None = None) -> np.ndarray:
     """bf16( silu( [fs *] GroupNorm(x) [+ fb] ) ) evaluated in float64, then rounded to fp32
-    and bf16. x NHWC bf16 bits; gamma/beta fp32 [C]; film [N, C]. Returns NHWC bf16 bits."""
-    x = torch.from_numpy(bf16_bits_to_f32(x_bits).astype(np.float64)).permute(0, 3, 1, 2)
+    and bf16. x NHWC bf16 bits or fp32 values; gamma/beta fp32 [C]; film [N, C]. Returns NHWC
+    bf16 bits."""
+    x = torch.from_numpy(_gn_input_f64(x_bits)).permute(0, 3, 1, 2)
     z = F.group_norm(x, groups, torch.from_numpy(gamma.astype(np.float64)),
                      torch.from_numpy(beta.astype(np.float64)), eps)
     if film_scale is not None:
@@ -240,9 +249,9 @@ def gn_silu_fwd(x_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups:
 def gn_silu_bwd(x_bits: np.ndarray, dout_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray,
                 groups: int, eps: float = 1e-5, film_scale: np.ndarray | None = None,
                 film_shift: np.ndarray | None = None):
-    """Autograd of gn_silu_fwd in float64. Returns (dx NHWC float64, dgamma, dbeta,
-    dfilm_scale [N,C] | None, dfilm_shift | None)."""
-    x = torch.from_numpy(bf16_bits_to_f32(x_bits).astype(np.float64)).permute(0, 3, 1, 2)
+    """Autograd of gn_silu_fwd in float64 (x as there). Returns (dx NHWC float64, dgamma,
+    dbeta, dfilm_scale [N,C] | None, dfilm_shift | None)."""
+    x = torch.from_numpy(_gn_input_f64(x_bits)).permute(0, 3, 1, 2)
     x.requires_grad_(True)
     g = torch.from_numpy(gamma.astype(np.float64)).requires_grad_(True)
     b = torch.from_numpy(beta.astype(np.float64)).requires_grad_(True)

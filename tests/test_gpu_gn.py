@@ -233,3 +233,95 @@ def test_one_launch_and_chunked_forms_agree(G, n, c, h, w, film):
     assert_bf16_close(nhwc_bits(a[3]), nhwc_bits(b[3]), "dx")
     for k in range(4, len(a)):
         assert rel(a[k].numpy(), b[k].numpy()) < 1e-4, k
+
+
+F32_CASES = [
+    # fp32 inputs (the fp32 residual stream / decoder concatenations): chunked and small forms
+    (2, 128, 32, 32, False),
+    (2, 256, 16, 16, True),
+    (2, 512, 8, 8, False),
+    (3, 256, 4, 4, True),
+    (2, 128, 17, 19, True),  # chunked, ragged last chunk
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,film", F32_CASES, ids=lambda v: str(v))
+def test_gn_silu_fp32_input_vs_oracle(G, n, c, h, w, film):
+    """An fp32 x is normalised as it is (autocast's float32 GroupNorm, diffusion/unet.py:151,
+    :157) and dx comes back in fp32: forward within one bf16 ulp of the float64 oracle on the
+    fp32 values, dx normwise 2e-5 of the oracle's float64 gradient."""
+    seed = n * 1000 + c + h + 7
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((n, c, h, w), generator=g) * 2.0 + 0.5     # fp32, not bf16-representable
+    dout = randn_bf16((n, c, h, w), seed=seed + 1, std=1e-2)
+    gamma, beta, fs, fb = params(c, n, seed + 2, film)
+    fs_d = None if fs is None else fs.cuda()[:, :, None, None]
+    fb_d = None if fb is None else fb.cuda()[:, :, None, None]
+    xd = cl(x)
+    assert G.f32_input_ok(xd)
+    out, mean, rstd = G.gn_silu_fwd(xd, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, fs_d, fb_d)
+    dx, dgamma, dbeta, dfs, dfb = G.gn_silu_bwd(
+        xd, cl(dout), gamma.cuda(), beta.cuda(), mean, rstd, GROUPS, fs_d, fb_d)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and dx.dtype == torch.float32
+    x_nhwc = x.permute(0, 2, 3, 1).contiguous().numpy()
+    npf = None if fs is None else fs.numpy()
+    npb = None if fb is None else fb.numpy()
+    ref = O.gn_silu_fwd(x_nhwc, gamma.numpy(), beta.numpy(), GROUPS, 1e-5, npf, npb)
+    assert_fwd_close(nhwc_bits(out.cpu()), ref, f"fp32 fwd {(n, c, h, w, film)}")
+    # the bf16-rounded input would miss: normalising bf16(x) differs from the oracle here
+    ref_b = O.gn_silu_fwd(nhwc_bits(x.to(torch.bfloat16)), gamma.numpy(), beta.numpy(), GROUPS,
+                          1e-5, npf, npb)
+    assert np.mean(ref_b != ref) > 0.05
+    rdx, rdg, rdb, rdfs, rdfb = O.gn_silu_bwd(x_nhwc, nhwc_bits(dout), gamma.numpy(),
+                                             beta.numpy(), GROUPS, 1e-5, npf, npb)
+    got = dx.permute(0, 2, 3, 1).contiguous().cpu().numpy()
+    assert rel(got, rdx) < 2e-5, rel(got, rdx)
+    assert rel(dgamma.cpu().numpy(), rdg) < 1e-4
+    assert rel(dbeta.cpu().numpy(), rdb) < 1e-4
+    if film:
+        assert rel(dfs.cpu().numpy(), rdfs) < 1e-4
+        assert rel(dfb.cpu().numpy(), rdfb) < 1e-4
+
+
+def test_gn_silu_fp32_autograd_and_fallback(G):
+    """Through the autograd Functions: an fp32 input keeps an fp32 gradient, equal to the
+    direct calls; a size outside the fp32 forms (12 x 12 = 144 pixels) is cast to bf16 first,
+    as before; the time-projection FiLM form takes fp32 x too."""
+    n, c, groups = 2, 256, GROUPS
+    g = torch.Generator().manual_seed(11)
+    gamma, beta = (1.0 + 0.1 * torch.randn(c, generator=g)).cuda(), (0.1 * torch.randn(c, generator=g)).cuda()
+    for h in (16, 12):
+        x = cl(torch.randn((n, c, h, h), generator=g) * 1.5)
+        xr = x.clone().requires_grad_(True)
+        y = G.group_norm_silu(xr, gamma, beta, groups, 1e-5)
+        dout = cl(torch.randn((n, c, h, h), generator=g) * 1e-2).to(torch.bfloat16)
+        y.backward(dout)
+        assert xr.grad.dtype == torch.float32
+        if h == 16:
+            assert G.f32_input_ok(x)
+            out, mean, rstd = G.gn_silu_fwd(x, gamma, beta, groups, 1e-5)
+            dx = G.gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups)[0]
+        else:
+            assert not G.f32_input_ok(x)
+            xb = x.to(torch.bfloat16)
+            out, mean, rstd = G.gn_silu_fwd(xb, gamma, beta, groups, 1e-5)
+            dx = G.gn_silu_bwd(xb, dout, gamma, beta, mean, rstd, groups)[0].float()
+        torch.cuda.synchronize()
+        assert torch.equal(y, out), h
+        assert torch.equal(xr.grad, dx), h
+    # FiLM read from the bf16 time projection, fp32 x: equals the split form on the same x
+    h = 16
+    x = cl(torch.randn((n, c, h, h), generator=g))
+    wb = (torch.randn((n, 2 * c, 1, 1), generator=g) * 0.2).cuda().to(torch.bfloat16)
+    xr = x.clone().requires_grad_(True)
+    y = G.group_norm_silu_film(xr, gamma, beta, groups, 1e-5, wb)
+    w, b = torch.chunk(wb, 2, dim=1)
+    x2 = x.clone().requires_grad_(True)
+    y2 = G.group_norm_silu(x2, gamma, beta, groups, 1e-5, (w + 1).float(), b.float())
+    dout = cl(torch.randn((n, c, h, h), generator=g) * 1e-2).to(torch.bfloat16)
+    y.backward(dout)
+    y2.backward(dout)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert xr.grad.dtype == torch.float32 and torch.equal(xr.grad, x2.grad)
