@@ -1,6 +1,7 @@
 """The U-Net's residual join ``(a + b) / sqrt(2)`` (diffusion/unet.py:161, :203) in one HIP
-pass on bf16 tensors, with torch's roundings (``dpa_residual_scale_bf16``); other dtypes or
-layouts take the torch expression."""
+pass, with torch's roundings: on two bf16 tensors (``dpa_residual_scale_bf16``), or on the fp32
+residual stream with a bf16 branch (``dpa_residual_scale_f32``, fp32 result, and its
+one-pass backward); other dtypes or layouts take the torch expression."""
 from __future__ import annotations
 
 import math
@@ -49,10 +50,38 @@ class ResidualScale(torch.autograd.Function):
         return gs, gs
 
 
+class ResidualScaleF32(torch.autograd.Function):
+    """a fp32, b bf16: (a + b) / sqrt(2) in fp32; gradients g / sqrt(2) in fp32 for a and
+    rounded to bf16 for b."""
+
+    @staticmethod
+    def forward(ctx: Any, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        y = torch.empty_like(a)
+        _lib.call("dpa_residual_scale_f32", a.data_ptr(), b.data_ptr(), y.data_ptr(), a.numel(),
+                  INV_SQRT2, _stream(a))
+        return y
+
+    @staticmethod
+    def backward(ctx: Any, g: torch.Tensor):
+        g = g.contiguous(memory_format=torch.channels_last) if g.ndim == 4 else g.contiguous()
+        if g.dtype != torch.float32:
+            gs = g.float() / math.sqrt(2.0)
+            return gs, gs.to(torch.bfloat16)
+        ga = torch.empty_like(g)
+        gb = torch.empty_like(g, dtype=torch.bfloat16)
+        _lib.call("dpa_residual_scale_bwd_f32", g.data_ptr(), ga.data_ptr(), gb.data_ptr(),
+                  g.numel(), INV_SQRT2, _stream(g))
+        return ga, gb
+
+
 def residual_join(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """(a + b) / sqrt(2)."""
-    if (a.is_cuda and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
-            and a.numel() % 8 == 0 and _same_dense(a, b)
-            and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0):
-        return ResidualScale.apply(a, b)
+    if a.is_cuda and _same_dense(a, b) and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0:
+        if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.numel() % 8 == 0:
+            return ResidualScale.apply(a, b)
+        if a.numel() % 4 == 0:
+            if a.dtype == torch.float32 and b.dtype == torch.bfloat16:
+                return ResidualScaleF32.apply(a, b)
+            if a.dtype == torch.bfloat16 and b.dtype == torch.float32:
+                return ResidualScaleF32.apply(b, a)
     return (a + b) / math.sqrt(2.0)

@@ -359,6 +359,16 @@ int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
 int dpa_residual_scale_bf16(const void* a, const void* b, void* y, int64_t n, float inv,
                             void* stream);
 
+/* The same join on the fp32 residual stream: a fp32, b bf16 (the branch output), y fp32 =
+ * RN32(RN32(a + b) * inv), torch's (a + b) / math.sqrt(2.0) with type promotion
+ * (diffusion/unet.py:161, :203 below the first level, where the skip path is fp32 under
+ * autocast). n % 4 == 0; a, y 16-B and b 8-B aligned. */
+int dpa_residual_scale_f32(const float* a, const void* b, float* y, int64_t n, float inv,
+                           void* stream);
+/* Its backward: ga = g * inv (fp32), gb = bf16(g * inv), one pass over g. */
+int dpa_residual_scale_bwd_f32(const float* g, float* ga, void* gb, int64_t n, float inv,
+                               void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Optimizer tail of the training step (train.py:104-149): clip_grad_norm_(max_norm),
  * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,

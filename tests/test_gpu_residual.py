@@ -33,3 +33,30 @@ def test_residual_join_bit_exact(shape, cl):
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     assert torch.equal(a1.grad, a2.grad) and torch.equal(b1.grad, b2.grad)
+
+
+@pytest.mark.parametrize("shape,cl,swap", [((4, 256, 16, 16), True, False),
+                                           ((3, 256, 8, 8), True, True),
+                                           ((2, 256, 4, 4), True, False),
+                                           ((128, 4, 256), False, True)])
+def test_residual_join_fp32_stream_bit_exact(shape, cl, swap):
+    """fp32 skip path + bf16 branch (the residual stream below the first level): torch's
+    promoted fp32 add and scalar division, and autograd's gradients (fp32 for the fp32
+    operand, rounded to bf16 for the bf16 one), bit for bit, in either operand order."""
+    g = torch.Generator().manual_seed(sum(shape) + 1)
+    a = (torch.randn(shape, generator=g) * 3).cuda()                       # fp32, full mantissa
+    b = (torch.randn(shape, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    gy = (torch.randn(shape, generator=g) * 1e-2).cuda()
+    if cl:
+        a, b, gy = (t.contiguous(memory_format=torch.channels_last) for t in (a, b, gy))
+    a1, b1 = a.clone().requires_grad_(), b.clone().requires_grad_()
+    a2, b2 = a.clone().requires_grad_(), b.clone().requires_grad_()
+    y1 = R.residual_join(b1, a1) if swap else R.residual_join(a1, b1)
+    y2 = (b2 + a2) / math.sqrt(2.0) if swap else (a2 + b2) / math.sqrt(2.0)
+    assert y1.dtype == torch.float32
+    y1.backward(gy)
+    y2.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert a1.grad.dtype == torch.float32 and b1.grad.dtype == torch.bfloat16
+    assert torch.equal(a1.grad, a2.grad) and torch.equal(b1.grad, b2.grad)
