@@ -4,7 +4,8 @@
 // divides a tensor by a CPU scalar as a product with the fp32 reciprocal). Its backward is
 // the same scaling of the incoming gradient. The fp32 form (an fp32 skip path plus a bf16
 // branch) does torch's fp32 add and scaling in one pass, and its backward writes both
-// operands' gradients in one pass.
+// operands' gradients in one pass. The decoder's upsample + concatenation is one pass each way
+// as well (below).
 #include "dpa_common.hpp"
 
 namespace dpa {
@@ -71,9 +72,160 @@ __global__ __launch_bounds__(kEwThreads) void residual_f32_bwd_kernel(
   gb[i] = uint2{pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w)};
 }
 
+// Decoder input of the U-Net (diffusion/unet.py:389-392): y = cat([up(a), h], channels) in
+// NHWC, fp32 (autocast runs F.interpolate in fp32 and the concatenation promotes), where
+// up(a) is a 2x nearest upsampling of a (or a itself). One pass reads a and h once and writes
+// y; the upsampled tensor is never formed. 4 channels per thread.
+template <typename T>
+__device__ __forceinline__ float4 load4f(const T* p);
+template <>
+__device__ __forceinline__ float4 load4f<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <>
+__device__ __forceinline__ float4 load4f<uint16_t>(const uint16_t* p) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  return float4{bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y)};
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float4 v);
+template <>
+__device__ __forceinline__ void store4<float>(float* p, float4 v) {
+  *reinterpret_cast<float4*>(p) = v;
+}
+template <>
+__device__ __forceinline__ void store4<uint16_t>(uint16_t* p, float4 v) {
+  *reinterpret_cast<uint2*>(p) = uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+}
+
+struct UpcatArgs {
+  int N, H, W, C1, C2, up;  // output H x W; a is (H >> up) x (W >> up) x C1, h is H x W x C2
+};
+
+template <typename TA, typename TH>
+__global__ __launch_bounds__(kEwThreads) void upcat_fwd_kernel(const TA* __restrict__ a,
+                                                                const TH* __restrict__ h,
+                                                                float* __restrict__ y,
+                                                                UpcatArgs g, int64_t total4) {
+  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= total4) return;
+  const int ct4 = (g.C1 + g.C2) >> 2;
+  const int64_t pix = i / ct4;
+  const int c = (int)(i - pix * ct4) * 4;
+  float4 v;
+  if (c < g.C1) {
+    const int64_t hw = (int64_t)g.H * g.W;
+    const int64_t n = pix / hw;
+    const int r = (int)(pix - n * hw);
+    const int yy = r / g.W, xx = r - yy * g.W;
+    const int64_t q = (n * (g.H >> g.up) + (yy >> g.up)) * (g.W >> g.up) + (xx >> g.up);
+    v = load4f<TA>(a + q * g.C1 + c);
+  } else {
+    v = load4f<TH>(h + pix * g.C2 + (c - g.C1));
+  }
+  *reinterpret_cast<float4*>(y + pix * (g.C1 + g.C2) + c) = v;
+}
+
+// Backward: ga = sum of gy over each 2x2 window (channels < C1), accumulated from zero in
+// row-major order as torch's upsample_nearest2d_backward does, in a's dtype; gh = gy's
+// channels >= C1 in h's dtype. Items [0, na4) are ga's, the rest gh's.
+template <typename TA, typename TH>
+__global__ __launch_bounds__(kEwThreads) void upcat_bwd_kernel(const float* __restrict__ gy,
+                                                                TA* __restrict__ ga,
+                                                                TH* __restrict__ gh, UpcatArgs g,
+                                                                int64_t na4, int64_t total4) {
+  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= total4) return;
+  const int ct = g.C1 + g.C2;
+  if (i < na4) {
+    const int c14 = g.C1 >> 2;
+    const int64_t q = i / c14;
+    const int c = (int)(i - q * c14) * 4;
+    const int hl = g.H >> g.up, wl = g.W >> g.up;
+    const int64_t hwl = (int64_t)hl * wl;
+    const int64_t n = q / hwl;
+    const int r = (int)(q - n * hwl);
+    const int yl = r / wl, xl = r - yl * wl;
+    const int s = 1 << g.up;
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    for (int dy = 0; dy < s; ++dy)
+      for (int dx = 0; dx < s; ++dx) {
+        const int64_t p = (n * g.H + (yl * s + dy)) * g.W + (xl * s + dx);
+        const float4 v = *reinterpret_cast<const float4*>(gy + p * ct + c);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+    store4<TA>(ga + q * g.C1 + c, acc);
+  } else {
+    const int64_t j = i - na4;
+    const int c24 = g.C2 >> 2;
+    const int64_t p = j / c24;
+    const int c = (int)(j - p * c24) * 4;
+    store4<TH>(gh + p * g.C2 + c, *reinterpret_cast<const float4*>(gy + p * ct + g.C1 + c));
+  }
+}
+
 }  // namespace dpa
 
 using namespace dpa;
+
+static int upcat_check(const void* a, const void* h, const void* y, int a_f32, int h_f32, int N,
+                       int H, int W, int C1, int C2, int up) {
+  if (!a || !h || !y) return DPA_ERR_NULL;
+  if (N <= 0 || H <= 0 || W <= 0 || C1 <= 0 || C2 <= 0 || C1 % 4 || C2 % 4) return DPA_ERR_SIZE;
+  if ((up != 0 && up != 1) || (up && (H % 2 || W % 2))) return DPA_ERR_SHAPE;
+  if ((int64_t)N * H * W * (C1 + C2) > ((int64_t)1 << 40)) return DPA_ERR_SIZE;
+  if (!aligned(a, a_f32 ? 16 : 8) || !aligned(h, h_f32 ? 16 : 8) || !aligned(y, 16))
+    return DPA_ERR_ALIGN;
+  return DPA_OK;
+}
+
+extern "C" int dpa_upsample_concat_f32(const void* a, int a_dtype, const void* h, int h_dtype,
+                                       float* y, int N, int H, int W, int C1, int C2, int up,
+                                       void* stream) {
+  const int af = a_dtype == DPA_DTYPE_F32, hf = h_dtype == DPA_DTYPE_F32;
+  if ((!af && a_dtype != DPA_DTYPE_BF16) || (!hf && h_dtype != DPA_DTYPE_BF16)) return DPA_ERR_SHAPE;
+  const int st = upcat_check(a, h, y, af, hf, N, H, W, C1, C2, up);
+  if (st != DPA_OK) return st;
+  UpcatArgs g{N, H, W, C1, C2, up};
+  const int64_t total4 = (int64_t)N * H * W * ((C1 + C2) / 4);
+  const unsigned grid = (unsigned)ceil_div(total4, (int64_t)kEwThreads);
+  hipStream_t s = (hipStream_t)stream;
+  if (af && hf)
+    upcat_fwd_kernel<float, float><<<grid, kEwThreads, 0, s>>>((const float*)a, (const float*)h, y, g, total4);
+  else if (af)
+    upcat_fwd_kernel<float, uint16_t><<<grid, kEwThreads, 0, s>>>((const float*)a, (const uint16_t*)h, y, g, total4);
+  else if (hf)
+    upcat_fwd_kernel<uint16_t, float><<<grid, kEwThreads, 0, s>>>((const uint16_t*)a, (const float*)h, y, g, total4);
+  else
+    upcat_fwd_kernel<uint16_t, uint16_t><<<grid, kEwThreads, 0, s>>>((const uint16_t*)a, (const uint16_t*)h, y, g, total4);
+  return launch_status();
+}
+
+extern "C" int dpa_upsample_concat_bwd_f32(const float* gy, void* ga, int a_dtype, void* gh,
+                                           int h_dtype, int N, int H, int W, int C1, int C2,
+                                           int up, void* stream) {
+  const int af = a_dtype == DPA_DTYPE_F32, hf = h_dtype == DPA_DTYPE_F32;
+  if ((!af && a_dtype != DPA_DTYPE_BF16) || (!hf && h_dtype != DPA_DTYPE_BF16)) return DPA_ERR_SHAPE;
+  const int st = upcat_check(ga, gh, gy, af, hf, N, H, W, C1, C2, up);
+  if (st != DPA_OK) return st;
+  UpcatArgs g{N, H, W, C1, C2, up};
+  const int64_t na4 = (int64_t)N * (H >> up) * (W >> up) * (C1 / 4);
+  const int64_t total4 = na4 + (int64_t)N * H * W * (C2 / 4);
+  const unsigned grid = (unsigned)ceil_div(total4, (int64_t)kEwThreads);
+  hipStream_t s = (hipStream_t)stream;
+  if (af && hf)
+    upcat_bwd_kernel<float, float><<<grid, kEwThreads, 0, s>>>(gy, (float*)ga, (float*)gh, g, na4, total4);
+  else if (af)
+    upcat_bwd_kernel<float, uint16_t><<<grid, kEwThreads, 0, s>>>(gy, (float*)ga, (uint16_t*)gh, g, na4, total4);
+  else if (hf)
+    upcat_bwd_kernel<uint16_t, float><<<grid, kEwThreads, 0, s>>>(gy, (uint16_t*)ga, (float*)gh, g, na4, total4);
+  else
+    upcat_bwd_kernel<uint16_t, uint16_t><<<grid, kEwThreads, 0, s>>>(gy, (uint16_t*)ga, (uint16_t*)gh, g, na4, total4);
+  return launch_status();
+}
 
 extern "C" int dpa_residual_scale_f32(const float* a, const void* b, float* y, int64_t n,
                                       float inv, void* stream) {

@@ -85,3 +85,52 @@ def residual_join(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
             if a.dtype == torch.bfloat16 and b.dtype == torch.float32:
                 return ResidualScaleF32.apply(b, a)
     return (a + b) / math.sqrt(2.0)
+
+
+_DT = {torch.bfloat16: 0, torch.float32: 1}  # include/dpa_fp8.h DPA_DTYPE_*
+
+
+class UpsampleConcat(torch.autograd.Function):
+    """cat([up(a), h], dim=1), fp32, NHWC, with up the 2x nearest upsampling (or identity):
+    the decoder input of diffusion/unet.py:389-392 in one pass each way."""
+
+    @staticmethod
+    def forward(ctx: Any, a: torch.Tensor, h: torch.Tensor, up: bool) -> torch.Tensor:
+        n, c1, ha, wa = a.shape
+        _, c2, hh, wh = h.shape
+        y = torch.empty((n, c1 + c2, hh, wh), device=a.device, dtype=torch.float32,
+                        memory_format=torch.channels_last)
+        _lib.call("dpa_upsample_concat_f32", a.data_ptr(), _DT[a.dtype], h.data_ptr(),
+                  _DT[h.dtype], y.data_ptr(), n, hh, wh, c1, c2, int(up), _stream(a))
+        ctx.meta = (a.shape, a.dtype, h.shape, h.dtype, int(up))
+        return y
+
+    @staticmethod
+    def backward(ctx: Any, gy: torch.Tensor):
+        a_shape, a_dtype, h_shape, h_dtype, up = ctx.meta
+        gy = gy.float().contiguous(memory_format=torch.channels_last)
+        ga = torch.empty(a_shape, device=gy.device, dtype=a_dtype, memory_format=torch.channels_last)
+        gh = torch.empty(h_shape, device=gy.device, dtype=h_dtype, memory_format=torch.channels_last)
+        n, c1 = a_shape[0], a_shape[1]
+        c2, hh, wh = h_shape[1], h_shape[2], h_shape[3]
+        _lib.call("dpa_upsample_concat_bwd_f32", gy.data_ptr(), ga.data_ptr(), _DT[a_dtype],
+                  gh.data_ptr(), _DT[h_dtype], n, hh, wh, c1, c2, up, _stream(gy))
+        return ga, gh, None
+
+
+def upsample_concat(a: torch.Tensor, h: torch.Tensor, up: bool) -> torch.Tensor:
+    """torch.concat([F.interpolate(a, scale_factor=2, mode="nearest") if up else a, h], 1) as
+    autocast evaluates it (fp32 result)."""
+    cl = torch.channels_last
+    # the fused result is fp32: what autocast's fp32 interpolate and the promoting concat give
+    f32_result = (up and torch.is_autocast_enabled("cuda")) or torch.float32 in (a.dtype, h.dtype)
+    if (f32_result and a.is_cuda and a.dtype in _DT and h.dtype in _DT and a.ndim == 4 and h.ndim == 4
+            and a.is_contiguous(memory_format=cl) and h.is_contiguous(memory_format=cl)
+            and a.shape[1] % 4 == 0 and h.shape[1] % 4 == 0
+            and a.shape[0] == h.shape[0]
+            and a.shape[2] << int(up) == h.shape[2] and a.shape[3] << int(up) == h.shape[3]
+            and a.data_ptr() % 16 == 0 and h.data_ptr() % 16 == 0):
+        return UpsampleConcat.apply(a, h, up)
+    import torch.nn.functional as F
+    x = F.interpolate(a, scale_factor=2.0, mode="nearest") if up else a
+    return torch.concat([x, h], dim=1)

@@ -33,7 +33,7 @@ import torch.nn.functional as F
 
 from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
-from .residual import residual_join
+from .residual import residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
 from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
@@ -501,8 +501,8 @@ class UNet(nn.Module):
         act = self.mid(act, t_emb)
         for i, stage in enumerate(self.up_stages):
             h = hs.pop()
-            up = self.upsample(act) if i > 0 else act
-            act = stage(torch.concat([up, h], dim=1), t_emb)
+            # torch.concat([self.upsample(act) if i > 0 else act, h], dim=1), one pass on the GPU
+            act = stage(upsample_concat(act, h, up=i > 0), t_emb)
         return self.out(act)
 
 

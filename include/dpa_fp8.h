@@ -369,6 +369,20 @@ int dpa_residual_scale_f32(const float* a, const void* b, float* y, int64_t n, f
 int dpa_residual_scale_bwd_f32(const float* g, float* ga, void* gb, int64_t n, float inv,
                                void* stream);
 
+/* Decoder input of the U-Net: y = cat([up(a), h], dim=1) in NHWC, fp32, where up is the 2x
+ * nearest upsampling (up = 1) or the identity (up = 0) -- diffusion/unet.py:389-392,
+ * torch.concat([self.upsample(act), h]) under autocast (F.interpolate runs in fp32 and the
+ * concatenation promotes). a: [N][H >> up][W >> up][C1], h: [N][H][W][C2], each bf16 or fp32
+ * (DPA_DTYPE_*); y: [N][H][W][C1 + C2] fp32. C1, C2 multiples of 4. One pass, no upsampled
+ * intermediate. */
+int dpa_upsample_concat_f32(const void* a, int a_dtype, const void* h, int h_dtype, float* y,
+                            int N, int H, int W, int C1, int C2, int up, void* stream);
+/* Its backward from gy (fp32, y's shape): ga = the sum of gy over each up x up window
+ * (accumulated from zero in row-major order, as torch's upsample_nearest2d_backward), gh =
+ * gy's last C2 channels, each in its operand's dtype. */
+int dpa_upsample_concat_bwd_f32(const float* gy, void* ga, int a_dtype, void* gh, int h_dtype,
+                                int N, int H, int W, int C1, int C2, int up, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Optimizer tail of the training step (train.py:104-149): clip_grad_norm_(max_norm),
  * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,

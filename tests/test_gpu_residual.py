@@ -60,3 +60,37 @@ def test_residual_join_fp32_stream_bit_exact(shape, cl, swap):
     assert torch.equal(y1, y2)
     assert a1.grad.dtype == torch.float32 and b1.grad.dtype == torch.bfloat16
     assert torch.equal(a1.grad, a2.grad) and torch.equal(b1.grad, b2.grad)
+
+
+@pytest.mark.parametrize("n,c1,c2,h,w,up,a32,h32", [
+    (4, 256, 256, 32, 32, True, False, False),   # decoder top level: bf16 act, bf16 skip
+    (4, 256, 256, 16, 16, True, False, True),    # bf16 act, fp32 skip
+    (3, 256, 256, 8, 8, True, True, True),
+    (2, 256, 256, 4, 4, False, True, True),      # first decoder stage: no upsampling
+    (2, 128, 64, 6, 10, True, True, False),      # odd channel split, non-square
+])
+def test_upsample_concat_bit_exact(n, c1, c2, h, w, up, a32, h32):
+    """cat([F.interpolate(a, 2x nearest), h], 1) as the U-Net evaluates it under autocast
+    (diffusion/unet.py:389-392): the fp32 output and both gradients (the upsampling's summed
+    in torch's order, each cast to its operand's dtype) bit for bit."""
+    g = torch.Generator().manual_seed(n * 100 + c1 + h)
+    hl, wl = (h // 2, w // 2) if up else (h, w)
+    a = torch.randn((n, c1, hl, wl), generator=g) * 2
+    hh = torch.randn((n, c2, h, w), generator=g)
+    gy = torch.randn((n, c1 + c2, h, w), generator=g) * 1e-2
+    a = a.cuda().to(torch.float32 if a32 else torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    hh = hh.cuda().to(torch.float32 if h32 else torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    gy = gy.cuda().contiguous(memory_format=torch.channels_last)
+    a1, h1 = a.clone().requires_grad_(), hh.clone().requires_grad_()
+    a2, h2 = a.clone().requires_grad_(), hh.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y1 = R.upsample_concat(a1, h1, up)
+        x2 = torch.nn.functional.interpolate(a2, scale_factor=2.0, mode="nearest") if up else a2
+        y2 = torch.concat([x2, h2], dim=1)
+    assert y1.dtype == y2.dtype == torch.float32
+    y1.backward(gy)
+    y2.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert a1.grad.dtype == a.dtype and h1.grad.dtype == hh.dtype
+    assert torch.equal(a1.grad, a2.grad) and torch.equal(h1.grad, h2.grad)
