@@ -167,9 +167,84 @@ __global__ __launch_bounds__(kEwThreads) void upcat_bwd_kernel(const float* __re
   }
 }
 
+// Encoder downsampling F.interpolate(a, scale_factor=0.5, mode="nearest") (diffusion/unet.py:
+// 370-373) under autocast: y[i][j] = f32(a[2i][2j]) in NHWC, fp32 out; backward ga[2i][2j] =
+// gy[i][j] and 0 elsewhere, in a's dtype. 4 channels per thread.
+template <typename TA>
+__global__ __launch_bounds__(kEwThreads) void down2_fwd_kernel(const TA* __restrict__ a,
+                                                                float* __restrict__ y, int H,
+                                                                int W, int C, int64_t total4) {
+  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= total4) return;
+  const int c4 = C >> 2, ho = H >> 1, wo = W >> 1;
+  const int64_t q = i / c4;
+  const int c = (int)(i - q * c4) * 4;
+  const int64_t hwo = (int64_t)ho * wo;
+  const int64_t n = q / hwo;
+  const int r = (int)(q - n * hwo);
+  const int yo = r / wo, xo = r - yo * wo;
+  const int64_t p = (n * H + 2 * yo) * W + 2 * xo;
+  *reinterpret_cast<float4*>(y + q * C + c) = load4f<TA>(a + p * C + c);
+}
+
+template <typename TA>
+__global__ __launch_bounds__(kEwThreads) void down2_bwd_kernel(const float* __restrict__ gy,
+                                                                TA* __restrict__ ga, int H, int W,
+                                                                int C, int64_t total4) {
+  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= total4) return;
+  const int c4 = C >> 2;
+  const int64_t p = i / c4;
+  const int c = (int)(i - p * c4) * 4;
+  const int64_t hw = (int64_t)H * W;
+  const int64_t n = p / hw;
+  const int r = (int)(p - n * hw);
+  const int yy = r / W, xx = r - yy * W;
+  float4 v = float4{0.f, 0.f, 0.f, 0.f};
+  if (((yy | xx) & 1) == 0) {
+    const int64_t q = (n * (H >> 1) + (yy >> 1)) * (W >> 1) + (xx >> 1);
+    v = *reinterpret_cast<const float4*>(gy + q * C + c);
+  }
+  store4<TA>(ga + p * C + c, v);
+}
+
 }  // namespace dpa
 
 using namespace dpa;
+
+extern "C" int dpa_downsample2_f32(const void* a, int a_dtype, float* y, int N, int H, int W,
+                                   int C, void* stream) {
+  const int af = a_dtype == DPA_DTYPE_F32;
+  if (!af && a_dtype != DPA_DTYPE_BF16) return DPA_ERR_SHAPE;
+  if (!a || !y) return DPA_ERR_NULL;
+  if (N <= 0 || H <= 0 || W <= 0 || C <= 0 || C % 4) return DPA_ERR_SIZE;
+  if (H % 2 || W % 2) return DPA_ERR_SHAPE;
+  if (!aligned(a, af ? 16 : 8) || !aligned(y, 16)) return DPA_ERR_ALIGN;
+  const int64_t total4 = (int64_t)N * (H / 2) * (W / 2) * (C / 4);
+  const unsigned grid = (unsigned)ceil_div(total4, (int64_t)kEwThreads);
+  if (af)
+    down2_fwd_kernel<float><<<grid, kEwThreads, 0, (hipStream_t)stream>>>((const float*)a, y, H, W, C, total4);
+  else
+    down2_fwd_kernel<uint16_t><<<grid, kEwThreads, 0, (hipStream_t)stream>>>((const uint16_t*)a, y, H, W, C, total4);
+  return launch_status();
+}
+
+extern "C" int dpa_downsample2_bwd_f32(const float* gy, void* ga, int a_dtype, int N, int H,
+                                       int W, int C, void* stream) {
+  const int af = a_dtype == DPA_DTYPE_F32;
+  if (!af && a_dtype != DPA_DTYPE_BF16) return DPA_ERR_SHAPE;
+  if (!gy || !ga) return DPA_ERR_NULL;
+  if (N <= 0 || H <= 0 || W <= 0 || C <= 0 || C % 4) return DPA_ERR_SIZE;
+  if (H % 2 || W % 2) return DPA_ERR_SHAPE;
+  if (!aligned(ga, af ? 16 : 8) || !aligned(gy, 16)) return DPA_ERR_ALIGN;
+  const int64_t total4 = (int64_t)N * H * W * (C / 4);
+  const unsigned grid = (unsigned)ceil_div(total4, (int64_t)kEwThreads);
+  if (af)
+    down2_bwd_kernel<float><<<grid, kEwThreads, 0, (hipStream_t)stream>>>(gy, (float*)ga, H, W, C, total4);
+  else
+    down2_bwd_kernel<uint16_t><<<grid, kEwThreads, 0, (hipStream_t)stream>>>(gy, (uint16_t*)ga, H, W, C, total4);
+  return launch_status();
+}
 
 static int upcat_check(const void* a, const void* h, const void* y, int a_f32, int h_f32, int N,
                        int H, int W, int C1, int C2, int up) {

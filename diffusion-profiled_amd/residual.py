@@ -134,3 +134,39 @@ def upsample_concat(a: torch.Tensor, h: torch.Tensor, up: bool) -> torch.Tensor:
     import torch.nn.functional as F
     x = F.interpolate(a, scale_factor=2.0, mode="nearest") if up else a
     return torch.concat([x, h], dim=1)
+
+
+class Downsample2(torch.autograd.Function):
+    """F.interpolate(a, scale_factor=0.5, mode="nearest") as autocast evaluates it: fp32 out,
+    gradient in a's dtype (zero off the sampled pixels); NHWC, one pass each way."""
+
+    @staticmethod
+    def forward(ctx: Any, a: torch.Tensor) -> torch.Tensor:
+        n, c, h, w = a.shape
+        y = torch.empty((n, c, h // 2, w // 2), device=a.device, dtype=torch.float32,
+                        memory_format=torch.channels_last)
+        _lib.call("dpa_downsample2_f32", a.data_ptr(), _DT[a.dtype], y.data_ptr(), n, h, w, c,
+                  _stream(a))
+        ctx.meta = (a.shape, a.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx: Any, gy: torch.Tensor):
+        shape, dtype = ctx.meta
+        gy = gy.float().contiguous(memory_format=torch.channels_last)
+        ga = torch.empty(shape, device=gy.device, dtype=dtype, memory_format=torch.channels_last)
+        n, c, h, w = shape
+        _lib.call("dpa_downsample2_bwd_f32", gy.data_ptr(), ga.data_ptr(), _DT[dtype], n, h, w, c,
+                  _stream(gy))
+        return ga
+
+
+def downsample2(a: torch.Tensor) -> torch.Tensor:
+    """F.interpolate(a, scale_factor=0.5, mode="nearest") (fp32 under autocast)."""
+    if ((torch.is_autocast_enabled("cuda") or a.dtype == torch.float32) and a.is_cuda
+            and a.dtype in _DT and a.ndim == 4 and a.shape[1] % 4 == 0
+            and a.shape[2] % 2 == 0 and a.shape[3] % 2 == 0
+            and a.is_contiguous(memory_format=torch.channels_last) and a.data_ptr() % 16 == 0):
+        return Downsample2.apply(a)
+    import torch.nn.functional as F
+    return F.interpolate(a, scale_factor=0.5, mode="nearest")

@@ -33,7 +33,7 @@ import torch.nn.functional as F
 
 from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
-from .residual import residual_join, upsample_concat
+from .residual import downsample2, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
 from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
@@ -496,7 +496,8 @@ class UNet(nn.Module):
         act = self.conv_in(x)
         hs = []
         for i, stage in enumerate(self.down_stages):
-            act = stage(self.downsample(act) if i > 0 else act, t_emb)
+            # self.downsample(act): F.interpolate(scale 0.5, nearest), one pass on the GPU
+            act = stage(downsample2(act) if i > 0 else act, t_emb)
             hs.append(act)
         act = self.mid(act, t_emb)
         for i, stage in enumerate(self.up_stages):

@@ -383,6 +383,15 @@ int dpa_upsample_concat_f32(const void* a, int a_dtype, const void* h, int h_dty
 int dpa_upsample_concat_bwd_f32(const float* gy, void* ga, int a_dtype, void* gh, int h_dtype,
                                 int N, int H, int W, int C1, int C2, int up, void* stream);
 
+/* Encoder downsampling F.interpolate(a, scale_factor=0.5, mode="nearest") under autocast
+ * (diffusion/unet.py:370-373): y[n][i][j][c] = a[n][2i][2j][c] as fp32; a [N][H][W][C] bf16
+ * or fp32 (H, W even, C % 4 == 0), y [N][H/2][W/2][C]. The backward writes ga (a's dtype and
+ * shape): gy at the sampled pixels, 0 elsewhere. One pass each. */
+int dpa_downsample2_f32(const void* a, int a_dtype, float* y, int N, int H, int W, int C,
+                        void* stream);
+int dpa_downsample2_bwd_f32(const float* gy, void* ga, int a_dtype, int N, int H, int W, int C,
+                            void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Optimizer tail of the training step (train.py:104-149): clip_grad_norm_(max_norm),
  * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,

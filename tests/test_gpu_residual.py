@@ -94,3 +94,25 @@ def test_upsample_concat_bit_exact(n, c1, c2, h, w, up, a32, h32):
     assert torch.equal(y1, y2)
     assert a1.grad.dtype == a.dtype and h1.grad.dtype == hh.dtype
     assert torch.equal(a1.grad, a2.grad) and torch.equal(h1.grad, h2.grad)
+
+
+@pytest.mark.parametrize("n,c,h,w,a32", [(4, 128, 32, 32, False), (4, 256, 16, 16, True),
+                                         (3, 256, 8, 8, True), (2, 64, 6, 10, False)])
+def test_downsample2_bit_exact(n, c, h, w, a32):
+    """F.interpolate(a, scale_factor=0.5, mode="nearest") under autocast (diffusion/unet.py:
+    370-373): fp32 output and the input gradient (in a's dtype) bit for bit."""
+    g = torch.Generator().manual_seed(n + c + h)
+    a = (torch.randn((n, c, h, w), generator=g) * 2).cuda()
+    a = a.to(torch.float32 if a32 else torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    gy = (torch.randn((n, c, h // 2, w // 2), generator=g) * 1e-2).cuda().contiguous(
+        memory_format=torch.channels_last)
+    a1, a2 = a.clone().requires_grad_(), a.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y1 = R.downsample2(a1)
+        y2 = torch.nn.functional.interpolate(a2, scale_factor=0.5, mode="nearest")
+    assert y1.dtype == y2.dtype == torch.float32
+    y1.backward(gy)
+    y2.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert a1.grad.dtype == a.dtype and torch.equal(a1.grad, a2.grad)

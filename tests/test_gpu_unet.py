@@ -197,8 +197,11 @@ def test_graph_captured_step_matches_eager_steps():
     for (name, buf), q in zip(a.model.named_buffers(), b.model.buffers()):
         if buf.dtype == torch.long:                  # window positions: exact
             assert torch.equal(buf, q), name
-        else:                                        # amax windows: scales of bf16 amaxes
-            torch.testing.assert_close(buf, q, rtol=2**-7, atol=0, msg=name)
+        else:
+            # amax windows: scales of bf16 amaxes. The MIOpen convs' gradient noise reaches the
+            # dy maxima of the deepest blocks: measured 0 on one box and up to 1.4e-2 relative
+            # on another (down_stages.3 conv_2 dy windows after six steps), so 2^-5
+            torch.testing.assert_close(buf, q, rtol=2**-5, atol=0, msg=name)
 
 
 def _conv_by_matmul(x: torch.Tensor, w: torch.Tensor, pad: int) -> torch.Tensor:
