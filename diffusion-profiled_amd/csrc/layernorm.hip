@@ -14,6 +14,8 @@
 // makes one memory round trip. The backward's column sums go to per-workgroup partials (a
 // fixed row range each), reduced over workgroups in a fixed order by a second kernel
 // (deterministic).
+#include <type_traits>
+
 #include "dpa_common.hpp"
 
 namespace dpa {
@@ -30,11 +32,11 @@ template <int V>
 constexpr int ln_rows_per_block() { return kLnWaves * ln_rows<V>(); }
 
 struct LnArgs {
-  const uint16_t* x;
+  const void* x;  // bf16 or fp32 rows
   const uint16_t* dout;
   const float* gamma;
   const float* beta;
-  uint16_t* out;
+  void* out;  // forward: bf16 y; backward: dx in x's type
   float* mean;
   float* rstd;
   float* part;  // bwd: [blocks][2][C]
@@ -98,16 +100,69 @@ __device__ __forceinline__ void ln_store(uint16_t* row, int lane, const float (&
   }
 }
 
+// fp32 rows (the fp32 residual stream, which autocast's float32 LayerNorm reads as it is)
 template <int V>
+struct LnRawF {
+  float f[V];
+};
+
+template <int V>
+__device__ __forceinline__ void ln_load(const float* row, int lane, LnRawF<V>& r) {
+  const float* p = row + lane * V;
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+      const float4 u = *reinterpret_cast<const float4*>(p + k);
+      r.f[k] = u.x;
+      r.f[k + 1] = u.y;
+      r.f[k + 2] = u.z;
+      r.f[k + 3] = u.w;
+    }
+  } else if constexpr (V == 2) {
+    const float2 u = *reinterpret_cast<const float2*>(p);
+    r.f[0] = u.x;
+    r.f[1] = u.y;
+  } else {
+    r.f[0] = p[0];
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void ln_unpack(const LnRawF<V>& r, float (&f)[V]) {
+#pragma unroll
+  for (int k = 0; k < V; ++k) f[k] = r.f[k];
+}
+
+template <int V>
+__device__ __forceinline__ void ln_store(float* row, int lane, const float (&f)[V]) {
+  float* p = row + lane * V;
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < V; k += 4)
+      *reinterpret_cast<float4*>(p + k) = float4{f[k], f[k + 1], f[k + 2], f[k + 3]};
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k) p[k] = f[k];
+  }
+}
+
+template <bool kF32>
+using LnXT = typename std::conditional<kF32, float, uint16_t>::type;
+template <int V, bool kF32>
+using LnXRaw = typename std::conditional<kF32, LnRawF<V>, LnRaw<V>>::type;
+
+template <int V, bool kF32>
 __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const LnArgs p) {
+  using XT = LnXT<kF32>;
+  const XT* px = static_cast<const XT*>(p.x);
   constexpr int R = ln_rows<V>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = (int64_t)blockIdx.x * ln_rows_per_block<V>() + wave * R;
-  LnRaw<V> raw[R];
+  LnXRaw<V, kF32> raw[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i < p.rows ? r0 + i : p.rows - 1;  // past the end: a valid row
-    ln_load<V>(p.x + r * p.C, lane, raw[i]);
+    ln_load<V>(px + r * p.C, lane, raw[i]);
   }
   float g[V], b[V];
 #pragma unroll
@@ -135,7 +190,7 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const LnArgs p) {
 #pragma unroll
     for (int k = 0; k < V; ++k) f[k] = (f[k] - mu) * rs * g[k] + b[k];
     if (r < p.rows) {
-      ln_store<V>(p.out + r * p.C, lane, f);
+      ln_store<V>(static_cast<uint16_t*>(p.out) + r * p.C, lane, f);
       if (lane == 0) {
         p.mean[r] = mu;
         p.rstd[r] = rs;
@@ -144,18 +199,21 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const LnArgs p) {
   }
 }
 
-template <int V>
+template <int V, bool kF32>
 __global__ __launch_bounds__(kLnThreads) void ln_bwd_kernel(const LnArgs p) {
+  using XT = LnXT<kF32>;
+  const XT* px = static_cast<const XT*>(p.x);
   constexpr int R = ln_rows<V>();
   __shared__ float red[kLnWaves][2][64 * V];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = (int64_t)blockIdx.x * ln_rows_per_block<V>() + wave * R;
-  LnRaw<V> rx[R], rd[R];
+  LnXRaw<V, kF32> rx[R];
+  LnRaw<V> rd[R];
   float mus[R], rss[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i < p.rows ? r0 + i : p.rows - 1;
-    ln_load<V>(p.x + r * p.C, lane, rx[i]);
+    ln_load<V>(px + r * p.C, lane, rx[i]);
     ln_load<V>(p.dout + r * p.C, lane, rd[i]);
     mus[i] = p.mean[r];
     rss[i] = p.rstd[r];
@@ -193,7 +251,7 @@ __global__ __launch_bounds__(kLnThreads) void ln_bwd_kernel(const LnArgs p) {
     const float m1 = wave_sum_f32(s1) * inv_c, m2 = wave_sum_f32(s2) * inv_c;
 #pragma unroll
     for (int k = 0; k < V; ++k) f[k] = rs * (d[k] - m1 - f[k] * m2);
-    if (live) ln_store<V>(p.out + r * p.C, lane, f);
+    if (live) ln_store<V>(static_cast<XT*>(p.out) + r * p.C, lane, f);
   }
   // this block's column sums: the waves in order
 #pragma unroll
@@ -263,29 +321,34 @@ static bool ln_shape_ok(int64_t rows, int C) {
          (v == 1 || v == 2 || v == 4 || v == 8 || v == 16);
 }
 
-template <template <int> class Launch>
-static int ln_dispatch(int C, hipStream_t s, const LnArgs& a, int blocks) {
+template <template <int, bool> class Launch, bool kF32>
+static int ln_dispatch_t(int C, hipStream_t s, const LnArgs& a, int blocks) {
   switch (C / 64) {
-    case 1: Launch<1>::go(a, blocks, s); break;
-    case 2: Launch<2>::go(a, blocks, s); break;
-    case 4: Launch<4>::go(a, blocks, s); break;
-    case 8: Launch<8>::go(a, blocks, s); break;
-    case 16: Launch<16>::go(a, blocks, s); break;
+    case 1: Launch<1, kF32>::go(a, blocks, s); break;
+    case 2: Launch<2, kF32>::go(a, blocks, s); break;
+    case 4: Launch<4, kF32>::go(a, blocks, s); break;
+    case 8: Launch<8, kF32>::go(a, blocks, s); break;
+    case 16: Launch<16, kF32>::go(a, blocks, s); break;
     default: return DPA_ERR_SHAPE;
   }
   return launch_status();
 }
+template <template <int, bool> class Launch>
+static int ln_dispatch(int C, hipStream_t s, const LnArgs& a, int blocks, bool f32 = false) {
+  return f32 ? ln_dispatch_t<Launch, true>(C, s, a, blocks)
+             : ln_dispatch_t<Launch, false>(C, s, a, blocks);
+}
 
-template <int V>
+template <int V, bool kF32>
 struct LnFwdLaunch {
   static void go(const LnArgs& a, int blocks, hipStream_t s) {
-    ln_fwd_kernel<V><<<(unsigned)blocks, kLnThreads, 0, s>>>(a);
+    ln_fwd_kernel<V, kF32><<<(unsigned)blocks, kLnThreads, 0, s>>>(a);
   }
 };
-template <int V>
+template <int V, bool kF32>
 struct LnBwdLaunch {
   static void go(const LnArgs& a, int blocks, hipStream_t s) {
-    ln_bwd_kernel<V><<<(unsigned)blocks, kLnThreads, 0, s>>>(a);
+    ln_bwd_kernel<V, kF32><<<(unsigned)blocks, kLnThreads, 0, s>>>(a);
   }
 };
 
@@ -293,23 +356,35 @@ struct LnBwdLaunch {
 
 using namespace dpa;
 
-extern "C" int dpa_layernorm_fwd_bf16(const void* x, const float* gamma, const float* beta,
-                                      void* out, float* mean, float* rstd, int64_t rows, int C,
-                                      float eps, void* stream) {
+static int ln_fwd(const void* x, bool f32, const float* gamma, const float* beta, void* out,
+                  float* mean, float* rstd, int64_t rows, int C, float eps, void* stream) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if (!ln_shape_ok(rows, C)) return DPA_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(out, 16)) return DPA_ERR_ALIGN;
   LnArgs a{};
-  a.x = (const uint16_t*)x;
+  a.x = x;
   a.gamma = gamma;
   a.beta = beta;
-  a.out = (uint16_t*)out;
+  a.out = out;
   a.mean = mean;
   a.rstd = rstd;
   a.rows = rows;
   a.C = C;
   a.eps = eps;
-  return ln_dispatch<LnFwdLaunch>(C, (hipStream_t)stream, a, ln_blocks(rows, C));
+  return ln_dispatch<LnFwdLaunch>(C, (hipStream_t)stream, a, ln_blocks(rows, C), f32);
+}
+
+extern "C" int dpa_layernorm_fwd_bf16(const void* x, const float* gamma, const float* beta,
+                                      void* out, float* mean, float* rstd, int64_t rows, int C,
+                                      float eps, void* stream) {
+  return ln_fwd(x, false, gamma, beta, out, mean, rstd, rows, C, eps, stream);
+}
+
+extern "C" int dpa_layernorm_fwd_ex(const void* x, int x_dtype, const float* gamma,
+                                    const float* beta, void* out, float* mean, float* rstd,
+                                    int64_t rows, int C, float eps, void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  return ln_fwd(x, x_dtype == DPA_DTYPE_F32, gamma, beta, out, mean, rstd, rows, C, eps, stream);
 }
 
 extern "C" int64_t dpa_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
@@ -317,11 +392,9 @@ extern "C" int64_t dpa_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
   return (int64_t)ln_blocks(rows, C) * 2 * C * 4;
 }
 
-extern "C" int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
-                                      const float* mean, const float* rstd, void* dx,
-                                      float* dgamma, float* dbeta, void* workspace,
-                                      int64_t workspace_bytes, int64_t rows, int C,
-                                      void* stream) {
+static int ln_bwd(const void* x, bool f32, const void* dout, const float* gamma,
+                  const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
+                  void* workspace, int64_t workspace_bytes, int64_t rows, int C, void* stream) {
   if (!x || !dout || !gamma || !mean || !rstd || !dx || !dgamma || !dbeta) return DPA_ERR_NULL;
   if (!ln_shape_ok(rows, C)) return DPA_ERR_SHAPE;
   if (!workspace || workspace_bytes < dpa_layernorm_bwd_workspace_bytes(rows, C))
@@ -329,10 +402,10 @@ extern "C" int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const flo
   if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4))
     return DPA_ERR_ALIGN;
   LnArgs a{};
-  a.x = (const uint16_t*)x;
+  a.x = x;
   a.dout = (const uint16_t*)dout;
   a.gamma = gamma;
-  a.out = (uint16_t*)dx;
+  a.out = dx;
   a.mean = const_cast<float*>(mean);
   a.rstd = const_cast<float*>(rstd);
   a.part = (float*)workspace;
@@ -340,9 +413,27 @@ extern "C" int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const flo
   a.C = C;
   hipStream_t s = (hipStream_t)stream;
   const int blocks = ln_blocks(rows, C);
-  int st = ln_dispatch<LnBwdLaunch>(C, s, a, blocks);
+  int st = ln_dispatch<LnBwdLaunch>(C, s, a, blocks, f32);
   if (st != DPA_OK) return st;
   ln_param_reduce_kernel<<<(unsigned)ceil_div(2 * C, 8), kLnThreads, 0, s>>>(
       (const float*)workspace, blocks, C, dgamma, dbeta);
   return launch_status();
+}
+
+extern "C" int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
+                                      const float* mean, const float* rstd, void* dx,
+                                      float* dgamma, float* dbeta, void* workspace,
+                                      int64_t workspace_bytes, int64_t rows, int C,
+                                      void* stream) {
+  return ln_bwd(x, false, dout, gamma, mean, rstd, dx, dgamma, dbeta, workspace,
+                workspace_bytes, rows, C, stream);
+}
+
+extern "C" int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout,
+                                    const float* gamma, const float* mean, const float* rstd,
+                                    void* dx, float* dgamma, float* dbeta, void* workspace,
+                                    int64_t workspace_bytes, int64_t rows, int C, void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  return ln_bwd(x, x_dtype == DPA_DTYPE_F32, dout, gamma, mean, rstd, dx, dgamma, dbeta,
+                workspace, workspace_bytes, rows, C, stream);
 }

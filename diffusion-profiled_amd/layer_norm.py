@@ -2,8 +2,10 @@
 library's dpa_layernorm_*).
 
 Replaces the attention block's ``self.norm(seq)`` (diffusion/unet.py:182, :186), which
-autocast runs in fp32 on an fp32 copy of the bf16 tokens and whose result the qkv projection
-rounds back to bf16: here the kernel reads the bf16 tokens and writes that bf16 result.
+autocast runs in fp32 (on an fp32 copy of bf16 tokens, or on fp32 tokens of the fp32 residual
+stream as they are) and whose result the qkv projection rounds back to bf16: here the kernel
+reads the bf16 or fp32 tokens and writes that bf16 result; the input gradient comes back in
+the tokens' dtype.
 """
 from __future__ import annotations
 
@@ -22,19 +24,24 @@ def supported(c: int) -> bool:
     return c % 64 == 0 and c // 64 in (1, 2, 4, 8, 16)
 
 
+DTYPE_BF16, DTYPE_F32 = 0, 1  # include/dpa_fp8.h DPA_DTYPE_*
+
+
 class LayerNormBF16(torch.autograd.Function):
-    """y = bf16(LayerNorm(x)) over the last axis; x bf16 (rows contiguous), gamma/beta fp32."""
+    """y = bf16(LayerNorm(x)) over the last axis; x bf16 or fp32 (rows contiguous),
+    gamma/beta fp32."""
 
     @staticmethod
     def forward(ctx: Any, x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float):
         c = x.shape[-1]
-        xb = x.to(torch.bfloat16).contiguous()
+        xb = x.contiguous() if x.dtype == torch.float32 else x.to(torch.bfloat16).contiguous()
         rows = xb.numel() // c
-        out = torch.empty_like(xb)
+        out = torch.empty_like(xb, dtype=torch.bfloat16)
         mean = torch.empty(rows, device=x.device, dtype=torch.float32)
         rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
-        _lib.call("dpa_layernorm_fwd_bf16", xb.data_ptr(), g32.data_ptr(), b32.data_ptr(),
+        dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
+        _lib.call("dpa_layernorm_fwd_ex", xb.data_ptr(), dt, g32.data_ptr(), b32.data_ptr(),
                   out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, c, float(eps),
                   _stream(xb))
         ctx.save_for_backward(xb, g32, mean, rstd)
@@ -53,7 +60,8 @@ class LayerNormBF16(torch.autograd.Function):
         dbeta = torch.empty(c, device=xb.device, dtype=torch.float32)
         ws_bytes = _lib.query("dpa_layernorm_bwd_workspace_bytes", rows, c)
         ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
-        _lib.call("dpa_layernorm_bwd_bf16", xb.data_ptr(), dout.data_ptr(), g32.data_ptr(),
+        dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
+        _lib.call("dpa_layernorm_bwd_ex", xb.data_ptr(), dt, dout.data_ptr(), g32.data_ptr(),
                   mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(),
                   dbeta.data_ptr(), ws.data_ptr(), ws_bytes, rows, c, _stream(xb))
         return (dx.to(ctx.x_dtype), dgamma.to(ctx.param_dtypes[0]),

@@ -352,6 +352,17 @@ int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
                            float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
                            int C, void* stream);
 
+/* The LayerNorm entries with x (and dx) in bf16 or fp32 (DPA_DTYPE_*), the output y bf16:
+ * an fp32 token row (the fp32 residual stream) is normalised as it is, as autocast's float32
+ * nn.LayerNorm does (diffusion/unet.py:182), and its gradient returned in fp32. */
+int dpa_layernorm_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
+                         void* out, float* mean, float* rstd, int64_t rows, int C, float eps,
+                         void* stream);
+int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
+                         const float* mean, const float* rstd, void* dx, float* dgamma,
+                         float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
+                         int C, void* stream);
+
 /* Residual join y = (a + b) / sqrt(2) of bf16 tensors in one pass (diffusion/unet.py:161 and
  * :203, under autocast), with torch's roundings: bf16(bf16(a + b) * inv), inv = RN32(1/sqrt 2)
  * passed by the caller. b == NULL gives y = bf16(a * inv) (the backward). n % 8 == 0,

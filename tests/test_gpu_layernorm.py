@@ -73,3 +73,36 @@ def test_layernorm_on_token_view_matches_module():
     frac = float((y == ref).float().mean())
     assert frac > 0.99, frac
     assert float((y.float() - ref.float()).abs().max()) <= 2**-7 * float(ref.float().abs().max())
+
+
+@pytest.mark.parametrize("rows,c", [(512, 256), (37, 256), (300, 64), (129, 128), (33, 1024),
+                                    (64 * 16, 256)])
+def test_layernorm_fp32_tokens_vs_float64(rows, c):
+    """fp32 tokens (the fp32 residual stream of the lower levels) are normalised as they are,
+    as autocast's float32 nn.LayerNorm does: forward within one bf16 ulp of the float64
+    reference on the fp32 values (and away from the bf16-rounded input's result), dx in fp32
+    normwise 2e-5, dgamma/dbeta 1e-4."""
+    g = torch.Generator().manual_seed(rows + c + 3)
+    x = torch.randn((rows, c), generator=g) * 2 + 0.7
+    gamma = 1 + 0.2 * torch.randn(c, generator=g)
+    beta = 0.1 * torch.randn(c, generator=g)
+    dy = (torch.randn((rows, c), generator=g) * 1e-2).to(torch.bfloat16)
+    xd = x.cuda().requires_grad_()
+    gd, bd = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    y = LN.LayerNormBF16.apply(xd, gd, bd, 1e-5)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and xd.grad.dtype == torch.float32
+    xr = x.double().requires_grad_()
+    gr, br = gamma.double().requires_grad_(), beta.double().requires_grad_()
+    yr = F.layer_norm(xr, (c,), gr, br, 1e-5)
+    yr.backward(dy.double())
+    got = y.detach().cpu().double().numpy()
+    want = yr.detach().numpy()
+    assert np.all(np.abs(got - want) <= 2.0**-7 * np.abs(want) + 1e-6), "forward beyond 1 bf16 ulp"
+    assert np.mean(bits(y.detach().cpu()) == bits(yr.detach().float().to(torch.bfloat16))) > 0.99
+    yb16 = F.layer_norm(x.to(torch.bfloat16).double(), (c,), gamma.double(), beta.double(), 1e-5)
+    assert np.mean(bits(yb16.float().to(torch.bfloat16)) != bits(yr.detach().float().to(torch.bfloat16))) > 0.02
+    assert rel(xd.grad.cpu().numpy(), xr.grad.numpy()) < 2e-5
+    assert rel(gd.grad.cpu().numpy(), gr.grad.numpy()) < 1e-4
+    assert rel(bd.grad.cpu().numpy(), br.grad.numpy()) < 1e-4
