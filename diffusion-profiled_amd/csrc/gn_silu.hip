@@ -45,9 +45,35 @@ struct GnArgs {
   float* dfb;
   const uint16_t* wb;  // or FiLM from the bf16 time projection [N][2C]: scale bf16(w + 1), shift b
   uint16_t* dwb;       // bwd: its gradient [N][2C] bf16, or null
+  const uint64_t* drop_seed;  // dropout after the SiLU: seed in device memory, or null
+  uint32_t drop_keep;         // keep an element when its hash is >= this (p * 2^32)
+  float drop_scale;           // RN32(1 / (1 - p))
   int N, HW, C, G, cpg;
   float eps;
 };
+
+// Dropout of the GroupNorm+SiLU output (diffusion/unet.py:160, nn.Dropout before conv_2): the
+// keep decision of element idx (NHWC index) is a counter hash of (seed, idx), so the backward
+// recomputes the mask instead of storing it; kept values are scaled by 1 / (1 - p) in fp32
+// before the bf16 rounding, as the reference drops its fp32 SiLU output before the conv's
+// bf16 cast. The hash: splitmix64 of seed + (idx / 2) * golden ratio, one output per pair of
+// elements, its low 32 bits deciding the even element and its high 32 bits the odd one.
+// Returns the keep bits of the 8 elements idx0 .. idx0 + 7 (idx0 a multiple of 8).
+__device__ __forceinline__ uint32_t drop_keep8(uint64_t seed, int64_t idx0, uint32_t keep_from) {
+  constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+  const uint64_t z0 = seed + (uint64_t)(idx0 >> 1) * kGolden;
+  uint32_t bits = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint64_t z = z0 + (uint64_t)i * kGolden;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    bits |= (uint32_t)((uint32_t)z >= keep_from) << (2 * i);
+    bits |= (uint32_t)((uint32_t)(z >> 32) >= keep_from) << (2 * i + 1);
+  }
+  return bits;
+}
 
 // sigmoid(v) = 1 / (1 + e^-v) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32,
 // about 1 ulp each), e^-v = 2^(-v log2 e). The SiLU and its derivative are rounded to bf16
@@ -652,10 +678,14 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   float fsc[8], fsh[8];
   const bool film = load_film(p, n, ch, fsc, fsh);
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
+  const bool drop = p.drop_seed != nullptr;
+  const uint64_t seed = drop ? *p.drop_seed : 0;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8];
     unpack_x<kF32>(v, u, f);
+    const uint32_t kb =
+        drop ? drop_keep8(seed, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, p.drop_keep) : 0u;
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -666,6 +696,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
         float t = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
         if (film) t = fsc[ee] * t + fsh[ee];
         z[k] = t * sigmoid_hw(t);
+        if (drop) z[k] = (kb >> ee) & 1u ? z[k] * p.drop_scale : 0.0f;
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
@@ -733,6 +764,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const bool drop = p.drop_seed != nullptr;
+  const uint64_t seed = drop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -748,6 +781,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
     float f[8], d[8], xh[8], z[8], g[8];
     unpack_x<kF32>(v, u, f);
     unpack8(v[in.kN - 1][u], d);
+    if (drop) {
+      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
+    }
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     if (ok[u]) {
 #pragma unroll
@@ -785,6 +823,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const bool drop = p.drop_seed != nullptr;
+  const uint64_t seed = drop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -865,6 +905,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
     float f[8], d[8], xh[8], z[8], g[8];
     unpack_x<kF32>(v, u, f);
     unpack8(v[in.kN - 1][u], d);
+    if (drop) {
+      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
+    }
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     auto dx = [&](int e) __attribute__((always_inline)) {
       const int h = e >> 2;
@@ -959,8 +1004,12 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
     }
   }
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
+  const bool drop = p.drop_seed != nullptr;
+  const uint64_t seed = drop ? *p.drop_seed : 0;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
+    const uint32_t kb =
+        drop ? drop_keep8(seed, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, p.drop_keep) : 0u;
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -971,6 +1020,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
         float t = (f[u][ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
         if (kFilm) t = fsc[ee] * t + fsh[ee];
         z[k] = t * sigmoid_hw(t);
+        if (drop) z[k] = (kb >> ee) & 1u ? z[k] * p.drop_scale : 0.0f;
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
@@ -988,6 +1038,8 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
+  const bool drop = p.drop_seed != nullptr;
+  const uint64_t seed = drop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -1004,6 +1056,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
     float f[8], d[8], xh[8], z[8], g[8];
     unpack_x<kF32>(v, u, f);
     unpack8(v[in.kN - 1][u], d);
+    if (drop) {
+      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
+    }
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     if (ok[u]) {
 #pragma unroll
@@ -1056,6 +1113,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
     float f[8], d[8], xh[8], z[8], g[8];
     unpack_x<kF32>(v, u, f);
     unpack8(v[in.kN - 1][u], d);
+    if (drop) {
+      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
+    }
     bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
     auto dx = [&](int e) __attribute__((always_inline)) {
       const int h = e >> 2;
@@ -1089,10 +1151,25 @@ static int64_t gn_fwd_workspace(int N, int HW, int G) {
   return (int64_t)N * gn_chunks(HW) * G * (int64_t)sizeof(float2);
 }
 
+// Dropout arguments: keep when the hash is >= p * 2^32; scale 1 / (1 - p) rounded as torch's
+// dropout forms it (1 - p in double, rounded to fp32, its reciprocal rounded to fp32).
+static int gn_set_dropout(GnArgs& a, const void* seed, float p) {
+  if (!seed) return DPA_OK;
+  if (!(p >= 0.0f && p < 1.0f)) return DPA_ERR_SIZE;
+  if (!aligned(seed, 8)) return DPA_ERR_ALIGN;
+  a.drop_seed = (const uint64_t*)seed;
+  const double t = (double)p * 4294967296.0;
+  a.drop_keep = t >= 4294967295.0 ? 0xffffffffu : (uint32_t)t;
+  const float pa = (float)(1.0 - (double)p);
+  a.drop_scale = (float)(1.0 / (double)pa);
+  return DPA_OK;
+}
+
 static int gn_fwd(const void* x, const float* gamma, const float* beta, const float* film_scale,
                   const float* film_shift, const void* film_wb, void* out, float* mean,
                   float* rstd, int N, int HW, int C, int G, float eps, void* stream,
-                  void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false) {
+                  void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false,
+                  const void* drop_seed = nullptr, float drop_p = 0.0f) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
@@ -1111,8 +1188,11 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   const int nchunk = gn_chunks(HW);
   const bool chunked = nchunk > 0 && workspace && workspace_bytes >= gn_fwd_workspace(N, HW, G) &&
                        aligned(workspace, 8);
-  // fp32 x: the chunked form (workspace) or the small-image form
-  if (x_f32 && !chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  // fp32 x and dropout: the chunked form (workspace) or the small-image form
+  if ((x_f32 || drop_seed) && !chunked && HW > kSmallMaxHW)
+    return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  const int dst = gn_set_dropout(a, drop_seed, drop_p);
+  if (dst != DPA_OK) return dst;
   hipStream_t s = (hipStream_t)stream;
   if (chunked) {
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
@@ -1192,7 +1272,7 @@ extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma
                                   const float* film_shift, const void* film_wb, void* out,
                                   float* mean, float* rstd, void* workspace,
                                   int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
-                                  void* stream) {
+                                  const void* drop_seed, float drop_p, void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
   if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
@@ -1200,7 +1280,8 @@ extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma
   if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
   if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
   return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
-                eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32);
+                eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
+                drop_p);
 }
 
 // per-image channel partials of dgamma/dbeta, then (chunked form) the chunk sums
@@ -1219,7 +1300,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
                   const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
                   int64_t workspace_bytes, int N, int HW, int C, int G, void* stream,
-                  bool x_f32 = false) {
+                  bool x_f32 = false, const void* drop_seed = nullptr, float drop_p = 0.0f) {
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1250,7 +1331,10 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   const int nchunk = gn_chunks(HW);
   const bool chunked =
       nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16);
-  if (x_f32 && !chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  if ((x_f32 || drop_seed) && !chunked && HW > kSmallMaxHW)
+    return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  const int dst = gn_set_dropout(a, drop_seed, drop_p);
+  if (dst != DPA_OK) return dst;
   const bool film = a.fs || a.wb;
   int st = DPA_OK;
   if (chunked) {
@@ -1331,10 +1415,10 @@ extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, 
                                   const float* rstd, void* dx, float* dgamma, float* dbeta,
                                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb,
                                   void* workspace, int64_t workspace_bytes, int N, int HW, int C,
-                                  int G, void* stream) {
+                                  int G, const void* drop_seed, float drop_p, void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
   return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dx, dgamma,
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
-                stream, x_dtype == DPA_DTYPE_F32);
+                stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p);
 }

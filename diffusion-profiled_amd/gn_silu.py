@@ -63,8 +63,21 @@ def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
     return out, mean, rstd
 
 
-def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps):
-    """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32."""
+def dropout_ok(x: torch.Tensor) -> bool:
+    """Images whose GroupNorm+SiLU kernels also apply dropout (the chunked and small forms)."""
+    hw = x.shape[2] * x.shape[3]
+    return hw <= 128 or 256 <= hw <= 64 * 128
+
+
+def new_dropout_seed(device) -> torch.Tensor:
+    """A fresh dropout seed in device memory, drawn from torch's generator (so it follows
+    torch.manual_seed and is redrawn on each replay of a captured graph)."""
+    return torch.randint(0, 2**62, (1,), device=device, dtype=torch.int64)
+
+
+def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0):
+    """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32;
+    seed: dropout seed tensor (int64 [1]) or None."""
     n, c, h, w = x.shape
     ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
@@ -74,7 +87,7 @@ def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps):
         "dpa_gn_silu_fwd_ex",
         x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
         mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c, groups, float(eps),
-        _stream(x),
+        p(seed), float(p_drop), _stream(x),
     )
 
 
@@ -102,7 +115,7 @@ def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_
         x.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
         beta.float().contiguous().data_ptr(), p(fs), p(fb), None, mean.data_ptr(),
         rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs), p(dfb), None,
-        ws.data_ptr(), ws_bytes, n, h * w, c, groups, _stream(x),
+        ws.data_ptr(), ws_bytes, n, h * w, c, groups, None, 0.0, _stream(x),
     )
     return dx, dgamma, dbeta, dfs, dfb
 
@@ -139,10 +152,12 @@ class GroupNormSiLU(torch.autograd.Function):
 class GroupNormSiLUFilm(torch.autograd.Function):
     """silu(bf16(w + 1) * GroupNorm(x) + b) with (w, b) = chunk(film_wb, 2, dim=1), the time
     projection of diffusion/unet.py:157-159, read by the kernel in bf16; the backward returns
-    the gradient of film_wb [N, 2C, 1, 1] (bf16) directly."""
+    the gradient of film_wb [N, 2C, 1, 1] (bf16) directly. With p_drop > 0 the output also
+    takes the dropout of diffusion/unet.py:160 (mask from a counter hash of a seed drawn here;
+    the backward recomputes it from the same seed)."""
 
     @staticmethod
-    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb):
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0):
         n, c, h, w = x.shape
         xb, _ = _prep_x(x)
         wb = film_wb.contiguous()
@@ -151,16 +166,20 @@ class GroupNormSiLUFilm(torch.autograd.Function):
         mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
-        _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps)
+        seed = new_dropout_seed(x.device) if p_drop > 0.0 else None
+        if seed is not None and not dropout_ok(x):
+            raise ValueError(f"fused dropout: no kernel form for {h}x{w} images")
+        _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps, seed, p_drop)
         ctx.groups = groups
         ctx.x_dtype = x.dtype
         ctx.wb_shape = film_wb.shape
-        ctx.save_for_backward(xb, gamma, beta, mean, rstd, wb)
+        ctx.p_drop = p_drop
+        ctx.save_for_backward(xb, gamma, beta, mean, rstd, wb, seed)
         return out
 
     @staticmethod
     def backward(ctx: Any, dout):
-        xb, gamma, beta, mean, rstd, wb = ctx.saved_tensors
+        xb, gamma, beta, mean, rstd, wb, seed = ctx.saved_tensors
         n, c, h, w = xb.shape
         dout = dout.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
         dx = torch.empty_like(xb, memory_format=torch.channels_last)
@@ -175,13 +194,15 @@ class GroupNormSiLUFilm(torch.autograd.Function):
             xb.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
             beta.float().contiguous().data_ptr(), None, None, wb.data_ptr(), mean.data_ptr(),
             rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), None, None,
-            dwb.data_ptr(), ws.data_ptr(), ws_bytes, n, h * w, c, ctx.groups, _stream(xb),
+            dwb.data_ptr(), ws.data_ptr(), ws_bytes, n, h * w, c, ctx.groups,
+            None if seed is None else seed.data_ptr(), float(ctx.p_drop), _stream(xb),
         )
-        return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, dwb
+        return (dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, dwb,
+                None)
 
 
-def group_norm_silu_film(x, gamma, beta, groups: int, eps: float, film_wb):
-    return GroupNormSiLUFilm.apply(x, gamma, beta, groups, eps, film_wb)
+def group_norm_silu_film(x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0):
+    return GroupNormSiLUFilm.apply(x, gamma, beta, groups, eps, film_wb, float(p_drop))
 
 
 def group_norm_silu(x, gamma, beta, groups: int, eps: float = 1e-5, film_scale=None, film_shift=None):

@@ -35,6 +35,7 @@ from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
 from .residual import downsample2, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
+from .gn_silu import dropout_ok as gn_dropout_ok
 from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
 
 
@@ -253,15 +254,17 @@ class ResidualBlock(nn.Module):
         resid = x
         x = self.conv_1(norm_silu(self.norm1, x, self.fused))
         wb = self.t_embed_wb(t)
+        p_drop = self.dropout.p if self.training else 0.0
         if (self.fused and _on_gpu(x) and wb.dtype == torch.bfloat16
-                and gn_supported(x.shape[1], self.norm2.num_groups)):
-            # the kernel reads (w, b) from wb and forms bf16(w + 1) itself
+                and gn_supported(x.shape[1], self.norm2.num_groups)
+                and (p_drop == 0.0 or gn_dropout_ok(x))):
+            # the kernel reads (w, b) from wb, forms bf16(w + 1) itself and applies the dropout
             h = group_norm_silu_film(x, self.norm2.weight, self.norm2.bias,
-                                     self.norm2.num_groups, self.norm2.eps, wb)
+                                     self.norm2.num_groups, self.norm2.eps, wb, p_drop)
         else:
             w, b = torch.chunk(wb, chunks=2, dim=1)
-            h = norm_silu(self.norm2, x, self.fused, w + 1, b)
-        x = self.conv_2(self.dropout(h))
+            h = self.dropout(norm_silu(self.norm2, x, self.fused, w + 1, b))
+        x = self.conv_2(h)
         return residual_join(self.skip_connection(resid), x)
 
 

@@ -246,18 +246,24 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * input gradient; with DPA_DTYPE_F32 the kernels read the fp32 x as it is and write dx in
  * fp32 (the output y stays bf16). fp32 x takes the chunked form (images of 256+ pixels, a
  * workspace of the *_workspace_bytes size) or the small-image form (<= 128 pixels); other
- * sizes return DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE. */
+ * sizes return DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE.
+ * Optional dropout of the output (diffusion/unet.py:160, nn.Dropout(p) before conv_2):
+ * drop_seed = a uint64 in device memory, NULL for none; an element is kept when its 32-bit
+ * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
+ * for even idx, the high half for odd idx) is >= p * 2^32, and kept values are scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
+ * reference drops the fp32 SiLU output). The backward recomputes the mask from the same seed
+ * and p. Dropout takes the chunked or small-image form as fp32 x does; 0 <= p < 1. */
 int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
                        const float* film_scale, const float* film_shift, const void* film_wb,
                        void* out, float* mean, float* rstd, void* workspace,
                        int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
-                       void* stream);
+                       const void* drop_seed, float drop_p, void* stream);
 int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
                        const float* beta, const float* film_scale, const float* film_shift,
                        const void* film_wb, const float* mean, const float* rstd, void* dx,
                        float* dgamma, float* dbeta, float* dfilm_scale, float* dfilm_shift,
                        void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N, int HW,
-                       int C, int G, void* stream);
+                       int C, int G, const void* drop_seed, float drop_p, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Grouped FP8 weight preparation. No single counterpart in the reference: it performs, for a

@@ -229,11 +229,44 @@ def _gn_input_f64(x: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(x).astype(np.float64)
 
 
+def splitmix64(seed: int, idx: np.ndarray) -> np.ndarray:
+    """splitmix64 output for state seed + idx * 0x9E3779B97F4A7C15 (Steele, Lea and Flood,
+    "Fast splittable pseudorandom number generators", OOPSLA 2014; Vigna's finaliser
+    constants), uint64 with wrap-around."""
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & (2**64 - 1)) + idx.astype(np.uint64) * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def dropout_keep(seed: int, n: int, p: float) -> np.ndarray:
+    """Keep mask of the fused dropout over n elements (NHWC index order): element idx is kept
+    when its 32-bit half of splitmix64(seed, idx // 2) (the low half for even idx, the high
+    half for odd idx) is >= p * 2^32. The reference draws its mask from torch's Philox
+    generator (diffusion/unet.py:160 nn.Dropout), which no restatement reproduces; this mask
+    has the same keep probability 1 - p."""
+    keep_from = min(int(p * 4294967296.0), 0xFFFFFFFF)
+    idx = np.arange(n, dtype=np.uint64)
+    z = splitmix64(seed, idx >> np.uint64(1))
+    half = np.where((idx & np.uint64(1)) == 1, z >> np.uint64(32), z & np.uint64(0xFFFFFFFF))
+    return half >= np.uint64(keep_from)
+
+
+def dropout_scale(p: float) -> np.float32:
+    """1 / (1 - p) as torch's dropout kernel forms it: 1 - p rounded to fp32, its reciprocal
+    taken in double and rounded to fp32."""
+    return np.float32(1.0 / float(np.float32(1.0 - p)))
+
+
 def gn_silu_fwd(x_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups: int,
                 eps: float = 1e-5, film_scale: np.ndarray | None = None,
-                film_shift: np.ndarray | None = None) -> np.ndarray:
+                film_shift: np.ndarray | None = None, drop: tuple[int, float] | None = None
+                ) -> np.ndarray:
     """bf16( silu( [fs *] GroupNorm(x) [+ fb] ) ) evaluated in float64, then rounded to fp32
-    and bf16. x NHWC bf16 bits or fp32 values; gamma/beta fp32 [C]; film [N, C]. Returns NHWC
+    and bf16. x NHWC bf16 bits or fp32 values; gamma/beta fp32 [C]; film [N, C]; drop =
+    (seed, p): the fp32 SiLU output is dropped or scaled by dropout_scale(p) in fp32 before the
+    bf16 rounding (dropout on autocast's fp32 SiLU output, diffusion/unet.py:160). Returns NHWC
     bf16 bits."""
     x = torch.from_numpy(_gn_input_f64(x_bits)).permute(0, 3, 1, 2)
     z = F.group_norm(x, groups, torch.from_numpy(gamma.astype(np.float64)),
@@ -243,14 +276,18 @@ def gn_silu_fwd(x_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups:
         fb = torch.from_numpy(film_shift.astype(np.float64))[:, :, None, None]
         z = fs * z + fb
     out = F.silu(z).permute(0, 2, 3, 1).contiguous().numpy().astype(np.float32)
+    if drop is not None:
+        keep = dropout_keep(drop[0], out.size, drop[1]).reshape(out.shape)
+        out = np.where(keep, out * dropout_scale(drop[1]), np.float32(0.0)).astype(np.float32)
     return f32_to_bf16_bits(out)
 
 
 def gn_silu_bwd(x_bits: np.ndarray, dout_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray,
                 groups: int, eps: float = 1e-5, film_scale: np.ndarray | None = None,
-                film_shift: np.ndarray | None = None):
-    """Autograd of gn_silu_fwd in float64 (x as there). Returns (dx NHWC float64, dgamma,
-    dbeta, dfilm_scale [N,C] | None, dfilm_shift | None)."""
+                film_shift: np.ndarray | None = None, drop: tuple[int, float] | None = None):
+    """Autograd of gn_silu_fwd in float64 (x and drop as there: the incoming gradient is
+    masked and scaled in fp32 first). Returns (dx NHWC float64, dgamma, dbeta, dfilm_scale
+    [N,C] | None, dfilm_shift | None)."""
     x = torch.from_numpy(_gn_input_f64(x_bits)).permute(0, 3, 1, 2)
     x.requires_grad_(True)
     g = torch.from_numpy(gamma.astype(np.float64)).requires_grad_(True)
@@ -262,7 +299,11 @@ def gn_silu_bwd(x_bits: np.ndarray, dout_bits: np.ndarray, gamma: np.ndarray, be
         fb = torch.from_numpy(film_shift.astype(np.float64)).requires_grad_(True)
         z = fs[:, :, None, None] * z + fb[:, :, None, None]
     out = F.silu(z)
-    d = torch.from_numpy(bf16_bits_to_f32(dout_bits).astype(np.float64)).permute(0, 3, 1, 2)
+    d32 = bf16_bits_to_f32(dout_bits)
+    if drop is not None:
+        keep = dropout_keep(drop[0], d32.size, drop[1]).reshape(d32.shape)
+        d32 = np.where(keep, d32 * dropout_scale(drop[1]), np.float32(0.0)).astype(np.float32)
+    d = torch.from_numpy(d32.astype(np.float64)).permute(0, 3, 1, 2)
     out.backward(d)
     dx = x.grad.permute(0, 2, 3, 1).contiguous().numpy()
     res = [dx, g.grad.numpy(), b.grad.numpy()]

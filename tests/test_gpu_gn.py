@@ -325,3 +325,88 @@ def test_gn_silu_fp32_autograd_and_fallback(G):
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
     assert xr.grad.dtype == torch.float32 and torch.equal(xr.grad, x2.grad)
+
+
+DROP_CASES = [
+    # (n, c, h, w, x fp32): chunked (bf16 and fp32 x) and small-image forms
+    (2, 128, 32, 32, True),
+    (3, 256, 16, 16, False),
+    (2, 512, 8, 8, True),
+    (4, 256, 4, 4, False),
+]
+
+
+@pytest.mark.parametrize("n,c,h,w,x32", DROP_CASES, ids=lambda v: str(v))
+def test_gn_silu_film_dropout_vs_oracle(G, n, c, h, w, x32):
+    """The dropout of diffusion/unet.py:160 fused into GroupNormSiLUFilm: the mask is the
+    oracle's splitmix64 mask of the seed the op draws (reproduced from the same torch CUDA
+    generator state), kept values are scaled by RN32(1 / RN32(1 - p)) in fp32 before the bf16
+    rounding; the backward recomputes the mask. Forward within one bf16 ulp of the float64
+    oracle, exact zeros off the mask, keep rate within 5 sigma of 1 - p; gradients against
+    the oracle's masked backward."""
+    p = 0.2
+    seed = n * 977 + c + h
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((n, c, h, w), generator=g) * 2.0 + 0.5
+    if not x32:
+        x = x.to(torch.bfloat16)
+    gamma, beta, _, _ = params(c, n, seed + 2, False)
+    wb = (0.3 * torch.randn((n, 2 * c, 1, 1), generator=g)).to(torch.bfloat16)
+    dout = randn_bf16((n, c, h, w), seed=seed + 1, std=1e-2)
+
+    torch.cuda.manual_seed(seed)
+    drop_seed = int(G.new_dropout_seed("cuda").item())
+    torch.cuda.manual_seed(seed)
+    xd = cl(x).requires_grad_()
+    gd, bd = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    wbd = wb.cuda().requires_grad_()
+    y = G.group_norm_silu_film(xd, gd, bd, GROUPS, 1e-5, wbd, p)
+    y.backward(cl(dout))
+    torch.cuda.synchronize()
+
+    x_nhwc = (x.float() if x32 else x).permute(0, 2, 3, 1).contiguous()
+    x_in = x_nhwc.numpy() if x32 else nhwc_bits(x)
+    wb32 = wb.float().reshape(n, 2 * c)
+    fs = (wb32[:, :c].to(torch.bfloat16).float() + 1).to(torch.bfloat16).float().numpy()
+    fb = wb32[:, c:].numpy()
+    keep = O.dropout_keep(drop_seed, n * h * w * c, p)
+    rate = keep.mean()
+    assert abs(rate - (1 - p)) < 5 * np.sqrt(p * (1 - p) / keep.size), rate
+    ref = O.gn_silu_fwd(x_in, gamma.numpy(), beta.numpy(), GROUPS, 1e-5, fs, fb, drop=(drop_seed, p))
+    got = nhwc_bits(y.detach().cpu())
+    assert (got.reshape(-1)[~keep] == 0).all()
+    assert_fwd_close(got, ref, f"dropout fwd {(n, c, h, w, x32)}")
+    rdx, rdg, rdb, rdfs, rdfb = O.gn_silu_bwd(x_in, nhwc_bits(dout), gamma.numpy(), beta.numpy(),
+                                             GROUPS, 1e-5, fs, fb, drop=(drop_seed, p))
+    # without the mask the gradient would be far off
+    rdx0 = O.gn_silu_bwd(x_in, nhwc_bits(dout), gamma.numpy(), beta.numpy(), GROUPS, 1e-5, fs, fb)[0]
+    assert rel(rdx0, rdx) > 0.1
+    got_dx = xd.grad.float().permute(0, 2, 3, 1).contiguous().cpu().numpy()
+    assert xd.grad.dtype == x.dtype
+    assert rel(got_dx, rdx) < (2e-5 if x32 else 4e-3), rel(got_dx, rdx)
+    assert rel(gd.grad.cpu().numpy(), rdg) < 1e-4
+    assert rel(bd.grad.cpu().numpy(), rdb) < 1e-4
+    dwb = wbd.grad.float().reshape(n, 2 * c).cpu().numpy()
+    assert rel(dwb[:, :c], rdfs) < 4e-3
+    assert rel(dwb[:, c:], rdfb) < 4e-3
+
+
+def test_gn_silu_film_dropout_zero_p_and_fresh_masks(G):
+    """p = 0 gives the undropped op bit for bit; two calls draw two seeds (different masks);
+    a size without a dropout form (12 x 12) is refused rather than silently undropped."""
+    n, c, h, w = 2, 256, 16, 16
+    g = torch.Generator().manual_seed(5)
+    x = cl((torch.randn((n, c, h, w), generator=g) + 0.5).to(torch.bfloat16))
+    gamma, beta, _, _ = params(c, n, 6, False)
+    wb = (0.3 * torch.randn((n, 2 * c, 1, 1), generator=g)).to(torch.bfloat16).cuda()
+    a = G.group_norm_silu_film(x, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.0)
+    b = G.group_norm_silu_film(x, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb)
+    assert torch.equal(a, b)
+    d1 = G.group_norm_silu_film(x, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)
+    d2 = G.group_norm_silu_film(x, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)
+    z1, z2 = (d1 == 0) & (a != 0), (d2 == 0) & (a != 0)
+    assert 0.45 < z1.float().mean().item() < 0.55
+    assert not torch.equal(z1, z2)
+    x12 = cl(torch.randn((n, c, 12, 12), generator=g).to(torch.bfloat16))
+    with pytest.raises(ValueError):
+        G.group_norm_silu_film(x12, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)

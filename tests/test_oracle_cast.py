@@ -180,3 +180,18 @@ def test_planted_mistakes_are_caught(bad_cast):
             caught = True
             break
     assert caught
+
+
+def test_dropout_hash_known_answers_and_rate():
+    """The fused dropout's hash is splitmix64: with seed 0 the state seed + idx * golden gamma
+    at idx = 1, 2, 3, 4 gives the published first outputs of splitmix64 seeded with 0; the keep
+    rate is 1 - p; the scale is torch's RN32(1 / RN32(1 - p))."""
+    got = O.splitmix64(0, np.arange(1, 5, dtype=np.uint64))
+    assert [int(v) for v in got] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                     0x06C45D188009454F, 0xF88BB8A8724C81EC]
+    for p in (0.1, 0.2, 0.5):
+        keep = O.dropout_keep(987654321, 1 << 18, p)
+        assert abs(keep.mean() - (1 - p)) < 5 * np.sqrt(p * (1 - p) / keep.size)
+    assert O.dropout_keep(7, 1000, 0.0).all()
+    assert O.dropout_scale(0.2) == np.float32(1.25)
+    assert O.dropout_scale(0.1) == np.float32(1.0) / np.float32(0.9)
