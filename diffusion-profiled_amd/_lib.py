@@ -127,7 +127,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "dpa_gn_silu_bwd_ex": (
         c_int,
-        [c_void_p, c_int] + [c_void_p] * 15 + [c_int64] + [c_int] * 4 + [c_void_p, c_float, c_void_p],
+        [c_void_p, c_int] + [c_void_p] * 16 + [c_int64] + [c_int] * 4 + [c_void_p, c_float, c_void_p],
     ),
 }
 

@@ -48,6 +48,7 @@ struct GnArgs {
   const uint64_t* drop_seed;  // dropout after the SiLU: seed in device memory, or null
   uint32_t drop_keep;         // keep an element when its hash is >= this (p * 2^32)
   float drop_scale;           // RN32(1 / (1 - p))
+  const void* dx_add;  // bwd: a gradient in x's type added to dx (chunked and small forms), or null
   int N, HW, C, G, cpg;
   float eps;
 };
@@ -530,16 +531,42 @@ __device__ __forceinline__ void unpack_x(const uint4 (&v)[NL][kChU], int u, floa
 // dx of 8 channels at element offset off, in x's type; dx(e) gives channel e's value
 template <bool kF32, typename F>
 __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
+  // with dx_add: dx + add as torch's gradient accumulation forms it (one fp32 add; in bf16 the
+  // sum of the two bf16 gradients, rounded once more)
+  const bool add = p.dx_add != nullptr;
   if constexpr (kF32) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = dx(e);
+    if (add) {
+      const float* a = static_cast<const float*>(p.dx_add) + off;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 w = *reinterpret_cast<const uint4*>(a + 4 * h);
+        v[4 * h] += __uint_as_float(w.x);
+        v[4 * h + 1] += __uint_as_float(w.y);
+        v[4 * h + 2] += __uint_as_float(w.z);
+        v[4 * h + 3] += __uint_as_float(w.w);
+      }
+    }
     float* d = static_cast<float*>(p.out) + off;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-      st_nt16(d + 4 * h, uint4{__float_as_uint(dx(4 * h)), __float_as_uint(dx(4 * h + 1)),
-                               __float_as_uint(dx(4 * h + 2)), __float_as_uint(dx(4 * h + 3))});
+      st_nt16(d + 4 * h, uint4{__float_as_uint(v[4 * h]), __float_as_uint(v[4 * h + 1]),
+                               __float_as_uint(v[4 * h + 2]), __float_as_uint(v[4 * h + 3])});
   } else {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = dx(e);
+    if (add) {
+      float a[8];
+      unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.dx_add) + off), a);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(f32_to_bf16_bits(v[e]) << 16) + a[e];
+    }
     uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(dx(e)) | (f32_to_bf16_bits(dx(e + 1)) << 16);
+    for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
     st_nt16(static_cast<uint16_t*>(p.out) + off, uint4{o[0], o[1], o[2], o[3]});
   }
 }
@@ -1300,7 +1327,8 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
                   const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
                   int64_t workspace_bytes, int N, int HW, int C, int G, void* stream,
-                  bool x_f32 = false, const void* drop_seed = nullptr, float drop_p = 0.0f) {
+                  bool x_f32 = false, const void* drop_seed = nullptr, float drop_p = 0.0f,
+                  const void* dx_add = nullptr) {
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1331,8 +1359,10 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   const int nchunk = gn_chunks(HW);
   const bool chunked =
       nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16);
-  if ((x_f32 || drop_seed) && !chunked && HW > kSmallMaxHW)
+  if ((x_f32 || drop_seed || dx_add) && !chunked && HW > kSmallMaxHW)
     return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  if (!aligned(dx_add, 16)) return DPA_ERR_ALIGN;
+  a.dx_add = dx_add;
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
   const bool film = a.fs || a.wb;
@@ -1412,13 +1442,14 @@ extern "C" int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const 
 extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
                                   const float* beta, const float* film_scale,
                                   const float* film_shift, const void* film_wb, const float* mean,
-                                  const float* rstd, void* dx, float* dgamma, float* dbeta,
-                                  float* dfilm_scale, float* dfilm_shift, void* dfilm_wb,
-                                  void* workspace, int64_t workspace_bytes, int N, int HW, int C,
-                                  int G, const void* drop_seed, float drop_p, void* stream) {
+                                  const float* rstd, void* dx, const void* dx_add, float* dgamma,
+                                  float* dbeta, float* dfilm_scale, float* dfilm_shift,
+                                  void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N,
+                                  int HW, int C, int G, const void* drop_seed, float drop_p,
+                                  void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
   return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dx, dgamma,
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
-                stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p);
+                stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p, dx_add);
 }

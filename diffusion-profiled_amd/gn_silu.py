@@ -75,6 +75,33 @@ def new_dropout_seed(device) -> torch.Tensor:
     return torch.randint(0, 2**62, (1,), device=device, dtype=torch.int64)
 
 
+class DropoutSeeds:
+    """Seeds for the dropout layers of one forward pass, drawn by one randint launch (instead of
+    one per layer): the model fills it before its forward and clears it after; each fused
+    dropout takes the next seed, or draws its own when none is left."""
+
+    def __init__(self):
+        self.seeds: torch.Tensor | None = None
+        self.next = 0
+
+    def fill(self, device, count: int) -> None:
+        self.seeds = torch.randint(0, 2**62, (count,), device=device, dtype=torch.int64)
+        self.next = 0
+
+    def clear(self) -> None:
+        self.seeds, self.next = None, 0
+
+    def take(self, device) -> torch.Tensor:
+        s = self.seeds
+        if s is not None and self.next < s.numel() and s.device == torch.device(device):
+            self.next += 1
+            return s[self.next - 1:self.next]
+        return new_dropout_seed(device)
+
+
+DROPOUT_SEEDS = DropoutSeeds()
+
+
 def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0):
     """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32;
     seed: dropout seed tensor (int64 [1]) or None."""
@@ -91,9 +118,10 @@ def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=Non
     )
 
 
-def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None):
+def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None,
+                dx_add=None):
     """Returns (dx in x's dtype (bf16 or fp32), dgamma, dbeta, dfilm_scale [N,C] | None,
-    dfilm_shift | None)."""
+    dfilm_shift | None); dx_add (x's dtype, channels-last) is added to dx by the kernel."""
     n, c, h, w = x.shape
     x = x.contiguous(memory_format=torch.channels_last)
     dout = dout.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
@@ -114,8 +142,8 @@ def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_
         "dpa_gn_silu_bwd_ex",
         x.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
         beta.float().contiguous().data_ptr(), p(fs), p(fb), None, mean.data_ptr(),
-        rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs), p(dfb), None,
-        ws.data_ptr(), ws_bytes, n, h * w, c, groups, None, 0.0, _stream(x),
+        rstd.data_ptr(), dx.data_ptr(), p(dx_add), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs),
+        p(dfb), None, ws.data_ptr(), ws_bytes, n, h * w, c, groups, None, 0.0, _stream(x),
     )
     return dx, dgamma, dbeta, dfs, dfb
 
@@ -149,6 +177,39 @@ class GroupNormSiLU(torch.autograd.Function):
         return dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, gfs, gfb
 
 
+class GroupNormSiLUTee(torch.autograd.Function):
+    """(silu(GroupNorm(x)), x): the residual block's first norm and its skip input
+    (diffusion/unet.py:149-151). The backward adds the skip path's gradient of x into dx inside
+    the GroupNorm kernel instead of autograd's separate accumulation kernel (same sum, same
+    roundings)."""
+
+    @staticmethod
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float):
+        xb, _ = _prep_x(x)
+        out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps)
+        ctx.groups = groups
+        ctx.x_dtype = x.dtype
+        ctx.save_for_backward(xb, gamma, beta, mean, rstd)
+        return out, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx: Any, dout, dskip):
+        xb, gamma, beta, mean, rstd = ctx.saved_tensors
+        add = None
+        if dskip is not None and dskip.dtype == xb.dtype == ctx.x_dtype and dropout_ok(xb):
+            add = dskip.contiguous(memory_format=torch.channels_last)
+        dx, dgamma, dbeta, _, _ = gn_silu_bwd(xb, dout, gamma, beta, mean, rstd, ctx.groups,
+                                              dx_add=add)
+        dx = dx.to(ctx.x_dtype)
+        if dskip is not None and add is None:
+            dx = dx + dskip
+        return dx, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None
+
+
+def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5):
+    return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps)
+
+
 class GroupNormSiLUFilm(torch.autograd.Function):
     """silu(bf16(w + 1) * GroupNorm(x) + b) with (w, b) = chunk(film_wb, 2, dim=1), the time
     projection of diffusion/unet.py:157-159, read by the kernel in bf16; the backward returns
@@ -166,7 +227,7 @@ class GroupNormSiLUFilm(torch.autograd.Function):
         mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
-        seed = new_dropout_seed(x.device) if p_drop > 0.0 else None
+        seed = DROPOUT_SEEDS.take(x.device) if p_drop > 0.0 else None
         if seed is not None and not dropout_ok(x):
             raise ValueError(f"fused dropout: no kernel form for {h}x{w} images")
         _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps, seed, p_drop)
@@ -193,7 +254,7 @@ class GroupNormSiLUFilm(torch.autograd.Function):
             "dpa_gn_silu_bwd_ex",
             xb.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
             beta.float().contiguous().data_ptr(), None, None, wb.data_ptr(), mean.data_ptr(),
-            rstd.data_ptr(), dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), None, None,
+            rstd.data_ptr(), dx.data_ptr(), None, dgamma.data_ptr(), dbeta.data_ptr(), None, None,
             dwb.data_ptr(), ws.data_ptr(), ws_bytes, n, h * w, c, ctx.groups,
             None if seed is None else seed.data_ptr(), float(ctx.p_drop), _stream(xb),
         )

@@ -35,8 +35,9 @@ from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
 from .residual import downsample2, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
-from .gn_silu import dropout_ok as gn_dropout_ok
-from .gn_silu import group_norm_silu, group_norm_silu_film, supported as gn_supported
+from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok
+from .gn_silu import group_norm_silu, group_norm_silu_film, group_norm_silu_tee
+from .gn_silu import supported as gn_supported
 
 
 @dataclass
@@ -251,8 +252,14 @@ class ResidualBlock(nn.Module):
         torch.nn.init.zeros_(self.conv_2.conv.weight)
 
     def forward(self, x: torch.Tensor, t: torch.Tensor):
-        resid = x
-        x = self.conv_1(norm_silu(self.norm1, x, self.fused))
+        if (self.fused and _on_gpu(x) and gn_supported(x.shape[1], self.norm1.num_groups)
+                and gn_dropout_ok(x)):
+            # the skip input's gradient is accumulated inside the GroupNorm backward
+            h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias,
+                                           self.norm1.num_groups, self.norm1.eps)
+        else:
+            resid, h = x, norm_silu(self.norm1, x, self.fused)
+        x = self.conv_1(h)
         wb = self.t_embed_wb(t)
         p_drop = self.dropout.p if self.training else 0.0
         if (self.fused and _on_gpu(x) and wb.dtype == torch.bfloat16
@@ -487,9 +494,14 @@ class UNet(nn.Module):
 
     def forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
         plan = self._weight_prep(x)
+        n_drop = sum(1 for m in self.modules()
+                     if isinstance(m, ResidualBlock) and m.training and m.dropout.p > 0.0)
+        if n_drop and _on_gpu(x):
+            DROPOUT_SEEDS.fill(x.device, n_drop)
         try:
             return self._forward(x, t)
         finally:
+            DROPOUT_SEEDS.clear()
             if plan is not None:
                 plan.active = False
                 plan.x_cache.clear()

@@ -252,7 +252,11 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
  * for even idx, the high half for odd idx) is >= p * 2^32, and kept values are scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
  * reference drops the fp32 SiLU output). The backward recomputes the mask from the same seed
- * and p. Dropout takes the chunked or small-image form as fp32 x does; 0 <= p < 1. */
+ * and p. Dropout takes the chunked or small-image form as fp32 x does; 0 <= p < 1.
+ * dx_add (backward; x's dtype and layout, or NULL): a second gradient of x added to dx as
+ * autograd accumulates it (fp32: one add; bf16: bf16(dx) + add, rounded to bf16) — the skip
+ * path's gradient of the residual block input (diffusion/unet.py:149, :161), which x feeds
+ * besides norm1. Chunked or small-image form only; may alias dx. */
 int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
                        const float* film_scale, const float* film_shift, const void* film_wb,
                        void* out, float* mean, float* rstd, void* workspace,
@@ -261,9 +265,9 @@ int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const flo
 int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
                        const float* beta, const float* film_scale, const float* film_shift,
                        const void* film_wb, const float* mean, const float* rstd, void* dx,
-                       float* dgamma, float* dbeta, float* dfilm_scale, float* dfilm_shift,
-                       void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N, int HW,
-                       int C, int G, const void* drop_seed, float drop_p, void* stream);
+                       const void* dx_add, float* dgamma, float* dbeta, float* dfilm_scale,
+                       float* dfilm_shift, void* dfilm_wb, void* workspace,
+                       int64_t workspace_bytes, int N, int HW, int C, int G, const void* drop_seed, float drop_p, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Grouped FP8 weight preparation. No single counterpart in the reference: it performs, for a

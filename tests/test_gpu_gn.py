@@ -410,3 +410,34 @@ def test_gn_silu_film_dropout_zero_p_and_fresh_masks(G):
     x12 = cl(torch.randn((n, c, 12, 12), generator=g).to(torch.bfloat16))
     with pytest.raises(ValueError):
         G.group_norm_silu_film(x12, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)
+
+
+@pytest.mark.parametrize("n,c,h,w,x32", [(2, 128, 32, 32, True), (3, 256, 16, 16, False),
+                                         (2, 512, 8, 8, True), (4, 256, 4, 4, False),
+                                         (2, 128, 12, 12, True)], ids=lambda v: str(v))
+def test_gn_silu_tee_accumulates_skip_gradient(G, n, c, h, w, x32):
+    """GroupNormSiLUTee returns (silu(GroupNorm(x)), x); its backward adds the second output's
+    gradient into dx in the kernel. x's gradient equals autograd's own accumulation over the
+    unfused pair (GroupNormSiLU on x and x used again) bit for bit, in fp32 and bf16; 12 x 12
+    (no fused form) takes the separate add."""
+    seed = n + c + h + 31
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((n, c, h, w), generator=g) * 2.0 + 0.5
+    if not x32:
+        x = x.to(torch.bfloat16)
+    gamma, beta, _, _ = params(c, n, seed + 2, False)
+    g1 = cl(randn_bf16((n, c, h, w), seed=seed + 1, std=1e-2))
+    g2 = cl(torch.randn((n, c, h, w), generator=g).to(x.dtype))
+    xa = cl(x).requires_grad_()
+    ga, ba = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    ya, ra = G.group_norm_silu_tee(xa, ga, ba, GROUPS, 1e-5)
+    torch.autograd.backward([ya, ra], [g1, g2])
+    xb = cl(x).requires_grad_()
+    gb, bb = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    yb = G.group_norm_silu(xb, gb, bb, GROUPS, 1e-5)
+    torch.autograd.backward([yb, xb * 1], [g1, g2])
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb) and torch.equal(ra, xb)
+    assert xa.grad.dtype == x.dtype
+    assert torch.equal(xa.grad, xb.grad)
+    assert torch.equal(ga.grad, gb.grad) and torch.equal(ba.grad, bb.grad)
