@@ -123,11 +123,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_gn_silu_fwd_ex": (
         c_int,
         [c_void_p, c_int] + [c_void_p] * 9 + [c_int64] + [c_int] * 4
-        + [c_float, c_void_p, c_float, c_void_p],
+        + [c_float, c_void_p, c_float, c_void_p, c_void_p],
     ),
     "dpa_gn_silu_bwd_ex": (
         c_int,
-        [c_void_p, c_int] + [c_void_p] * 16 + [c_int64] + [c_int] * 4 + [c_void_p, c_float, c_void_p],
+        [c_void_p, c_int] + [c_void_p] * 10 + [c_int] + [c_void_p] * 6 + [c_int64] + [c_int] * 4
+        + [c_void_p, c_float, c_void_p],
     ),
 }
 

@@ -48,7 +48,9 @@ struct GnArgs {
   const uint64_t* drop_seed;  // dropout after the SiLU: seed in device memory, or null
   uint32_t drop_keep;         // keep an element when its hash is >= this (p * 2^32)
   float drop_scale;           // RN32(1 / (1 - p))
-  const void* dx_add;  // bwd: a gradient in x's type added to dx (chunked and small forms), or null
+  const void* dx_add;  // bwd: a gradient added to dx (chunked and small forms), or null
+  int dx_add_bf16;     // bwd: dx_add is bf16 while x and dx are fp32
+  uint16_t* x_bf16;    // fwd: fp32 x also written as bf16 here (chunked and small forms), or null
   int N, HW, C, G, cpg;
   float eps;
 };
@@ -538,7 +540,12 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = dx(e);
-    if (add) {
+    if (add && p.dx_add_bf16) {
+      float a[8];
+      unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.dx_add) + off), a);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += a[e];
+    } else if (add) {
       const float* a = static_cast<const float*>(p.dx_add) + off;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -569,6 +576,15 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
     for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
     st_nt16(static_cast<uint16_t*>(p.out) + off, uint4{o[0], o[1], o[2], o[3]});
   }
+}
+
+// fp32 x also stored rounded to bf16 (RNE), for a consumer that rounds it anyway (the residual
+// block's 1x1 skip conv), so no separate cast pass reads x again
+__device__ __forceinline__ void store_x_bf16(const GnArgs& p, int64_t off, const float (&f)[8]) {
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(f[e]) | (f32_to_bf16_bits(f[e + 1]) << 16);
+  st_nt16(p.x_bf16 + off, uint4{o[0], o[1], o[2], o[3]});
 }
 
 __device__ __forceinline__ int chunk_pixels(int HW, int chunk) {
@@ -711,6 +727,9 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   for (int u = 0; u < kChU; ++u) {
     float f[8];
     unpack_x<kF32>(v, u, f);
+    if constexpr (kF32) {
+      if (p.x_bf16 && ok[u]) store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f);
+    }
     const uint32_t kb =
         drop ? drop_keep8(seed, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, p.drop_keep) : 0u;
     uint32_t o[4];
@@ -969,6 +988,13 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   float f[kChU][8];
 #pragma unroll
   for (int u = 0; u < kChU; ++u) unpack_x<kF32>(v, u, f[u]);
+  if constexpr (kF32) {
+    if (p.x_bf16) {
+#pragma unroll
+      for (int u = 0; u < kChU; ++u)
+        if (ok[u]) store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f[u]);
+    }
+  }
   float sm[2] = {0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < kChU; ++u)
@@ -1196,7 +1222,7 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
                   const float* film_shift, const void* film_wb, void* out, float* mean,
                   float* rstd, int N, int HW, int C, int G, float eps, void* stream,
                   void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false,
-                  const void* drop_seed = nullptr, float drop_p = 0.0f) {
+                  const void* drop_seed = nullptr, float drop_p = 0.0f, void* x_bf16 = nullptr) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
@@ -1218,6 +1244,9 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   // fp32 x and dropout: the chunked form (workspace) or the small-image form
   if ((x_f32 || drop_seed) && !chunked && HW > kSmallMaxHW)
     return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+  if (x_bf16 && !x_f32) return DPA_ERR_SHAPE;  // the bf16 copy is of an fp32 x
+  if (!aligned(x_bf16, 16)) return DPA_ERR_ALIGN;
+  a.x_bf16 = (uint16_t*)x_bf16;
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
   hipStream_t s = (hipStream_t)stream;
@@ -1299,7 +1328,8 @@ extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma
                                   const float* film_shift, const void* film_wb, void* out,
                                   float* mean, float* rstd, void* workspace,
                                   int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
-                                  const void* drop_seed, float drop_p, void* stream) {
+                                  const void* drop_seed, float drop_p, void* x_bf16,
+                                  void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
   if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
@@ -1308,7 +1338,7 @@ extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma
   if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
   return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
                 eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
-                drop_p);
+                drop_p, x_bf16);
 }
 
 // per-image channel partials of dgamma/dbeta, then (chunked form) the chunk sums
@@ -1328,7 +1358,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
                   int64_t workspace_bytes, int N, int HW, int C, int G, void* stream,
                   bool x_f32 = false, const void* drop_seed = nullptr, float drop_p = 0.0f,
-                  const void* dx_add = nullptr) {
+                  const void* dx_add = nullptr, bool dx_add_bf16 = false) {
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1363,6 +1393,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
     return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
   if (!aligned(dx_add, 16)) return DPA_ERR_ALIGN;
   a.dx_add = dx_add;
+  a.dx_add_bf16 = x_f32 && dx_add_bf16;
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
   const bool film = a.fs || a.wb;
@@ -1442,7 +1473,8 @@ extern "C" int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const 
 extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
                                   const float* beta, const float* film_scale,
                                   const float* film_shift, const void* film_wb, const float* mean,
-                                  const float* rstd, void* dx, const void* dx_add, float* dgamma,
+                                  const float* rstd, void* dx, const void* dx_add,
+                                  int dx_add_dtype, float* dgamma,
                                   float* dbeta, float* dfilm_scale, float* dfilm_shift,
                                   void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N,
                                   int HW, int C, int G, const void* drop_seed, float drop_p,
@@ -1451,5 +1483,6 @@ extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, 
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
   return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dx, dgamma,
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
-                stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p, dx_add);
+                stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p, dx_add,
+                dx_add_dtype == DPA_DTYPE_BF16);
 }

@@ -46,8 +46,9 @@ def supported(c: int, groups: int) -> bool:
     return cpg >= 4 and 64 % cpg == 0
 
 
-def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
-    """Returns (out bf16 channels-last, mean [N*G], rstd [N*G])."""
+def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None, x_bf16=None):
+    """Returns (out bf16 channels-last, mean [N*G], rstd [N*G]); with x_bf16 (fp32 x) the
+    kernel also writes bf16(x) there."""
     n, c, h, w = x.shape
     x, _ = _prep_x(x)
     out = torch.empty_like(x, dtype=torch.bfloat16, memory_format=torch.channels_last)
@@ -59,7 +60,7 @@ def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None):
     if film_scale is not None:
         fs = film_scale.float().reshape(n, c).contiguous()
         fb = film_shift.float().reshape(n, c).contiguous()
-    _fwd_call(x, gamma, beta, fs, fb, None, out, mean, rstd, groups, eps)
+    _fwd_call(x, gamma, beta, fs, fb, None, out, mean, rstd, groups, eps, x_bf16=x_bf16)
     return out, mean, rstd
 
 
@@ -102,7 +103,8 @@ class DropoutSeeds:
 DROPOUT_SEEDS = DropoutSeeds()
 
 
-def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0):
+def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0,
+              x_bf16=None):
     """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32;
     seed: dropout seed tensor (int64 [1]) or None."""
     n, c, h, w = x.shape
@@ -114,7 +116,7 @@ def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=Non
         "dpa_gn_silu_fwd_ex",
         x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
         mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c, groups, float(eps),
-        p(seed), float(p_drop), _stream(x),
+        p(seed), float(p_drop), p(x_bf16), _stream(x),
     )
 
 
@@ -142,7 +144,9 @@ def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_
         "dpa_gn_silu_bwd_ex",
         x.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
         beta.float().contiguous().data_ptr(), p(fs), p(fb), None, mean.data_ptr(),
-        rstd.data_ptr(), dx.data_ptr(), p(dx_add), dgamma.data_ptr(), dbeta.data_ptr(), p(dfs),
+        rstd.data_ptr(), dx.data_ptr(), p(dx_add),
+        DTYPE_BF16 if dx_add is not None and dx_add.dtype == torch.bfloat16 else DTYPE_F32,
+        dgamma.data_ptr(), dbeta.data_ptr(), p(dfs),
         p(dfb), None, ws.data_ptr(), ws_bytes, n, h * w, c, groups, None, 0.0, _stream(x),
     )
     return dx, dgamma, dbeta, dfs, dfb
@@ -181,33 +185,42 @@ class GroupNormSiLUTee(torch.autograd.Function):
     """(silu(GroupNorm(x)), x): the residual block's first norm and its skip input
     (diffusion/unet.py:149-151). The backward adds the skip path's gradient of x into dx inside
     the GroupNorm kernel instead of autograd's separate accumulation kernel (same sum, same
-    roundings)."""
+    roundings). With skip_bf16 and an fp32 x the second output is x.to(bfloat16), written by
+    the GroupNorm kernel as it reads x (what the 1x1 skip conv rounds its input to), and its
+    bf16 gradient is added to the fp32 dx as autograd would (cast, then one fp32 add)."""
 
     @staticmethod
-    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float):
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, skip_bf16: bool = False):
         xb, _ = _prep_x(x)
-        out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps)
+        x16 = None
+        if skip_bf16 and xb.dtype == torch.float32 and dropout_ok(xb):
+            x16 = torch.empty_like(xb, dtype=torch.bfloat16, memory_format=torch.channels_last)
+        out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps, x_bf16=x16)
         ctx.groups = groups
         ctx.x_dtype = x.dtype
         ctx.save_for_backward(xb, gamma, beta, mean, rstd)
-        return out, x.view_as(x)
+        if x16 is not None:
+            return out, x16
+        return out, (x.to(torch.bfloat16) if skip_bf16 else x.view_as(x))
 
     @staticmethod
     def backward(ctx: Any, dout, dskip):
         xb, gamma, beta, mean, rstd = ctx.saved_tensors
         add = None
-        if dskip is not None and dskip.dtype == xb.dtype == ctx.x_dtype and dropout_ok(xb):
+        if (dskip is not None and xb.dtype == ctx.x_dtype and dropout_ok(xb)
+                and (dskip.dtype == xb.dtype
+                     or (dskip.dtype == torch.bfloat16 and xb.dtype == torch.float32))):
             add = dskip.contiguous(memory_format=torch.channels_last)
         dx, dgamma, dbeta, _, _ = gn_silu_bwd(xb, dout, gamma, beta, mean, rstd, ctx.groups,
                                               dx_add=add)
         dx = dx.to(ctx.x_dtype)
         if dskip is not None and add is None:
-            dx = dx + dskip
-        return dx, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None
+            dx = dx + dskip.to(dx.dtype)
+        return dx, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, None
 
 
-def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5):
-    return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps)
+def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5, skip_bf16: bool = False):
+    return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps, skip_bf16)
 
 
 class GroupNormSiLUFilm(torch.autograd.Function):
@@ -254,7 +267,8 @@ class GroupNormSiLUFilm(torch.autograd.Function):
             "dpa_gn_silu_bwd_ex",
             xb.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
             beta.float().contiguous().data_ptr(), None, None, wb.data_ptr(), mean.data_ptr(),
-            rstd.data_ptr(), dx.data_ptr(), None, dgamma.data_ptr(), dbeta.data_ptr(), None, None,
+            rstd.data_ptr(), dx.data_ptr(), None, DTYPE_BF16, dgamma.data_ptr(),
+            dbeta.data_ptr(), None, None,
             dwb.data_ptr(), ws.data_ptr(), ws_bytes, n, h * w, c, ctx.groups,
             None if seed is None else seed.data_ptr(), float(ctx.p_drop), _stream(xb),
         )

@@ -255,8 +255,12 @@ class ResidualBlock(nn.Module):
         if (self.fused and _on_gpu(x) and gn_supported(x.shape[1], self.norm1.num_groups)
                 and gn_dropout_ok(x)):
             # the skip input's gradient is accumulated inside the GroupNorm backward
+            # a 1x1 skip conv rounds its input to bf16 (FP8 path or autocast); the kernel
+            # writes that copy as it reads x
+            skip16 = (isinstance(self.skip_connection, Conv1x1FP8)
+                      and torch.is_autocast_enabled("cuda"))
             h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias,
-                                           self.norm1.num_groups, self.norm1.eps)
+                                           self.norm1.num_groups, self.norm1.eps, skip16)
         else:
             resid, h = x, norm_silu(self.norm1, x, self.fused)
         x = self.conv_1(h)

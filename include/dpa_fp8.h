@@ -256,16 +256,20 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * dx_add (backward; x's dtype and layout, or NULL): a second gradient of x added to dx as
  * autograd accumulates it (fp32: one add; bf16: bf16(dx) + add, rounded to bf16) — the skip
  * path's gradient of the residual block input (diffusion/unet.py:149, :161), which x feeds
- * besides norm1. Chunked or small-image form only; may alias dx. */
+ * besides norm1; dx_add_dtype DPA_DTYPE_BF16 with an fp32 x adds a bf16 gradient (autograd's
+ * fp32 cast of it, then one fp32 add). Chunked or small-image form only; may alias dx.
+ * x_bf16 (forward, fp32 x only, or NULL): also writes x rounded to bf16 (RNE) there — the
+ * input the 1x1 skip conv rounds to anyway — so no separate cast pass reads x again. */
 int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
                        const float* film_scale, const float* film_shift, const void* film_wb,
                        void* out, float* mean, float* rstd, void* workspace,
                        int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
-                       const void* drop_seed, float drop_p, void* stream);
+                       const void* drop_seed, float drop_p, void* x_bf16, void* stream);
 int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float* gamma,
                        const float* beta, const float* film_scale, const float* film_shift,
                        const void* film_wb, const float* mean, const float* rstd, void* dx,
-                       const void* dx_add, float* dgamma, float* dbeta, float* dfilm_scale,
+                       const void* dx_add, int dx_add_dtype, float* dgamma, float* dbeta,
+                       float* dfilm_scale,
                        float* dfilm_shift, void* dfilm_wb, void* workspace,
                        int64_t workspace_bytes, int N, int HW, int C, int G, const void* drop_seed, float drop_p, void* stream);
 

@@ -441,3 +441,36 @@ def test_gn_silu_tee_accumulates_skip_gradient(G, n, c, h, w, x32):
     assert xa.grad.dtype == x.dtype
     assert torch.equal(xa.grad, xb.grad)
     assert torch.equal(ga.grad, gb.grad) and torch.equal(ba.grad, bb.grad)
+
+
+@pytest.mark.parametrize("n,c,h,w,x32", [(2, 128, 32, 32, True), (2, 512, 8, 8, True),
+                                         (3, 256, 16, 16, False), (2, 128, 12, 12, True)],
+                         ids=lambda v: str(v))
+def test_gn_silu_tee_bf16_skip_copy(G, n, c, h, w, x32):
+    """With skip_bf16 the tee's second output is x.to(bfloat16) (written by the GroupNorm kernel
+    for an fp32 x) and its bf16 gradient is accumulated into x's gradient as autograd does for
+    the unfused pair (GroupNormSiLU on x, x.to(bfloat16) for the skip): outputs and all
+    gradients bit-identical."""
+    seed = n + c + h + 57
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((n, c, h, w), generator=g) * 2.0 + 0.5
+    if not x32:
+        x = x.to(torch.bfloat16)
+    gamma, beta, _, _ = params(c, n, seed + 2, False)
+    g1 = cl(randn_bf16((n, c, h, w), seed=seed + 1, std=1e-2))
+    g2 = cl(randn_bf16((n, c, h, w), seed=seed + 3, std=1e-1))
+    xa = cl(x).requires_grad_()
+    ga, ba = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    ya, ra = G.group_norm_silu_tee(xa, ga, ba, GROUPS, 1e-5, True)
+    torch.autograd.backward([ya, ra], [g1, g2])
+    xb = cl(x).requires_grad_()
+    gb, bb = gamma.cuda().requires_grad_(), beta.cuda().requires_grad_()
+    yb = G.group_norm_silu(xb, gb, bb, GROUPS, 1e-5)
+    rb = xb.to(torch.bfloat16)
+    torch.autograd.backward([yb, rb], [g1, g2])
+    torch.cuda.synchronize()
+    assert ra.dtype == torch.bfloat16
+    assert torch.equal(ya, yb) and torch.equal(ra, rb)
+    assert xa.grad.dtype == x.dtype
+    assert torch.equal(xa.grad, xb.grad)
+    assert torch.equal(ga.grad, gb.grad) and torch.equal(ba.grad, bb.grad)
