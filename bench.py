@@ -445,7 +445,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU scaling is not "
-                                   "measured (see DESIGN.md for how the path would shard)",
+                                   "measured; the path would shard by data parallelism, one "
+                                   "process per GPU, gradients all-reduced over RCCL",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     K = importlib.import_module("diffusion-profiled_amd.fp8_kernels")
