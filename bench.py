@@ -386,13 +386,35 @@ def time_part(fn, reps):
     return start.elapsed_time(end) / reps * 1e3  # microseconds
 
 
+def host_identity():
+    """CPU model name (as lscpu prints it, from /proc/cpuinfo), nproc and os.cpu_count()."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu_model": model, "nproc": nproc, "os_cpu_count": os.cpu_count()}
+
+
+def host_threads() -> int:
+    """Threads for the CPU baseline: every core this process may run on (nproc), capped at
+    the 16-core host share a one-GPU box grants a job."""
+    return max(1, min(host_identity()["nproc"] or 1, 16))
+
+
 def cpu_baseline(wl, seconds):
     """The reference recipe on torch CPU (e4m3 round trip, fp32 conv/dgrad/wgrad) on a bounded
     sample of the workload: the first `b` images, b grown until the run takes ~seconds."""
     from oracle import fp8_oracle  # noqa: F401  (the CPU restatement of the recipe)
     import torch.nn.functional as F
 
-    threads = torch.get_num_threads()
+    threads = host_threads()
+    torch.set_num_threads(threads)
 
     def q(t):
         t = t.float()
@@ -416,7 +438,8 @@ def cpu_baseline(wl, seconds):
         dt = (time.perf_counter() - t0) / done
         flop = 2.0 * rows * wl.nn * wl.kk
         return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-                "sample": f"{rows} of {wl.m} rows, {done} reps, {dt * 1e3:.1f} ms/rep"}
+                "sample": f"{rows} of {wl.m} rows, {done} reps, {dt * 1e3:.1f} ms/rep",
+                "host": host_identity()}
     b = 1
     x = wl.x[:b].cpu().float()
     w = wl.wt.cpu()
@@ -438,7 +461,8 @@ def cpu_baseline(wl, seconds):
     flop = 3 * wl.flop * b / wl.n
     return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{b} of {wl.n} images (fwd+dgrad+wgrad incl. e4m3 round trip), {reps} reps, "
-                      f"{dt * 1e3:.0f} ms/rep; torch CPU fp32"}
+                      f"{dt * 1e3:.0f} ms/rep; torch CPU fp32",
+            "host": host_identity()}
 
 
 def main():

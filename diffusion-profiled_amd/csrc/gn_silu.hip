@@ -1481,6 +1481,11 @@ extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, 
                                   void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  // the added gradient is x's dtype, or bf16 beside an fp32 x; nothing else is read
+  if (dx_add && dx_add_dtype != DPA_DTYPE_BF16 && dx_add_dtype != DPA_DTYPE_F32)
+    return DPA_ERR_SHAPE;
+  if (dx_add && x_dtype == DPA_DTYPE_BF16 && dx_add_dtype != DPA_DTYPE_BF16)
+    return DPA_ERR_SHAPE;
   return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dx, dgamma,
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
                 stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p, dx_add,

@@ -82,19 +82,6 @@ __shared__ __attribute__((aligned(1024))) uint8_t ig_slot[kWaves][kSlotBytes];
 // reads of ds_read_b128 conflict-free, where (r & 7) or ((r >> 1) & 7) cost 2 passes.
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
-#ifdef DPA_IG_PROBE
-__device__ unsigned long long g_ig_probe[4096 * 16];
-#define IG_STAMP(slot)                                                                   \
-  do {                                                                                   \
-    if (threadIdx.x == 0 && blockIdx.x < 4096)                                           \
-      g_ig_probe[blockIdx.x * 16 + (slot)] = __builtin_readcyclecounter();               \
-  } while (0)
-#else
-#define IG_STAMP(slot) \
-  do {                 \
-  } while (0)
-#endif
-
 // m -> (n, i, j) of the launch grid [N, Pg, Qg]
 __device__ __forceinline__ void decode_pixel(const IgemmArgs& p, int m, int& n, int& i, int& j) {
   const uint32_t t = fdiv((uint32_t)m, p.divQ);
@@ -118,7 +105,6 @@ __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
 }
 
 __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArgs p) {
-  IG_STAMP(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -278,11 +264,9 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
       for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
   };
 
-  IG_STAMP(1);
   issue(ig_st[0], 0);
   issue(ig_st[1], 1);
   issue(ig_st[2], 2);
-  IG_STAMP(2);
   wait_vmcnt<2 * kLoadsPerStage>();
   lds_barrier();
 #pragma unroll
@@ -317,10 +301,8 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
       epilogue((int)fdiv((uint32_t)s, p.divNK));
     }
     cur = nx;
-    if (s == 0) IG_STAMP(3);
   }
   wait_vmcnt<0>();  // trailing zero-page DMAs land before the workgroup retires
-  IG_STAMP(4);
 }
 
 // wt[ci][r][s][co] = w[co][r][s][ci] (e4m3 bytes): 32x32 byte tiles through LDS.

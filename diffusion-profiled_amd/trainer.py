@@ -9,14 +9,59 @@ of their buffers come from torch's allocator (the graph's private pool).
 
 ``TrainState`` bundles model, optimizer, diffusion wrapper, EMA and the static input buffers
 so a benchmark or test can build the reference's training setup in one call.
+
+``save_checkpoint`` / ``load_checkpoint`` use the reference's file format (train.py:85-91).
 """
 from __future__ import annotations
+
+import dataclasses
+import os
 
 import torch
 
 from .ddpm import DiffusionWrapper, EWMAWrapper
 from .optim import FusedAdamWEMA
 from .unet import UNet, UNetConfig
+
+
+CHECKPOINT_KEYS = ("model_state_dict", "step", "config")
+_COMPILED_PREFIX = "_orig_mod."  # state_dict prefix of a torch.compile'd module
+
+
+def save_checkpoint(model: torch.nn.Module, step: int, config: dict, filename: str) -> None:
+    """train.py:85-91: ``{"model_state_dict": model.state_dict(), "step": step, "config":
+    config}`` written with torch.save. The reference passes its EMA model and
+    ``UNetConfig.as_dict()`` plus ``hparams.*`` entries; the keys of this build's state dict
+    are the reference's (module tree, parameter and FP8 window buffer names)."""
+    torch.save({"model_state_dict": model.state_dict(), "step": int(step), "config": config},
+               filename)
+
+
+def config_from_dict(config: dict) -> UNetConfig:
+    """The UNetConfig of a checkpoint's ``config``: the dataclass fields it names (the
+    reference's ``hparams.*`` and any other keys are not model fields and are skipped)."""
+    names = {f.name for f in dataclasses.fields(UNetConfig)}
+    return UNetConfig(**{k: v for k, v in config.items() if k in names})
+
+
+def load_checkpoint(filename: str | os.PathLike, model: torch.nn.Module | None = None,
+                    map_location="cpu", strict: bool = True):
+    """Reads a checkpoint in the reference's format with ``torch.load(weights_only=True)``
+    (tensors, numbers, strings and containers only; nothing in the file is executed).
+    State dicts saved from a torch.compile'd module (the reference compiles its model and
+    its EMA copy, train.py:251, diffusion/ddpm.py:16) carry an ``_orig_mod.`` prefix, which
+    is removed. Loads into ``model`` (built from the checkpoint's config when None) and
+    returns ``(model, step, config)``."""
+    ck = torch.load(filename, map_location=map_location, weights_only=True)
+    if not isinstance(ck, dict) or any(k not in ck for k in CHECKPOINT_KEYS):
+        raise KeyError(f"{filename}: not a checkpoint with keys {CHECKPOINT_KEYS}")
+    sd = {(k[len(_COMPILED_PREFIX):] if k.startswith(_COMPILED_PREFIX) else k): v
+          for k, v in ck["model_state_dict"].items()}
+    config = ck["config"]
+    if model is None:
+        model = UNet(config_from_dict(config))
+    model.load_state_dict(sd, strict=strict)
+    return model, int(ck["step"]), config
 
 
 def _one_step(ddpm: DiffusionWrapper, model: torch.nn.Module, ema_ddpm: DiffusionWrapper,

@@ -250,7 +250,9 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * Optional dropout of the output (diffusion/unet.py:160, nn.Dropout(p) before conv_2):
  * drop_seed = a uint64 in device memory, NULL for none; an element is kept when its 32-bit
  * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
- * for even idx, the high half for odd idx) is >= p * 2^32, and kept values are scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
+ * for even idx, the high half for odd idx) is >= floor(p * 2^32) with p the fp32 drop_p
+ * argument (exact in double; 0xffffffff when that reaches 2^32 - 1), and kept values are
+ * scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
  * reference drops the fp32 SiLU output). The backward recomputes the mask from the same seed
  * and p. Dropout takes the chunked or small-image form as fp32 x does; 0 <= p < 1.
  * dx_add (backward; x's dtype and layout, or NULL): a second gradient of x added to dx as
@@ -258,6 +260,7 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * path's gradient of the residual block input (diffusion/unet.py:149, :161), which x feeds
  * besides norm1; dx_add_dtype DPA_DTYPE_BF16 with an fp32 x adds a bf16 gradient (autograd's
  * fp32 cast of it, then one fp32 add). Chunked or small-image form only; may alias dx.
+ * Any other dx_add_dtype, or an fp32 dx_add beside a bf16 x, returns DPA_ERR_SHAPE.
  * x_bf16 (forward, fp32 x only, or NULL): also writes x rounded to bf16 (RNE) there — the
  * input the 1x1 skip conv rounds to anyway — so no separate cast pass reads x again. */
 int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,

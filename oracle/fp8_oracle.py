@@ -245,8 +245,10 @@ def dropout_keep(seed: int, n: int, p: float) -> np.ndarray:
     when its 32-bit half of splitmix64(seed, idx // 2) (the low half for even idx, the high
     half for odd idx) is >= p * 2^32. The reference draws its mask from torch's Philox
     generator (diffusion/unet.py:160 nn.Dropout), which no restatement reproduces; this mask
-    has the same keep probability 1 - p."""
-    keep_from = min(int(p * 4294967296.0), 0xFFFFFFFF)
+    has the same keep probability 1 - p. p is taken as the fp32 value the C ABI receives
+    (``float drop_p``): the threshold is floor(fp32(p) * 2^32), computed exactly in double."""
+    t = float(np.float32(p)) * 4294967296.0
+    keep_from = 0xFFFFFFFF if t >= 4294967295.0 else int(t)
     idx = np.arange(n, dtype=np.uint64)
     z = splitmix64(seed, idx >> np.uint64(1))
     half = np.where((idx & np.uint64(1)) == 1, z >> np.uint64(32), z & np.uint64(0xFFFFFFFF))
@@ -255,8 +257,8 @@ def dropout_keep(seed: int, n: int, p: float) -> np.ndarray:
 
 def dropout_scale(p: float) -> np.float32:
     """1 / (1 - p) as torch's dropout kernel forms it: 1 - p rounded to fp32, its reciprocal
-    taken in double and rounded to fp32."""
-    return np.float32(1.0 / float(np.float32(1.0 - p)))
+    taken in double and rounded to fp32; p is the fp32 value the C ABI receives."""
+    return np.float32(1.0 / float(np.float32(1.0 - float(np.float32(p)))))
 
 
 def gn_silu_fwd(x_bits: np.ndarray, gamma: np.ndarray, beta: np.ndarray, groups: int,

@@ -79,3 +79,30 @@ def assert_bf16_close(got_bits: np.ndarray, ref_bits: np.ndarray, what: str = ""
         f"{np.max(np.abs(g - r) - bound):.3e}, norm err {norm_err:.3e}"
     )
     return float(np.mean(got_bits == ref_bits))
+
+
+def _splitmix64_state_for(z: int) -> int:
+    """Inverse of splitmix64's finaliser: the state whose output is z (each xorshift and odd
+    multiply is a bijection on 64-bit words)."""
+    m = (1 << 64) - 1
+    z ^= (z >> 31) ^ (z >> 62)
+    z = (z * pow(0x94D049BB133111EB, -1, 1 << 64)) & m
+    z ^= (z >> 27) ^ (z >> 54)
+    z = (z * pow(0xBF58476D1CE4E5B9, -1, 1 << 64)) & m
+    z ^= (z >> 30) ^ (z >> 60)
+    return z
+
+
+def dropout_band_seed(p: float = 0.2) -> tuple[int, int]:
+    """A seed whose element-0 hash lies in [floor(p * 2^32), floor(fp32(p) * 2^32)): kept under
+    a double-precision threshold, dropped under the fp32 one the C ABI takes. Returns
+    (seed, element-0 hash)."""
+    lo_d = int(p * 4294967296.0)
+    lo_f = int(float(np.float32(p)) * 4294967296.0)
+    assert lo_d < lo_f
+    h0 = (lo_d + lo_f) // 2
+    for hi in range(0xFFFFFFFF, 0xFFFFFF00, -1):  # element 1 kept; the seed fits an int64
+        seed = _splitmix64_state_for((hi << 32) | h0)
+        if seed < 2**62:
+            return seed, h0
+    raise AssertionError("no seed below 2^62")

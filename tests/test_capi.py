@@ -73,8 +73,12 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, fake, fake, fake, fake, nul, 0, fake, fake, nul, nul, fake, fake, 1 << 20, 1, 16, 128, 32, fake, -0.5, nul) == -2
     # dx_add: 16-B aligned, chunked or small-image form only; x_bf16 needs an fp32 x
     assert lib.dpa_gn_silu_fwd_ex(fake, 0, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 128, 32, 1e-5, nul, 0.0, fake, nul) == -4
-    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, ctypes.c_void_p(0x1008), 1, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 16, 128, 32, nul, 0.0, nul) == -3
-    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 1, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 144, 128, 32, nul, 0.0, nul) == -4
+    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, ctypes.c_void_p(0x1008), 0, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 16, 128, 32, nul, 0.0, nul) == -3
+    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 0, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 144, 128, 32, nul, 0.0, nul) == -4
+    # dx_add_dtype: BF16 or F32 only, and an fp32 dx_add only beside an fp32 x
+    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 1, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 1024, 128, 32, nul, 0.0, nul) == -4
+    assert lib.dpa_gn_silu_bwd_ex(fake, 1, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 2, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 1024, 128, 32, nul, 0.0, nul) == -4
+    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, -1, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 1024, 128, 32, nul, 0.0, nul) == -4
     assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, nul, fake, 4, 0,
                                                     fake, 4096, nul) == -1
     assert lib.dpa_quantize_fp8_delayed_window_bf16(fake, 16, fake, fake, fake, fake, fake, 0, 0,

@@ -14,7 +14,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from conftest import assert_bf16_close, dpa_mod, nhwc_bits, randn_bf16
+from conftest import assert_bf16_close, dpa_mod, dropout_band_seed, nhwc_bits, randn_bf16
 from oracle import fp8_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -389,6 +389,44 @@ def test_gn_silu_film_dropout_vs_oracle(G, n, c, h, w, x32):
     dwb = wbd.grad.float().reshape(n, 2 * c).cpu().numpy()
     assert rel(dwb[:, :c], rdfs) < 4e-3
     assert rel(dwb[:, c:], rdfb) < 4e-3
+
+
+@pytest.mark.parametrize("n,c,h,w,x32", [(1, 256, 16, 16, False), (1, 256, 8, 8, True)],
+                         ids=lambda v: str(v))
+def test_gn_silu_film_dropout_threshold_band(G, n, c, h, w, x32):
+    """The keep threshold is floor(fp32(p) * 2^32). With p = 0.2 a hash in
+    [floor(0.2 * 2^32), floor(fp32(0.2) * 2^32)) must be dropped: the seed is built (by
+    inverting splitmix64) so that element 0's hash lies in that 13-value band. The kernel's
+    whole mask, forward and backward, equals the oracle's."""
+    p = 0.2
+    seed, _ = dropout_band_seed(p)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn((n, c, h, w), generator=g) + 0.5
+    if not x32:
+        x = x.to(torch.bfloat16)
+    gamma, beta, _, _ = params(c, n, 10, False)
+    wb = (0.3 * torch.randn((n, 2 * c, 1, 1), generator=g)).to(torch.bfloat16)
+    G.DROPOUT_SEEDS.seeds = torch.tensor([seed], device="cuda", dtype=torch.int64)
+    G.DROPOUT_SEEDS.next = 0
+    try:
+        xd = cl(x).requires_grad_()
+        y = G.group_norm_silu_film(xd, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb.cuda(), p)
+        assert G.DROPOUT_SEEDS.next == 1  # the op took the planted seed
+    finally:
+        G.DROPOUT_SEEDS.clear()
+    y.backward(torch.ones_like(y))
+    torch.cuda.synchronize()
+    keep = O.dropout_keep(seed, n * h * w * c, p)
+    assert not keep[0] and keep[1]
+    got = nhwc_bits(y.detach().cpu()).reshape(-1)
+    undropped = G.group_norm_silu_film(cl(x), gamma.cuda(), beta.cuda(), GROUPS, 1e-5,
+                                       wb.cuda(), 0.0)
+    ub = nhwc_bits(undropped.cpu()).reshape(-1)
+    assert ub[0] & 0x7FFF != 0  # element 0 is nonzero before dropout, zero after
+    assert got[0] & 0x7FFF == 0
+    assert np.array_equal((got & 0x7FFF) == 0, (~keep) | ((ub & 0x7FFF) == 0))
+    gx = xd.grad.float().permute(0, 2, 3, 1).contiguous().reshape(-1).cpu().numpy()
+    assert np.isfinite(gx).all()
 
 
 def test_gn_silu_film_dropout_zero_p_and_fresh_masks(G):

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from oracle import c_oracle
+import conftest
 from oracle import fp8_oracle as O
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "cast_digests.npz")
@@ -195,3 +196,55 @@ def test_dropout_hash_known_answers_and_rate():
     assert O.dropout_keep(7, 1000, 0.0).all()
     assert O.dropout_scale(0.2) == np.float32(1.25)
     assert O.dropout_scale(0.1) == np.float32(1.0) / np.float32(0.9)
+
+
+def test_e4m3_decode_matches_torch_on_all_codes():
+    """e4m3_to_f32 decodes every operand of the conv/GEMM oracle; it must equal torch's own
+    float8_e4m3fn decoder on all 256 codes (subnormals k * 2^-9, both zeros, NaN at 0x7f/0xff)."""
+    codes = np.arange(256, dtype=np.uint8)
+    got = O.e4m3_to_f32(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    nan_g, nan_r = np.isnan(got), np.isnan(ref)
+    assert np.array_equal(nan_g, nan_r)
+    assert np.flatnonzero(nan_r).tolist() == [0x7F, 0xFF]
+    assert np.array_equal(got[~nan_g].view(np.uint32), ref[~nan_r].view(np.uint32))
+
+
+def test_bf16_rounding_matches_torch():
+    """f32_to_bf16_bits against torch's Tensor.to(bfloat16) on > 1M fp32 values: random bit
+    patterns over the whole finite range, exact ties (low half 0x8000) at both mantissa
+    parities, values one ulp either side of a tie, subnormals, infinities and the largest
+    finite values (which round to inf); bf16_bits_to_f32 against torch's widening."""
+    rng = np.random.default_rng(11)
+    u = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    u = u[(u & 0x7F800000) != 0x7F800000]  # finite
+    hi = rng.integers(0, 1 << 16, size=1 << 16, dtype=np.uint32) << 16
+    ties = hi | 0x8000
+    near = np.concatenate([ties - 1, ties + 1])
+    sub = rng.integers(1, 1 << 23, size=1 << 14, dtype=np.uint32)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7F7FFFFF, 0xFF7FFFFF,
+                        0x7F7F8000, 0x7F7F7FFF, 0x00008000, 0x00018000], dtype=np.uint32)
+    allu = np.concatenate([u, ties, near, sub, sub | 0x80000000, special])
+    allu = allu[(allu & 0x7FFFFFFF) <= 0x7F800000]  # NaNs have no single rounding
+    f = allu.view(np.float32)
+    got = O.f32_to_bf16_bits(f)
+    ref = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert f.size > 1_000_000
+    assert np.array_equal(got, ref)
+    codes = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    wide = O.bf16_bits_to_f32(codes)
+    tw = torch.from_numpy(codes.view(np.int16)).view(torch.bfloat16).float().numpy()
+    fin = ~np.isnan(tw)
+    assert np.array_equal(np.isnan(wide), ~fin)
+    assert np.array_equal(wide[fin].view(np.uint32), tw[fin].view(np.uint32))
+
+
+def test_dropout_threshold_uses_fp32_p():
+    """The keep threshold is floor(fp32(p) * 2^32): for p = 0.2 that is 858993472, 13 above
+    floor(0.2 * 2^32). A hash inside that band (built by inverting splitmix64) is dropped."""
+    seed, h0 = conftest.dropout_band_seed(0.2)
+    z = int(O.splitmix64(seed, np.zeros(1, dtype=np.uint64))[0])
+    assert z & 0xFFFFFFFF == h0 and z >> 32 > 0xFFFFFF00
+    keep = O.dropout_keep(seed, 2, 0.2)
+    assert not keep[0] and keep[1]
+    assert O.dropout_keep(seed, 2, np.float32(0.2))[0] == keep[0]

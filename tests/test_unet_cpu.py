@@ -207,3 +207,54 @@ def test_resblock_math_on_cpu():
     t = torch.randn(2, 512)
     out = blk(x, t)
     torch.testing.assert_close(out, blk.skip_connection(x) / math.sqrt(2.0))
+
+
+def test_checkpoint_round_trip_in_reference_format(tmp_path):
+    """train.py:85-91 format: {"model_state_dict", "step", "config"} via torch.save. Every
+    entry, FP8 amax windows and window positions included, survives the round trip bit for
+    bit; the file loads with weights_only=True; a checkpoint of a torch.compile'd model
+    (keys prefixed "_orig_mod.", config with the reference's fields and hparams.* entries)
+    loads into a model built from its config; a missing key fails under strict loading."""
+    from importlib import import_module
+
+    T = import_module("diffusion-profiled_amd.trainer")
+    torch.manual_seed(0)
+    m = U.UNet(reference_train_config())
+    g = torch.Generator().manual_seed(3)
+    for name, buf in m.named_buffers():
+        if name.endswith("window_pos"):
+            buf.fill_(int(torch.randint(0, 1024, (1,), generator=g)))
+        elif "amax_window" in name:
+            buf.copy_(torch.rand(buf.shape, generator=g))
+    config = m.config.as_dict()
+    config.update({"hparams.max_t": 1000, "hparams.batch_size": 128})
+    path = tmp_path / "checkpoint_linear.pt"
+    T.save_checkpoint(m, 1234, config, str(path))
+    raw = torch.load(path, weights_only=True)
+    assert set(raw) == set(T.CHECKPOINT_KEYS)
+    m2, step, cfg2 = T.load_checkpoint(path)
+    assert step == 1234 and cfg2 == config
+    sd, sd2 = m.state_dict(), m2.state_dict()
+    assert list(sd) == list(sd2)
+    for k in sd:
+        assert sd[k].dtype == sd2[k].dtype and torch.equal(sd[k], sd2[k]), k
+
+    ref_fields = {"in_channels", "base_hidden", "scales", "n_heads", "p_drop", "attn_resolutions",
+                  "in_resolution", "n_resblocks", "fp8_convs_enabled", "fp8_scaling_type",
+                  "fp8_amax_history"}  # diffusion/unet.py:13-25
+    ref_cfg = {k: v for k, v in config.items() if k in ref_fields or k.startswith("hparams.")}
+    compiled = {"_orig_mod." + k: v for k, v in sd.items()}
+    torch.save({"model_state_dict": compiled, "step": 7, "config": ref_cfg}, tmp_path / "c.pt")
+    m3, step3, _ = T.load_checkpoint(tmp_path / "c.pt")
+    assert step3 == 7
+    for k, v in m3.state_dict().items():
+        assert torch.equal(v, sd[k]), k
+
+    broken = dict(sd)
+    broken.pop("down_stages.0.blocks.0.conv_1.window_pos")
+    torch.save({"model_state_dict": broken, "step": 1, "config": config}, tmp_path / "b.pt")
+    with pytest.raises(RuntimeError):
+        T.load_checkpoint(tmp_path / "b.pt")
+    torch.save({"step": 1}, tmp_path / "n.pt")
+    with pytest.raises(KeyError):
+        T.load_checkpoint(tmp_path / "n.pt")
