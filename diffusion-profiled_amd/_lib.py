@@ -20,6 +20,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_abi_version": (c_int, []),
     "dpa_quant_workspace_bytes": (c_int64, [c_int64]),
     "dpa_quantize_fp8_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "dpa_quantize_fp8_bf16_noalloc_scratch_bytes": (c_int64, []),
+    "dpa_quantize_fp8_bf16_noalloc": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "dpa_quantize_fp8_delayed_bf16": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],

@@ -16,6 +16,9 @@
 // e4m3 output goes out with nontemporal stores (measured ~2 us faster per 16.8M elements).
 #include "dpa_common.hpp"
 
+#include <atomic>
+#include <mutex>
+
 namespace dpa {
 
 constexpr int kQThreads = 256;
@@ -334,6 +337,63 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
                                                         scale_out);
   }
   return launch_status();
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free current scaling. The amax partials (one u32 per amax workgroup, at most
+// kMaxPartials) live in a file-scope device array, `scratch`, instead of a caller workspace:
+// every GPU the library runs on holds its own copy (4 KB) until the process ends. Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in symbol); it
+// passes the device address hipGetSymbolAddress returns, looked up once per device.
+// ---------------------------------------------------------------------------------------
+constexpr int kScratchBytes = kMaxPartials * 4;
+static __device__ __align__(256) uint32_t scratch[kMaxPartials];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device address of `scratch` on device dev (looked up with dev current, once).
+static int scratch_ptr(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return DPA_ERR_SIZE;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = -1;
+      hipError_t e = hipGetDevice(&cur);
+      if (e != hipSuccess) return (int)e;
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess || !p) return e != hipSuccess ? (int)e : DPA_ERR_NULL;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return DPA_OK;
+}
+
+extern "C" int64_t dpa_quantize_fp8_bf16_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int dpa_quantize_fp8_bf16_noalloc(const void* x, int64_t n, void* q, float* scale_out,
+                                             void* stream) {
+  if (!x || !q || !scale_out) return DPA_ERR_NULL;
+  if (n <= 0) return DPA_ERR_SIZE;
+  if (dpa_quant_workspace_bytes(n) > kScratchBytes) return DPA_ERR_WORKSPACE;
+  if (!aligned(scale_out, 4) || !aligned(x, 2)) return DPA_ERR_ALIGN;
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  void* ws = nullptr;
+  const int st = scratch_ptr(dev, &ws);
+  if (st != DPA_OK) return st;
+  // the same launches as dpa_quantize_fp8_bf16; every partial the cast reads is written first
+  return dpa_quantize_fp8_bf16(x, n, q, scale_out, ws, kScratchBytes, stream);
 }
 
 static int quantize_delayed(const void* x, int64_t n, const float* prev_scale, void* q,

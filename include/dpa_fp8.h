@@ -67,6 +67,21 @@ int64_t dpa_quant_workspace_bytes(int64_t n);
 int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* scale_out,
                           void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Current scaling with no workspace argument and no allocation: the same launches, bytes and
+ * scale as dpa_quantize_fp8_bf16, with the amax partials in a fixed 4 KB device array of the
+ * library (dpa_quantize_fp8_bf16_noalloc_scratch_bytes(); one copy per GPU, held until the
+ * process ends; its device address is looked up once per device on the first call there).
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). Calls no hipMalloc,
+ * hipFree or allocating library routine. Every n > 0 fits (the partial count is capped at
+ * 1024); a size whose workspace would exceed the array returns DPA_ERR_WORKSPACE. All calls
+ * on one GPU share the array: calls that overlap on that GPU (concurrent streams, threads)
+ * race and must be serialised by the caller. The stream's device (or the current device for
+ * the NULL stream) selects the array. */
+int64_t dpa_quantize_fp8_bf16_noalloc_scratch_bytes(void);
+int dpa_quantize_fp8_bf16_noalloc(const void* x, int64_t n, void* q, float* scale_out,
+                                  void* stream);
+
 /* Delayed scaling: q <- cast(x, *prev_scale); cur_scale_out <- scale(amax(x)).
  * One read of x. Replaces quantize_fp8_delayed (diffusion/fp8_kernels.py:518-556). */
 int dpa_quantize_fp8_delayed_bf16(const void* x, int64_t n, const float* prev_scale, void* q,

@@ -85,6 +85,11 @@ def test_precondition_errors_return_before_launch(lib):
                                                     fake, 4096, nul) == -2
     assert lib.dpa_window_max3_f32(nul, fake, fake, 4, fake, nul) == -1
     assert lib.dpa_window_max3_f32(fake, fake, fake, 0, fake, nul) == -2
+    # the allocation-free quantize checks its arguments before it looks up its device array
+    assert lib.dpa_quantize_fp8_bf16_noalloc(nul, 16, fake, fake, nul) == -1
+    assert lib.dpa_quantize_fp8_bf16_noalloc(fake, 0, fake, fake, nul) == -2
+    assert lib.dpa_quantize_fp8_bf16_noalloc(fake, 16, fake, ctypes.c_void_p(0x1002), nul) == -3
+    assert lib.dpa_quantize_fp8_bf16_noalloc_scratch_bytes() == lib.dpa_quant_workspace_bytes(1 << 40)
     # workspace too small
     assert lib.dpa_quantize_fp8_bf16(fake, 16, fake, fake, fake, 8, nul) == -5
     assert lib.dpa_conv2d_dgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -5
