@@ -4,6 +4,7 @@ fake-quant emulation, and the graph-captured U-Net training step against eager s
 """
 from __future__ import annotations
 
+import copy
 import math
 import types
 
@@ -13,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 from conftest import assert_bf16_close, bits, dpa_mod, kaiming_uniform_bf16, nhwc_bits, randn_bf16
-from fakequant import emulate
+from fakequant import emulate, emulate_on_gpu
 from oracle import fp8_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -204,6 +205,186 @@ def test_graph_captured_step_matches_eager_steps():
             torch.testing.assert_close(buf, q, rtol=2**-5, atol=0, msg=name)
 
 
+def _nonzero_init(model: torch.nn.Module) -> torch.nn.Module:
+    """Kaiming-uniform weights for the zero-initialised projections (each block's conv_2,
+    the attention output projections, the output conv), so every path carries signal."""
+    with torch.no_grad():
+        for p in model.parameters():
+            if p.dim() > 1 and not p.any():
+                torch.nn.init.kaiming_uniform_(p, a=math.sqrt(5))
+    return model
+
+
+def _fp8_site_active(m, x) -> bool:
+    if isinstance(m, U.Conv2dFP8):
+        return m.conv_fp8(x, m.conv.weight) or m.conv_fp8_general(x, m.conv.weight)
+    if isinstance(m, U.Conv1x1FP8):
+        return m.fp8 and m.in_channels % 128 == 0 and m.out_channels % 128 == 0
+    return m.fp8 and K.linear_fp8_supported(m.in_features, m.out_features)
+
+
+def test_unet_forward_backward_vs_fakequant_emulation():
+    """cfg5's U-Net (current scaling, dropout off) at batch 2, one forward+backward under
+    autocast: every FP8 site (registry and general 3x3 convs, 1x1 skips, linears) is checked
+    inside the model, teacher-forced: the output it computed from the x it received, and the
+    dx / dw its backward produced from the dy it received, against the fake-quant emulation of
+    that site on the same x and dy (tests/fakequant.py: torch e4m3 casts, exact fp64 products,
+    the reference's epilogue) -- normwise 1e-2, outputs >= 95 % bit-identical. The whole
+    model's loss is checked against the emulated model's (fakequant.emulate_on_gpu, same
+    weights and inputs) within 1e-2 relative (train.py:104-149 around
+    diffusion/unet.py:245-388).
+
+    The epsilon prediction is not compared elementwise: an e4m3 cast turns a one-ulp
+    difference at one site into rounding flips (steps of 2^-4 relative) at the next, so two
+    correct FP8 implementations drift to the quantization noise level within a few layers
+    (measured: 15 % normwise at the output, with the loss equal to 1e-4)."""
+    from fakequant import GpuFakeQuantConv, GpuFakeQuantLinear
+
+    torch.manual_seed(3)
+    model = _nonzero_init(U.UNet(_cfg())).to(memory_format=torch.channels_last).cuda()
+    em = emulate_on_gpu(copy.deepcopy(model))
+    g = torch.Generator().manual_seed(4)
+    x0 = torch.rand((2, 3, 32, 32), generator=g) * 2 - 1
+    t = torch.randint(0, 1000, (2,), generator=g).cuda()
+    eps = torch.randn((2, 3, 32, 32), generator=g).cuda()
+    ab = dpa_mod("ddpm").make_schedule(1000, "linear")[1].cuda()[t].float()[:, None, None, None]
+    xt = (ab.sqrt() * x0.cuda() + (1 - ab).sqrt() * eps).contiguous(memory_format=torch.channels_last)
+
+    rec, hooks = {}, []
+    for n, m in model.named_modules():
+        if isinstance(m, (U.Conv2dFP8, U.Conv1x1FP8, U.LinearFP8)):
+            hooks.append(m.register_forward_hook(
+                lambda mod, i, o, n=n: rec.__setitem__(n, {"x": i[0].detach().clone(),
+                                                           "y": o.detach().clone()})))
+            hooks.append(m.register_full_backward_hook(
+                lambda mod, gi, go, n=n: rec[n].update(
+                    dy=go[0].detach().clone(),
+                    dx=None if gi[0] is None else gi[0].detach().clone())))
+    losses = {}
+    for name, m in (("hip", model), ("emu", em)):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = F.mse_loss(m(xt, t), eps)
+        loss.backward()
+        losses[name] = float(loss)
+        for h in hooks:
+            h.remove()
+        hooks = []
+    torch.cuda.synchronize()
+    print(f"unet batch 2: loss {losses['hip']:.6f} vs emulation {losses['emu']:.6f}", flush=True)
+    assert math.isfinite(losses["hip"]) and losses["hip"] == pytest.approx(losses["emu"], rel=1e-2)
+
+    mods = dict(model.named_modules())
+    checked, worst = 0, []
+    for n, r in rec.items():
+        m = mods[n]
+        if not _fp8_site_active(m, r["x"]):
+            continue
+        x = r["x"].clone().requires_grad_(r["dx"] is not None)
+        if isinstance(m, U.LinearFP8):
+            w = m.weight.detach().clone().requires_grad_()
+            y = GpuFakeQuantLinear.apply(x, w)
+        else:
+            w = (m.conv.weight if isinstance(m, U.Conv2dFP8) else m.weight).detach().clone()
+            w = w.requires_grad_()
+            y = GpuFakeQuantConv.apply(x, w, 1, 1 if isinstance(m, U.Conv2dFP8) else 0)
+        y.backward(r["dy"])
+        wg = (m.conv.weight if isinstance(m, U.Conv2dFP8) else m.weight).grad
+        errs = {"y": nerr(r["y"], y), "dw": nerr(wg, w.grad)}
+        if r["dx"] is not None:             # the time embedding's input needs no gradient
+            errs["dx"] = nerr(r["dx"], x.grad)
+        same = float((r["y"].view(torch.int16) == y.detach().view(torch.int16)).float().mean())
+        worst.append((max(errs.values()), n, errs, same, tuple(r["x"].shape), r["x"].dtype))
+        checked += 1
+    worst.sort(key=lambda v: -v[0])
+    for e, n, errs, same, shp, dt in worst[:12]:
+        print(f"  {n} {shp} {dt}: " + " ".join(f"{k} {v:.2e}" for k, v in errs.items())
+              + f" bit-identical y {same:.4f}", flush=True)
+    print(f"{checked} FP8 sites", flush=True)
+    # 44 3x3 convs, 5 1x1 skips, 22 FiLM projections, 24 attention projections, 2 time-MLP linears
+    assert checked == 97, checked
+    for e, n, errs, same, _, _ in worst:
+        assert e < 1e-2, (n, errs)
+        assert same >= 0.95, (n, same)
+
+
+def test_graph_captured_cfg5_step_at_batch_128():
+    """One graph-captured step of the timed configuration (cfg5: delayed scaling, 1024-slot
+    windows, dropout 0.2, batch 128) against an eager step from the same state and the same
+    random stream (the dropout seeds are drawn inside the step): finite and equal losses,
+    parameters within the batch-4 test's bounds, every delayed layer's window position
+    advanced by one and its new window entries written."""
+    kw = dict(fp8_scaling_type="delayed", p_drop=0.2)
+    a = _state(128, **kw)
+    b = _state(128, **kw)
+    torch.cuda.manual_seed(11)
+    a.capture(warmup=3)
+    torch.cuda.manual_seed(11)
+    for _ in range(3):
+        b.eager_step()
+    for st in (a, b):
+        if st.model._wprep is not None:
+            st.model._wprep.flush()        # window records lag one step until flushed
+    torch.cuda.synchronize()
+    a.loss_acc.zero_()
+    b.loss_acc.zero_()
+    # the 43 registry convs run delayed scaling; the one other 3x3 conv runs current scaling
+    pos0 = {n: int(v) for n, v in a.model.named_buffers() if n.endswith("window_pos") and int(v)}
+    assert len(pos0) == 43 and all(v == 3 for v in pos0.values()), pos0
+    assert pos0 == {n: int(v) for n, v in b.model.named_buffers()
+                    if n.endswith("window_pos") and int(v)}
+    torch.cuda.manual_seed(12)
+    a.replay()
+    torch.cuda.synchronize()
+    torch.cuda.manual_seed(12)
+    b.eager_step()
+    torch.cuda.synchronize()
+    for st in (a, b):
+        if st.model._wprep is not None:
+            st.model._wprep.flush()        # the deferred window records of the step
+    torch.cuda.synchronize()
+    la, lb = float(a.loss_acc), float(b.loss_acc)
+    print(f"cfg5 batch 128: replay loss {la:.6f}, eager loss {lb:.6f}", flush=True)
+    assert math.isfinite(la) and la == pytest.approx(lb, rel=1e-4), (la, lb)
+    for (name, p), q in zip(a.model.named_parameters(), b.model.parameters()):
+        d = float((p.detach() - q.detach()).float().norm())
+        bound = 1e-4 * float(q.detach().float().norm()) + 1e-5 * math.sqrt(q.numel())
+        assert d <= bound, (name, d, bound)
+    bufs_a = dict(a.model.named_buffers())
+    for name, p0 in pos0.items():
+        assert int(bufs_a[name]) == (p0 + 1) % 1024, name
+        mod = name[: -len("window_pos")]
+        for w in ("amax_window_acts", "amax_window_weights"):
+            assert float(bufs_a[mod + w][p0]) > 0, (mod + w, p0)   # this step's x / w scales
+        assert float(bufs_a[mod + "amax_window_dy"][(p0 + 1) % 1024]) > 0, mod  # its dy scale
+    for (name, buf), q in zip(a.model.named_buffers(), b.model.buffers()):
+        if buf.dtype == torch.long:
+            assert torch.equal(buf, q), name
+        else:
+            torch.testing.assert_close(buf, q, rtol=2**-5, atol=0, msg=name)
+
+
+def _loss_curve(st, images, t_all, eps_all, batch, eager=False):
+    """Per-step losses of a TrainState over the given timesteps and noise (images cycled)."""
+    steps = t_all.shape[0]
+    st.set_batch(images[:batch], t_all[0], eps_all[0])
+    if eager:
+        for _ in range(3):
+            st.eager_step()
+    else:
+        st.capture(warmup=3)
+    losses = torch.zeros(steps, device="cuda")
+    for i in range(steps):
+        j = (i * batch) % images.shape[0]
+        st.set_batch(images[j:j + batch], t_all[i], eps_all[i])
+        st.loss_acc.zero_()
+        if eager:
+            st.eager_step()
+        else:
+            st.replay()
+        losses[i].copy_(st.loss_acc)
+    return losses.cpu().numpy()
+
+
 def _conv_by_matmul(x: torch.Tensor, w: torch.Tensor, pad: int) -> torch.Tensor:
     """bf16 conv (stride 1) as unfold + one 2-D GEMM, channels-last result."""
     b, c, h, wd = x.shape
@@ -247,8 +428,9 @@ def test_unet_loss_tracks_bf16_over_training():
       window after the first (measured: ~13 % above bf16);
     * delayed scaling with the reference's 1024-slot window (diffusion/unet.py:25) learns
       but trails: the loss falls ~10x in the first 100 steps, and the maximum over the
-      window keeps the large early dy scales for 1024 steps, so small gradients lose their
-      mantissa bits in e4m3. The same state machine behaves the same way in the reference.
+      window keeps the large early scales for the whole run, so small values lose their
+      mantissa bits in e4m3. The torch emulation of the same recipe trails the same way
+      (test_unet_delayed_loss_tracks_recipe_emulation).
     """
     steps, batch, window = 1000, 16, 100
     images = _smooth_images(64, seed=4).cuda()
@@ -286,3 +468,48 @@ def test_unet_loss_tracks_bf16_over_training():
     assert (rel["fp8-delayed-h16"][1:] < rel["fp8-delayed"][1:]).all(), rel
     assert rel["fp8-delayed-h16"][1:].mean() <= 0.2, rel["fp8-delayed-h16"]
     assert curves["fp8-delayed"][-1] < 0.5 * curves["fp8-delayed"][0]
+
+
+def test_unet_delayed_loss_tracks_recipe_emulation():
+    """The timed configuration's scaling (delayed, 1024-slot windows) over 1000 steps at batch
+    16: the HIP model's loss curve (graph replays) against the torch emulation of the same
+    recipe (fakequant.emulate_on_gpu: the window state machine of diffusion/unet.py:69-91 and
+    diffusion/fp8_kernels.py:845-889 on the module buffers, torch e4m3 casts, exact fp64
+    products, torch's clip_grad_norm_ + fused AdamW + EMA), from the same initial weights with
+    the same images, timesteps and noise. The emulation runs eager steps: replays of a graph
+    holding torch's multi-block reductions (its amax) are unreliable on these GPUs.
+
+    The delayed trajectory is chaotic: two emulations that differ only in optimizer rounding
+    (torch's tail, the fused tail) differed by 15-25 % per 100-step window (measured), and
+    repeated HIP runs by up to 24 %. So each HIP window (2-10) must lie within [0.6, 1.6]x the
+    emulation's and the mean |log ratio| over windows 2-10 must stay below 0.2. The recipe
+    itself trails current scaling over a run this short (the window maximum keeps the first
+    steps' large scales for all 1000 steps): windows 6-10 of both curves are >= 2x the
+    current-scaling HIP curve (measured ~3.3x)."""
+    steps, batch, window = 1000, 16, 100
+    images = _smooth_images(64, seed=4).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    t_all = torch.randint(0, 1000, (steps, batch), device="cuda", generator=gen)
+    eps_all = torch.randn((steps, batch, 3, 32, 32), device="cuda", generator=gen)
+    curves = {}
+    for name in ("fp8-current", "fp8-delayed", "emu-delayed"):
+        scaling = "current" if name == "fp8-current" else "delayed"
+        emu = name.startswith("emu")
+        st = T.TrainState(_cfg(fp8_scaling_type=scaling, fp8_amax_history=1024), batch=batch,
+                          seed=0, fixed_noise=True, fused_tail=not emu)
+        if emu:
+            emulate_on_gpu(st.model)
+            for m in st.model.modules():       # GroupNorm+SiLU stay the fused kernel
+                if hasattr(m, "fused"):
+                    m.fused = True
+        losses = _loss_curve(st, images, t_all, eps_all, batch, eager=emu)
+        curves[name] = losses.reshape(-1, window).mean(axis=1)
+        print(f"loss curve {name}: window means " + " ".join(f"{m:.4f}" for m in curves[name]),
+              flush=True)
+        assert np.isfinite(curves[name]).all(), name
+        del st
+    hip, emu, cur = curves["fp8-delayed"], curves["emu-delayed"], curves["fp8-current"]
+    ratio = hip[1:] / emu[1:]
+    assert ((ratio > 0.6) & (ratio < 1.6)).all(), ratio
+    assert np.abs(np.log(ratio)).mean() < 0.2, ratio
+    assert hip[5:].mean() >= 2 * cur[5:].mean() and emu[5:].mean() >= 2 * cur[5:].mean(), curves
