@@ -109,13 +109,24 @@ class ConvWorkload:
         self.xq, self.xs = K.quantize_fp8(self.x)
         self.wprep.run()
         self.wq, self.wq_t, self.ws = self.wprep.q[0], self.wprep.qt[0], self.wprep.scale(0)
+        if self.frag:
+            self.wf, self.wf_t = K.weight_frag_fp8(self.wq)
         self.dyq, self.dys = K.quantize_fp8(self.dy)
 
+    @property
+    def frag(self):
+        return self.K.hconv_shape(self.n, self.cin, self.cout, self.h, self.w, self.k,
+                                  self.stride, self.pad)
+
     def fwd(self):
+        if self.frag:
+            return self.K.conv2d_fp8_fwd_wf(self.xq, self.wf, self.xs, self.ws, self.cout)
         return self.K.conv2d_fp8_fwd_general(self.xq, self.wq, self.xs, self.ws, self.stride, self.pad)
 
     def dgrad(self):
         """The data-gradient GEMM kernel alone (the transposed weight comes from quantize)."""
+        if self.frag:
+            return self.K.conv2d_fp8_dgrad_wf(self.dyq, self.wf_t, self.dys, self.ws, self.cin)
         return self.K.conv2d_fp8_dgrad_general(self.dyq, self.wq, self.dys, self.ws, (self.h, self.w),
                                                self.stride, self.pad, weight_t=self.wq_t)
 

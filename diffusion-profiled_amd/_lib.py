@@ -45,6 +45,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 5 + [c_int] * 9 + [c_void_p],
     ),
     "dpa_weight_transpose_fp8": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "dpa_weight_frag_bytes": (c_int64, [c_int] * 4),
+    "dpa_weight_frag_fp8": (c_int, [c_void_p] * 3 + [c_int] * 4 + [c_void_p]),
+    "dpa_conv2d_fwd_fp8_wf": (c_int, [c_void_p] * 6 + [c_int] * 5 + [c_void_p]),
+    "dpa_conv2d_dgrad_fp8_wf": (c_int, [c_void_p] * 5 + [c_int] * 5 + [c_void_p]),
     "dpa_conv2d_wgrad_workspace_bytes": (c_int64, [c_int] * 10),
     "dpa_conv2d_wgrad_fp8": (
         c_int,

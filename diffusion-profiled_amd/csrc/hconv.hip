@@ -1,4 +1,4 @@
-// FP8 3x3 / stride-1 / pad-1 convolution (forward and data gradient) with a halo-patch A
+// FP8 3x3 / stride-1 / pad-1 convolution (forward and data gradient) with a halo-patch pixel
 // operand, for images W = 16 or 32 pixels wide.
 //
 // Reference: diffusion/fp8_kernels.py conv2d_fwd_fp8_kernel :142-247 and conv2d_dx_fp8_kernel
@@ -6,39 +6,52 @@
 //
 // The nine taps of a 3x3 conv read the same input pixels shifted by (dy, dx). An output tile
 // of 256 pixels is TR = 256 / W whole image rows, so its input is one (TR + 2) x (W + 2)
-// pixel patch. Per 128-channel chunk the patch is DMA'd into LDS once and the nine K-steps
-// (one per tap) read their A fragments from it at offset dy * (W + 2) + dx; only the 16 KB
-// weight slice is loaded per step. Against one A tile per tap this moves 2.3x fewer bytes
-// from L2 into LDS (cfg2: 21 KB instead of 48 KB per K-step).
+// pixel patch. Per 128-channel chunk the patch goes into LDS once and the nine K-steps (one
+// per tap) read their pixel fragments from it at offset dy * (W + 2) + dx.
 //
-// Schedule (as igemm.hip): persistent, one workgroup of 8 waves (4 x 2 of 64 x 64) per CU,
-// XCD-aware contiguous tile ranges; K-steps are (chunk, tap) with taps inner. The weight
-// slices go through a 3-deep LDS ring issued three steps ahead; the patch of the next chunk
-// (double-buffered) is issued one 16-B slot per thread over the first steps of the current
-// chunk, always ahead of the weight DMA it must precede, so the in-order vmcnt waits that
-// guard the ring also guard the patch. The data gradient is the same kernel on dy with the
-// weight transposed to [Cin][3][3][Cout] and the taps mirrored.
+// Schedule: persistent, one workgroup of 8 waves per CU, XCD-aware contiguous tile ranges;
+// K-steps are (chunk, tap) with taps inner. Workgroup tile 256 pixels x 128 channels; each
+// wave owns 128 pixels x 32 channels and keeps its own weight fragments in registers: a
+// three-deep ring of per-tap fragments loaded from L2 two taps ahead. No wave reads data
+// another wave loads except the patch, so the waves synchronise once per chunk (the patch's
+// double buffer), not once per K-step: two waves share each SIMD and while one stalls the
+// other issues MFMAs. The next chunk's patch is staged through registers (global loads at
+// the chunk start, LDS stores late in the chunk), so every wait is the compiler's own
+// precise count. Each fragment's reads are issued two fragments ahead of their MFMAs, and
+// scheduling barriers keep the compiler from sinking them (or the weight loads) next to
+// their consumers.
+//
+// Weights: in the fragment-native layout (WFRAG, written by weight_frag_kernel from the
+// OHWI e4m3 weight) each per-lane fragment load is one contiguous 1 KB per wave; from the
+// OHWI weight itself each load touches 16 half-used cache lines (measured 6 us slower per
+// cfg2 launch), which the op-level entry without a weight preparation still accepts.
+// Epilogue: the wave's accumulators go through its 8 KB LDS slot and leave as 16-B
+// nontemporal stores of 64-B channel runs (8-B stores straight from the accumulators,
+// nontemporal or not, were 9-17 us slower per launch; plain 16-B stores 2 us slower). The data gradient is the same kernel
+// on dy with the transposed weight and the taps mirrored (baked into its fragment layout).
 #include "dpa_common.hpp"
 
 namespace dpa {
 
 constexpr int kHcThreads = 512;
 constexpr int kHcWaves = kHcThreads / 64;
-constexpr int kHcWavesM = 4;
 constexpr int kHcBM = 256;  // output pixels per tile (TR whole rows)
 constexpr int kHcBN = 128;  // output channels per tile
 constexpr int kHcBK = 128;  // K bytes per step (MFMA depth)
+constexpr int kHcWM = 128;  // pixels per wave
+constexpr int kHcWN = 32;   // channels per wave
+constexpr int kHcPF = kHcWM / 16;                          // pixel fragments per wave (8)
 constexpr int kHcPitch = 144;                              // patch pixel pitch in LDS
 constexpr int kHcPatchSlots = 3072;                        // 16-B slots per patch buffer
 constexpr int kHcPatchBytes = kHcPatchSlots * 16;          // 48 KB >= 340 pixels x 144 B
-constexpr int kHcPatchLoads = kHcPatchSlots / kHcThreads;  // 6 DMAs per thread per patch
-constexpr int kHcBBytes = kHcBN * kHcBK;                   // 16 KB weight slice
-constexpr int kHcBLoads = kHcBBytes / 16 / kHcThreads;     // 2
-constexpr int kHcSlotBytes = 16 * 64 * 2;                  // epilogue: 16 px x 64 ch bf16
+constexpr int kHcPatchLoads = kHcPatchSlots / kHcThreads;  // 6 slots per thread per patch
+constexpr int kHcSlotBytes = kHcWM * kHcWN * 2;            // epilogue: 128 px x 32 ch bf16
+static_assert(kHcWaves == (kHcBM / kHcWM) * (kHcBN / kHcWN), "wave grid");
+static_assert(kHcPatchLoads == 6, "six staging registers");
 
 struct HconvArgs {
   const uint8_t* act;  // [N][H][W][C]
-  const uint8_t* wgt;  // [Cout][3][3][C]
+  const uint8_t* wgt;  // OHWI [Cout][3][3][C], or the fragment layout (weight_frag_kernel)
   uint16_t* out;       // bf16 [N][H][W][Cout]
   const float* sa;
   const float* sb;
@@ -48,36 +61,39 @@ struct HconvArgs {
   int wshift;         // log2(W)
   int KC, nk;         // 128-channel chunks, K-steps per tile (9 * KC)
   int tiles_n, tiles, tiles_per_xcd, wg_per_xcd;
-  int flip;           // 1: data gradient (weight tap 8 - t)
+  int flip;           // OHWI weight only: 1 = data gradient (weight tap 8 - t)
   FastDiv divTN, divKC, divH;
 };
 
 __device__ __attribute__((aligned(64))) uint8_t hc_zero16[64];
 
-// 2 patch buffers + 3 weight stages + per-wave epilogue slots = 96 + 48 + 16 = 160 KB.
+// Two patch buffers (the current chunk's and the next one's) and the per-wave epilogue slots:
+// 96 + 64 = 160 KB, all of the CU's LDS.
 __shared__ __attribute__((aligned(1024))) uint8_t hc_patch[2][kHcPatchBytes];
-__shared__ __attribute__((aligned(1024))) uint8_t hc_b[3][kHcBBytes];
 __shared__ __attribute__((aligned(1024))) uint8_t hc_slot[kHcWaves][kHcSlotBytes];
 
-// Weight rows (aligned 16-row fragments): granule g at g ^ ((r ^ (r >> 3)) & 7).
-__device__ __forceinline__ int hc_bswz(int r) { return (r ^ (r >> 3)) & 7; }
-// Patch pixels sit at a 144-B pitch (128 B of channels + 16 B gap). A fragment starts at any
-// pixel, and measured on gfx950 (SQ_LDS_BANK_CONFLICT) no XOR swizzle is conflict-free at
-// arbitrary starts either (the best one saves a pass only at starts that are multiples of
-// 4); the pitch makes every tap's address the pixel's base plus a wave-uniform offset.
-
-__device__ __forceinline__ v8i hc_frag2(const uint8_t* base, uint32_t a0, uint32_t a1) {
+// Patch pixels sit at a 144-B pitch (128 B of channels + 16 B gap): the 16 pixels of a
+// fragment land on 16 distinct 4-bank groups (36 banks apart mod 64), and every tap's address
+// is the pixel's base plus a wave-uniform offset.
+__device__ __forceinline__ v8i hc_frag2(const uint8_t* base, uint32_t a0) {
   const uint4 lo = *reinterpret_cast<const uint4*>(base + a0);
-  const uint4 hi = *reinterpret_cast<const uint4*>(base + a1);
+  const uint4 hi = *reinterpret_cast<const uint4*>(base + a0 + 16);
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
+__device__ __forceinline__ v8i hc_gload2(const uint8_t* lo_src, const uint8_t* hi_src) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(lo_src);
+  const uint4 hi = *reinterpret_cast<const uint4*>(hi_src);
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+template <bool WFRAG>
 __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % kHcWavesM;  // pixel quarter (64 output pixels)
-  const int wn = wave / kHcWavesM;  // channel half (64 output channels)
+  const int wm = wave & 1;   // pixel half (128 output pixels)
+  const int wn = wave >> 1;  // channel quarter (32 output channels)
   const int frow = lane & 15, fq = lane >> 4;
 
   const int xcd = blockIdx.x & 7;
@@ -90,7 +106,7 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
   const int nchunks = nt * p.KC;
   const float scale = p.sa[0] * p.sb[0];
 
-  // ---- patch DMA slots of this thread: slot e = d * 512 + tid covers LDS bytes [16e, +16):
+  // ---- patch slots of this thread: slot e = d * 512 + tid covers LDS bytes [16e, +16):
   // pixel e / 9 of the patch, granule e % 9 (granule 8 is the pitch gap). Per slot: patch
   // row | (1 << 8 if the slot holds in-image data), and the source offset from the patch
   // origin (pixel (n, y0 - 1, -1) is row 0, column 0).
@@ -106,19 +122,13 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
     prw[d] = pr | (ok << 8);
     pxo[d] = ((pr - 1) * p.W + (pc - 1)) * p.C + g * 16;
   }
-  // weight DMA rows of this thread (relative to the tile's first output channel)
-  int b_row[kHcBLoads];
-#pragma unroll
-  for (int r = 0; r < kHcBLoads; ++r) {
-    const int row = wave * (kHcBN / kHcWaves) + 8 * r + (lane >> 3);
-    b_row[r] = row * 9 * p.C + ((lane & 7) ^ hc_bswz(row)) * 16;
-  }
 
   // per-chunk scalars: chunk g -> tile (m0, n0), channel chunk kc; patch origin and first
   // image row; weight base
   struct Chunk {
     int live, m0, n0, y0, pbase, wbase;
   };
+  const int cb16 = p.Cout >> 4;  // 16-row weight blocks per tap (fragment layout)
   auto chunk_info = [&](int g) __attribute__((always_inline)) {
     Chunk c;
     c.live = g < nchunks;
@@ -132,170 +142,149 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
     const int row0 = c.m0 >> p.wshift;  // global output row n * H + y0
     c.y0 = row0 - (int)fdiv((uint32_t)row0, p.divH) * p.H;
     c.pbase = row0 * p.W * p.C + kc * kHcBK;
-    c.wbase = c.n0 * 9 * p.C + kc * kHcBK;
+    if (WFRAG)  // 2 KB block of (kc, tap 0, this wave's first 16 rows)
+      c.wbase = ((kc * 9) * cb16 + (c.n0 >> 4) + wn * (kHcWN / 16)) * 2048 + lane * 16;
+    else
+      c.wbase = c.n0 * 9 * p.C + kc * kHcBK;
     return c;
   };
 
-  // patch slot d (wave-uniform, 0..5) of chunk c into buffer `buf`; when the chunk is past
-  // the end the slot is filled from the zero page
-  auto issue_patch_slot = [&](const Chunk& c, int d, uint32_t buf) __attribute__((always_inline)) {
-    int pr = prw[0], po = pxo[0];
+  // The patch of chunk c into registers (out-of-image slots and dead chunks read zeros), and
+  // from there into LDS buffer buf. Six named registers with the slot index spelled out: an
+  // array here is indexed before the loops unroll and would be promoted to LDS.
+  uint4 st0, st1, st2, st3, st4, st5;
+#define HC_LD(d, dst, c)                                                                   \
+  {                                                                                        \
+    const int y_ = (c).y0 + (prw[d] & 0xff) - 1;                                           \
+    const bool ok_ = (c).live & ((prw[d] >> 8) != 0) & ((unsigned)y_ < (unsigned)p.H);     \
+    const uint8_t* src_ = ok_ ? p.act + (uint32_t)((c).pbase + pxo[d]) : hc_zero16;        \
+    dst = *reinterpret_cast<const uint4*>(src_);                                           \
+  }
+#define HC_LOAD_PATCH(c) \
+  HC_LD(0, st0, c) HC_LD(1, st1, c) HC_LD(2, st2, c) HC_LD(3, st3, c) HC_LD(4, st4, c) HC_LD(5, st5, c)
+#define HC_ST(d, src, buf) \
+  *reinterpret_cast<uint4*>(&hc_patch[(buf)][((d) * kHcThreads + tid) * 16]) = src;
+#define HC_STORE_PATCH(buf)                                                                \
+  HC_ST(0, st0, buf) HC_ST(1, st1, buf) HC_ST(2, st2, buf) HC_ST(3, st3, buf)              \
+  HC_ST(4, st4, buf) HC_ST(5, st5, buf)
+
+  // weight fragments of (chunk c, tap t) for the wave's two 16-channel blocks: lane
+  // (frow, fq) holds row 16 cb + frow, K bytes [32 fq, +32) of the chunk (L2-resident; the
+  // two pixel halves of a channel quarter read the same lines)
+  int wrow[2];
 #pragma unroll
-    for (int q = 1; q < kHcPatchLoads; ++q) {
-      pr = d == q ? prw[q] : pr;
-      po = d == q ? pxo[q] : po;
-    }
-    const int y = c.y0 + (pr & 0xff) - 1;
-    const bool ok = c.live & ((pr >> 8) != 0) & ((unsigned)y < (unsigned)p.H);
-    const uint8_t* src = ok ? p.act + (uint32_t)(c.pbase + po) : hc_zero16;
-    dma16_lds(src, buf + (uint32_t)((d * kHcThreads + wave * 64) * 16));
-  };
-  // weight slice of (chunk c, tap t) into ring stage st
-  auto issue_b = [&](const Chunk& c, int t, int st) __attribute__((always_inline)) {
-    const int wt = p.flip ? 8 - t : t;
-    const int off = c.wbase + wt * p.C;
-    const uint32_t base = LDS_ADDR(hc_b) + (uint32_t)(st * kHcBBytes) +
-                          (uint32_t)(wave * (kHcBN / kHcWaves) * kHcBK);
+  for (int cb = 0; cb < 2; ++cb) wrow[cb] = (wn * kHcWN + cb * 16 + frow) * 9 * p.C + fq * 32;
+  auto load_w = [&](const Chunk& c, int t, v8i (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < kHcBLoads; ++r) {
-      const uint8_t* src = c.live ? p.wgt + (uint32_t)(off + b_row[r]) : hc_zero16;
-      dma16_lds(src, base + (uint32_t)(8 * r * kHcBK));
+    for (int cb = 0; cb < 2; ++cb) {
+      if (WFRAG) {
+        const uint8_t* src = p.wgt + (uint32_t)(c.wbase + (t * cb16 + cb) * 2048);
+        w[cb] = hc_gload2(src, src + 1024);
+      } else {
+        const int tap = p.flip ? 8 - t : t;
+        const uint8_t* src = p.wgt + (uint32_t)(c.wbase + wrow[cb] + tap * p.C);
+        w[cb] = hc_gload2(src, src + 16);
+      }
     }
   };
 
-  // ---- compute side ----
-  // A fragment: lane (frow, fq) of pixel fragment pj reads patch pixel centre + tap offset,
-  // granules 2 fq and 2 fq + 1; base address per pj, plus (dy * PC + dx) * 144 per tap
-  uint32_t abase[4];
+  // pixel fragment pf: lane (frow, fq) reads patch pixel centre + tap offset, granules 2 fq
+  // and 2 fq + 1; base address per pf, plus (dy * PC + dx) * 144 per tap
+  uint32_t abase[kHcPF];
 #pragma unroll
-  for (int pj = 0; pj < 4; ++pj) {
-    const int m = wm * 64 + pj * 16 + frow;
+  for (int pf = 0; pf < kHcPF; ++pf) {
+    const int m = wm * kHcWM + pf * 16 + frow;
     const int orow = m >> p.wshift, ocol = m & (p.W - 1);
-    abase[pj] = (uint32_t)(((orow + 1) * p.PC + ocol + 1) * kHcPitch + 32 * fq);
+    abase[pf] = (uint32_t)(((orow + 1) * p.PC + ocol + 1) * kHcPitch + 32 * fq);
   }
-  uint32_t b_addr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = wn * 64 + i * 16 + frow;
-    b_addr[i] = (uint32_t)(row * kHcBK + (((2 * fq) ^ hc_bswz(row)) * 16));
-  }
+  auto tap_off = [&](int t) __attribute__((always_inline)) {
+    const int ty = t / 3, tx = t - 3 * ty;
+    return (uint32_t)(((ty - 1) * p.PC + tx - 1) * kHcPitch);
+  };
 
-  v4f acc[4][4];
+  v4f acc[2][kHcPF];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  v8i fa[4], fb[4];
+    for (int j = 0; j < kHcPF; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // Epilogue per finished tile: bf16(RN32(acc * RN32(sa * sb)) [+ bias]) staged through the
-  // wave's LDS slot into 128-B rows and written with nontemporal stores (measured 2.3 us
-  // faster per cfg2 launch than plain stores, whose write-backs delayed the next loads).
+  // Epilogue per finished tile: bf16(RN32(acc * RN32(sa * sb)) [+ bias]). Lane (frow, fq)
+  // of block (cb, pf) holds channels 16 cb + 4 fq .. + 3 of pixel 16 pf + frow: all of them
+  // go into the wave's slot [128 px][64 B] first (granule g of row r at g ^ ((r >> 2) & 3):
+  // conflict-free both ways), then lane l reads pixel 16 pf + l / 4, granule l % 4 and stores
+  // 16 B nontemporally; a store instruction covers 16 pixels x 64 B. All writes before any
+  // read, so the LDS latency is paid once per tile, not once per fragment.
+  uint8_t* slot = hc_slot[wave];
   auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
-    uint8_t* slot = hc_slot[wave];
-    const int c0 = n0 + wn * 64;
 #pragma unroll
-    for (int pj = 0; pj < 4; ++pj) {
+    for (int pf = 0; pf < kHcPF; ++pf) {
 #pragma unroll
-      for (int ci = 0; ci < 4; ++ci) {
+      for (int cb = 0; cb < 2; ++cb) {
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[ci][pj][e] * scale;
+        for (int e = 0; e < 4; ++e) v[e] = acc[cb][pf][e] * scale;
         if (p.bias) {
+          const int c = n0 + wn * kHcWN + cb * 16 + 4 * fq;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[c0 + ci * 16 + 4 * fq + e];
+          for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[c + e];
         }
-        const int g = 2 * ci + (fq >> 1);
-        uint2 o;
-        o.x = pack_bf16x2(v[0], v[1]);
-        o.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(slot + frow * 128 + ((g ^ (frow & 7)) * 16) + (fq & 1) * 8) = o;
-      }
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int c = lane + 64 * rr;
-        const int r = c >> 3, g = c & 7;
-        const uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((g ^ (r & 7)) * 16));
-        const int m = m0 + wm * 64 + pj * 16 + r;
-        st_nt16(p.out + (uint32_t)(m * p.Cout + c0 + g * 8), v);
+        const int r = pf * 16 + frow, g = cb * 2 + (fq >> 1);
+        *reinterpret_cast<uint2*>(slot + r * 64 + ((g ^ ((r >> 2) & 3)) * 16) + (fq & 1) * 8) =
+            uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        acc[cb][pf] = v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
+    const int g_rd = lane & 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int pf = 0; pf < kHcPF; ++pf) {
+      const int r = pf * 16 + (lane >> 2);
+      const uint4 o = *reinterpret_cast<const uint4*>(slot + r * 64 + ((g_rd ^ ((r >> 2) & 3)) * 16));
+      st_nt16(p.out + (uint32_t)((m0 + wm * kHcWM + r) * p.Cout + n0 + wn * kHcWN + g_rd * 8), o);
+    }
   };
 
-  const uint32_t patch0 = LDS_ADDR(hc_patch);
-  auto patch_buf = [&](int g) { return patch0 + (uint32_t)((g & 1) * kHcPatchBytes); };
-
-  // ---- prologue: patch of chunk 0; weight stages 0..2 with one duplicate patch slot
-  // before the last, so every step finds three DMAs issued after the stage it waits for ----
+  // ---- prologue: patch of chunk 0 and the weights of its first two taps ----
   Chunk cc = chunk_info(0);   // current chunk
   Chunk cn = chunk_info(1);   // next chunk
-#pragma unroll
-  for (int d = 0; d < kHcPatchLoads; ++d) issue_patch_slot(cc, d, patch_buf(0));
-  issue_b(cc, 0, 0);
-  issue_b(cc, 1, 1);
-  issue_patch_slot(cc, 0, patch_buf(0));  // duplicate of a landed-or-landing slot: same bytes
-  issue_b(cc, 2, 2);
-  wait_vmcnt<2 * kHcBLoads + 1>();  // patch 0 and stage 0 landed
-  lds_barrier();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) fb[i] = hc_frag2(hc_b[0], b_addr[i], b_addr[i] ^ 16u);
-  {
-    const uint32_t off = (uint32_t)(-(p.PC + 1) * kHcPitch);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = hc_frag2(hc_patch[0], abase[i] + off, abase[i] + off + 16);
-  }
+  v8i w0[2], w1[2], w2[2];    // weight ring: taps with t % 3 == 0, 1, 2
+  HC_LOAD_PATCH(cc)
+  load_w(cc, 0, w0);
+  load_w(cc, 1, w1);
+  HC_STORE_PATCH(0)
 
-  // Step (chunk gc, tap t), weight stage t % 3 (nine taps per chunk): wait until the next
-  // step's stage landed (the last three DMAs may still fly), barrier, the 16 MFMAs of this
-  // step interleaved with the next step's fragment reads, then queue patch slot t of chunk
-  // gc+1 (a duplicate of slot 0 for t >= 6) and the weight slice three steps ahead.
   for (int gc = 0; gc < nchunks; ++gc) {
+    // this chunk's patch is complete (own stores done, then every wave's); every wave is
+    // past the previous chunk, so the other buffer is free for the next patch
+    wait_lgkmcnt0();
+    lds_barrier();
+    HC_LOAD_PATCH(cn)
+    const uint8_t* pa = hc_patch[gc & 1];
+    v8i fa[3];
+    fa[0] = hc_frag2(pa, abase[0] + tap_off(0));
+    fa[1] = hc_frag2(pa, abase[1] + tap_off(0));
+#pragma unroll
     for (int t = 0; t < 9; ++t) {
-      // the weight-fragment reads of the previous step (from the stage the DMAs below
-      // refill) must be done; the two reads of the last A fragment, issued after them and
-      // from a patch buffer no DMA of this step touches, may still be in flight
-      wait_vmcnt<kHcBLoads + 1>();
-      wait_lgkmcnt<2>();
-      lds_barrier();
-      const int t1 = t == 8 ? 0 : t + 1;
-      const int ty1 = t1 >= 6 ? 2 : (t1 >= 3 ? 1 : 0);
-      const uint32_t aoff = (uint32_t)(((ty1 - 1) * p.PC + (t1 - 3 * ty1) - 1) * kHcPitch);
-      const uint8_t* pa = hc_patch[(t == 8 ? gc + 1 : gc) & 1];
-      const int st = t - (t >= 6 ? 6 : (t >= 3 ? 3 : 0));  // t % 3
-      const int st1 = st == 2 ? 0 : st + 1;
-      const uint8_t* pb = hc_b[st1];
-      // pixel fragments 0..2: 4 MFMAs each, then the next step's A fragment in its place;
-      // the DMAs of this step go out after the first group
+      v8i(&wc)[2] = t % 3 == 0 ? w0 : (t % 3 == 1 ? w1 : w2);
+      v8i(&wp)[2] = t % 3 == 0 ? w2 : (t % 3 == 1 ? w0 : w1);
+      // the weights of the step two ahead (this chunk's tap t + 2, or the next chunk's);
+      // each stage below is closed by a scheduling barrier, so the loads stay two taps and
+      // the fragment reads two stages ahead of their use
+      if (t < 7)
+        load_w(cc, t + 2, wp);
+      else
+        load_w(cn, t - 7, wp);
 #pragma unroll
-      for (int pj = 0; pj < 3; ++pj) {
-#pragma unroll
-        for (int ci = 0; ci < 4; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
-        const uint32_t a0 = abase[pj] + aoff;
-        fa[pj] = hc_frag2(pa, a0, a0 + 16);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
-        if (pj == 0) {
-          issue_patch_slot(cn, t < kHcPatchLoads ? t : 0, patch_buf(gc + 1));
-          if (t < 6)
-            issue_b(cc, t + 3, st);
-          else
-            issue_b(cn, t - 6, st);
-        }
+      for (int pf = 0; pf < kHcPF; ++pf) {
+        const int f = t * kHcPF + pf;
+        const int f2 = f + 2;
+        if (f2 < 9 * kHcPF)
+          fa[f2 % 3] = hc_frag2(pa, abase[f2 % kHcPF] + tap_off(f2 / kHcPF));
+        acc[0][pf] = mfma16x16x128_e4m3(wc[0], fa[f % 3], acc[0][pf]);
+        acc[1][pf] = mfma16x16x128_e4m3(wc[1], fa[f % 3], acc[1][pf]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // pixel fragment 3: each weight fragment's last use, then its next-step reload
-#pragma unroll
-      for (int ci = 0; ci < 4; ++ci) {
-        acc[ci][3] = mfma16x16x128_e4m3(fb[ci], fa[3], acc[ci][3]);
-        fb[ci] = hc_frag2(pb, b_addr[ci], b_addr[ci] ^ 16u);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
-      }
-      {
-        const uint32_t a0 = abase[3] + aoff;
-        fa[3] = hc_frag2(pa, a0, a0 + 16);
+      if (t == 6) {
+        HC_STORE_PATCH((gc + 1) & 1)
       }
     }
     const int j = (int)fdiv((uint32_t)gc, p.divKC);
@@ -303,7 +292,45 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
     cc = cn;
     cn = chunk_info(gc + 2);
   }
-  wait_vmcnt<0>();  // trailing DMAs land before the workgroup retires
+#undef HC_LD
+#undef HC_LOAD_PATCH
+#undef HC_ST
+#undef HC_STORE_PATCH
+}
+
+// Fragment-native weight layout for hconv_fp8_kernel<true>: 2 KB blocks, block
+// (kc * T + t) * (rows / 16) + rb holds, at byte half * 1024 + lane * 16 + b, row
+// 16 rb + (lane & 15), K byte 128 kc + 32 (lane >> 4) + 16 half + b of tap t. The forward
+// weight is read as [rows = Cout][T][K = Cin] (OHWI); the data gradient's as the transpose
+// with the taps mirrored: row ci, K co, tap t <- w[co][T - 1 - t][ci]. One thread per 16 B.
+__global__ __launch_bounds__(256) void weight_frag_kernel(const uint8_t* __restrict__ w,
+                                                          uint8_t* __restrict__ out, int rows,
+                                                          int K, int T, int transpose) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-B unit
+  const int64_t units = (int64_t)rows * K * T / 16;
+  if (i >= units) return;
+  const int lane = (int)(i & 63), half = (int)((i >> 6) & 1);
+  const int64_t blk = i >> 7;
+  const int nrb = rows >> 4;
+  const int rb = (int)(blk % nrb);
+  const int64_t kt = blk / nrb;
+  const int t = (int)(kt % T), kc = (int)(kt / T);
+  const int row = rb * 16 + (lane & 15);
+  const int k0 = kc * 128 + (lane >> 4) * 32 + half * 16;
+  uint4 v;
+  if (!transpose) {
+    v = *reinterpret_cast<const uint4*>(w + ((int64_t)row * T + t) * K + k0);
+  } else {
+    const int ts = T - 1 - t;
+    uint32_t b[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) b[j] = w[((int64_t)(k0 + j) * T + ts) * rows + row];
+    v.x = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    v.y = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    v.z = b[8] | (b[9] << 8) | (b[10] << 16) | (b[11] << 24);
+    v.w = b[12] | (b[13] << 8) | (b[14] << 16) | (b[15] << 24);
+  }
+  *reinterpret_cast<uint4*>(out + i * 16) = v;
 }
 
 static bool hconv_shape_ok(int N, int H, int W, int C, int Cout) {
@@ -318,7 +345,7 @@ static bool hconv_shape_ok(int N, int H, int W, int C, int Cout) {
 
 static int hconv_launch(const void* act, const void* wgt, const float* sa, const float* sb,
                         const float* bias, void* out, int N, int H, int W, int C, int Cout,
-                        int flip, int num_cus, hipStream_t s) {
+                        int flip, int wfrag, int num_cus, hipStream_t s) {
   HconvArgs a{};
   a.act = (const uint8_t*)act;
   a.wgt = (const uint8_t*)wgt;
@@ -344,7 +371,10 @@ static int hconv_launch(const void* act, const void* wgt, const float* sa, const
   a.divTN = make_fastdiv((uint32_t)a.tiles_n);
   a.divKC = make_fastdiv((uint32_t)a.KC);
   a.divH = make_fastdiv((uint32_t)H);
-  hconv_fp8_kernel<<<(unsigned)grid, kHcThreads, 0, s>>>(a);
+  if (wfrag)
+    hconv_fp8_kernel<true><<<(unsigned)grid, kHcThreads, 0, s>>>(a);
+  else
+    hconv_fp8_kernel<false><<<(unsigned)grid, kHcThreads, 0, s>>>(a);
   return launch_status();
 }
 
@@ -355,9 +385,22 @@ namespace dpa {
 bool hconv_supported(int N, int H, int W, int C, int Cout) {
   return hconv_shape_ok(N, H, W, C, Cout);
 }
+// wgt: the OHWI weight (flip = 1: the data gradient's transposed weight, taps mirrored), or
+// with wfrag = 1 the fragment layout of weight_frag_run (taps already in consumption order).
 int hconv_run(const void* act, const void* wgt, const float* sa, const float* sb,
               const float* bias, void* out, int N, int H, int W, int C, int Cout, int flip,
-              int num_cus, hipStream_t s) {
-  return hconv_launch(act, wgt, sa, sb, bias, out, N, H, W, C, Cout, flip, num_cus, s);
+              int wfrag, int num_cus, hipStream_t s) {
+  return hconv_launch(act, wgt, sa, sb, bias, out, N, H, W, C, Cout, flip, wfrag, num_cus, s);
+}
+// Fragment layout of an e4m3 weight w: [rows][T][K] (transpose = 0) or, for the data
+// gradient, [K][T][rows] read transposed with the taps mirrored (transpose = 1).
+// rows % 16 == 0, K % 128 == 0.
+int weight_frag_run(const void* w, void* out, int rows, int K, int T, int transpose,
+                    hipStream_t s) {
+  if (rows % 16 != 0 || K % 128 != 0 || T <= 0) return DPA_ERR_SHAPE;
+  const int64_t units = (int64_t)rows * K * T / 16;
+  weight_frag_kernel<<<(unsigned)ceil_div(units, 256), 256, 0, s>>>(
+      (const uint8_t*)w, (uint8_t*)out, rows, K, T, transpose);
+  return launch_status();
 }
 }  // namespace dpa

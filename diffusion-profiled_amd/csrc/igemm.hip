@@ -470,7 +470,9 @@ static void fill_common(IgemmArgs& a, const void* act, const void* wgt, void* ou
 bool hconv_supported(int N, int H, int W, int C, int Cout);
 int hconv_run(const void* act, const void* wgt, const float* sa, const float* sb,
               const float* bias, void* out, int N, int H, int W, int C, int Cout, int flip,
-              int num_cus, hipStream_t s);
+              int wfrag, int num_cus, hipStream_t s);
+int weight_frag_run(const void* w, void* out, int rows, int K, int T, int transpose,
+                    hipStream_t s);
 
 static bool use_hconv(int N, int H, int W, int C, int Cout, int R, int S, int stride, int pad) {
   return R == 3 && S == 3 && stride == 1 && pad == 1 && hconv_supported(N, H, W, C, Cout);
@@ -495,8 +497,9 @@ static int conv_fwd(const void* xq, const void* wq, const float* xs, const float
                     const float* bias, void* y, int N, int H, int W, int Cin, int Cout, int R,
                     int S, int stride, int pad, hipStream_t s, void* workspace = nullptr,
                     int64_t workspace_bytes = 0) {
-  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad))
-    return hconv_run(xq, wq, xs, ws, bias, y, N, H, W, Cin, Cout, 0, num_cus(), s);
+  // the halo-patch kernel's epilogue stores 16 B per lane
+  if (use_hconv(N, H, W, Cin, Cout, R, S, stride, pad) && aligned(y, 16))
+    return hconv_run(xq, wq, xs, ws, bias, y, N, H, W, Cin, Cout, 0, 0, num_cus(), s);
   IgemmArgs a{};
   fill_common(a, xq, wq, y, xs, ws, bias);
   fwd_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad);
@@ -543,8 +546,8 @@ static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const f
                       int stride, int pad, hipStream_t s, void* workspace = nullptr,
                       int64_t workspace_bytes = 0) {
   // the 3x3 / s1 / p1 data gradient is a conv of dy with the mirrored, transposed weight
-  if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad))
-    return hconv_run(dyq, wt, dys, ws, nullptr, dx, N, H, W, Cout, Cin, 1, num_cus(), s);
+  if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad) && aligned(dx, 16))
+    return hconv_run(dyq, wt, dys, ws, nullptr, dx, N, H, W, Cout, Cin, 1, 0, num_cus(), s);
   for (int ay = 0; ay < stride; ++ay)
     for (int ax = 0; ax < stride; ++ax) {
       IgemmArgs a{};
@@ -621,10 +624,57 @@ extern "C" int dpa_conv2d_dgrad_fp8(const void* dyq, const void* wq, const float
   if (!workspace || workspace_bytes < dpa_conv2d_dgrad_workspace_bytes(Cin, Cout, R, S))
     return DPA_ERR_WORKSPACE;
   if (!aligned(dyq, 16) || !aligned(workspace, 16) || !aligned(dx, 8)) return DPA_ERR_ALIGN;
+  if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad) && aligned(dx, 16)) {
+    // the halo-patch kernel takes the transposed, mirrored weight in its fragment layout
+    int st = weight_frag_run(wq, workspace, Cin, Cout, R * S, 1, (hipStream_t)stream);
+    if (st != DPA_OK) return st;
+    return hconv_run(dyq, workspace, dy_scale, w_scale, nullptr, dx, N, H, W, Cout, Cin, 0, 1,
+                     num_cus(), (hipStream_t)stream);
+  }
   int st = dpa_weight_transpose_fp8(wq, workspace, Cout, R, S, Cin, stream);
   if (st != DPA_OK) return st;
   return conv_dgrad(dyq, workspace, dy_scale, w_scale, dx, N, H, W, Cin, Cout, R, S, stride,
                     pad, (hipStream_t)stream);
+}
+
+// ---- fragment-native weights for the 3x3 / stride-1 / pad-1 halo-patch kernel ----
+
+extern "C" int64_t dpa_weight_frag_bytes(int Cout, int R, int S, int Cin) {
+  if (Cout <= 0 || Cin <= 0 || R <= 0 || S <= 0) return 0;
+  return (int64_t)Cout * R * S * Cin;
+}
+
+extern "C" int dpa_weight_frag_fp8(const void* wq, void* wf, void* wf_dgrad, int Cout, int R,
+                                   int S, int Cin, void* stream) {
+  if (!wq || (!wf && !wf_dgrad)) return DPA_ERR_NULL;
+  if (Cout <= 0 || Cin <= 0 || R <= 0 || S <= 0) return DPA_ERR_SIZE;
+  if (Cout % kBN != 0 || Cin % kBK != 0) return DPA_ERR_SHAPE;
+  if (!aligned(wq, 16) || !aligned(wf, 16) || !aligned(wf_dgrad, 16)) return DPA_ERR_ALIGN;
+  int st = DPA_OK;
+  if (wf) st = weight_frag_run(wq, wf, Cout, Cin, R * S, 0, (hipStream_t)stream);
+  if (st == DPA_OK && wf_dgrad)
+    st = weight_frag_run(wq, wf_dgrad, Cin, Cout, R * S, 1, (hipStream_t)stream);
+  return st;
+}
+
+extern "C" int dpa_conv2d_fwd_fp8_wf(const void* xq, const void* wf, const float* x_scale,
+                                     const float* w_scale, const float* bias, void* y, int N,
+                                     int H, int W, int Cin, int Cout, void* stream) {
+  if (!xq || !wf || !x_scale || !w_scale || !y) return DPA_ERR_NULL;
+  if (!use_hconv(N, H, W, Cin, Cout, 3, 3, 1, 1)) return DPA_ERR_SHAPE;
+  if (!aligned(xq, 16) || !aligned(wf, 16) || !aligned(y, 16)) return DPA_ERR_ALIGN;
+  return hconv_run(xq, wf, x_scale, w_scale, bias, y, N, H, W, Cin, Cout, 0, 1, num_cus(),
+                   (hipStream_t)stream);
+}
+
+extern "C" int dpa_conv2d_dgrad_fp8_wf(const void* dyq, const void* wf_dgrad,
+                                       const float* dy_scale, const float* w_scale, void* dx,
+                                       int N, int H, int W, int Cin, int Cout, void* stream) {
+  if (!dyq || !wf_dgrad || !dy_scale || !w_scale || !dx) return DPA_ERR_NULL;
+  if (!use_hconv(N, H, W, Cout, Cin, 3, 3, 1, 1)) return DPA_ERR_SHAPE;
+  if (!aligned(dyq, 16) || !aligned(wf_dgrad, 16) || !aligned(dx, 16)) return DPA_ERR_ALIGN;
+  return hconv_run(dyq, wf_dgrad, dy_scale, w_scale, nullptr, dx, N, H, W, Cout, Cin, 0, 1,
+                   num_cus(), (hipStream_t)stream);
 }
 
 extern "C" int dpa_gemm_fp8(const void* a, const void* b, const float* a_scale,

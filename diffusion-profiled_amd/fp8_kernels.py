@@ -326,6 +326,62 @@ def conv2d_fp8_dgrad_general(
     return dx
 
 
+def hconv_shape(batch: int, cin: int, cout: int, height: int, width: int, k: int = 3,
+                stride: int = 1, padding: int = 1) -> bool:
+    """Shapes of the halo-patch conv kernel (3x3, stride 1, pad 1, images 16 or 32 pixels
+    wide with whole 256-pixel row groups, channels multiples of 128): the only shapes the
+    fragment-layout weight entries (dpa_conv2d_*_fp8_wf) accept."""
+    return (k == 3 and stride == 1 and padding == 1 and width in (16, 32)
+            and height % (256 // width) == 0 and cin % 128 == 0 and cout % 128 == 0
+            and batch * height * width * max(cin, cout) < 2**31)
+
+
+def weight_frag_fp8(weight: torch.Tensor, forward: bool = True, dgrad: bool = True):
+    """The fragment-native layouts of an OHWI e4m3 weight for the halo-patch conv: (forward,
+    data gradient), flat uint8 tensors (either None when not asked for)."""
+    assert weight.dtype == FP8_DTYPE
+    weight = _nhwc(weight)
+    cout, cin, kh, kw = weight.shape
+    n = weight.numel()
+    wf = torch.empty(n, device=weight.device, dtype=torch.uint8) if forward else None
+    wt = torch.empty(n, device=weight.device, dtype=torch.uint8) if dgrad else None
+    _lib.call("dpa_weight_frag_fp8", weight.data_ptr(), _ptr(wf), _ptr(wt), cout, kh, kw, cin,
+              _stream(weight))
+    return wf, wt
+
+
+def conv2d_fp8_fwd_wf(x: torch.Tensor, wf: torch.Tensor, x_scale: torch.Tensor,
+                      weight_scale: torch.Tensor, cout: int,
+                      bias: torch.Tensor | None = None) -> torch.Tensor:
+    """The 3x3 / stride-1 / pad-1 forward with the weight in its fragment layout
+    (weight_frag_fp8): the same values as conv2d_fp8_fwd_general."""
+    assert x.dtype == FP8_DTYPE and wf.dtype == torch.uint8 and wf.is_contiguous()
+    x = _nhwc(x)
+    batch, cin, height, width = x.shape
+    assert wf.numel() == cout * 9 * cin and hconv_shape(batch, cin, cout, height, width)
+    y = torch.empty((batch, cout, height, width), device=x.device, dtype=torch.bfloat16,
+                    memory_format=torch.channels_last)
+    _lib.call("dpa_conv2d_fwd_fp8_wf", x.data_ptr(), wf.data_ptr(), x_scale.data_ptr(),
+              weight_scale.data_ptr(), _ptr(bias), y.data_ptr(), batch, height, width, cin, cout,
+              _stream(x))
+    return y
+
+
+def conv2d_fp8_dgrad_wf(dy: torch.Tensor, wf_dgrad: torch.Tensor, dy_scale: torch.Tensor,
+                        weight_scale: torch.Tensor, cin: int) -> torch.Tensor:
+    """The 3x3 / stride-1 / pad-1 data gradient with the weight in its data-gradient fragment
+    layout (weight_frag_fp8): the same values as conv2d_fp8_dgrad_general."""
+    assert dy.dtype == FP8_DTYPE and wf_dgrad.dtype == torch.uint8 and wf_dgrad.is_contiguous()
+    dy = _nhwc(dy)
+    batch, cout, height, width = dy.shape
+    assert wf_dgrad.numel() == cout * 9 * cin and hconv_shape(batch, cin, cout, height, width)
+    dx = torch.empty((batch, cin, height, width), device=dy.device, dtype=torch.bfloat16,
+                     memory_format=torch.channels_last)
+    _lib.call("dpa_conv2d_dgrad_fp8_wf", dy.data_ptr(), wf_dgrad.data_ptr(), dy_scale.data_ptr(),
+              weight_scale.data_ptr(), dx.data_ptr(), batch, height, width, cin, cout, _stream(dy))
+    return dx
+
+
 def weight_transpose_fp8(weight: torch.Tensor) -> torch.Tensor:
     """[Cout][R][S][Cin] e4m3 bytes -> [Cin][R][S][Cout] (the data-gradient operand)."""
     assert weight.dtype == FP8_DTYPE

@@ -120,6 +120,31 @@ int dpa_conv2d_fwd_fp8(const void* xq, const void* wq, const float* x_scale,
                        const float* w_scale, const float* bias, void* y, int N, int H, int W,
                        int Cin, int Cout, int R, int S, int stride, int pad, void* stream);
 
+/* Fragment-native e4m3 weights for the 3x3 / stride-1 / pad-1 convolutions of 16- or
+ * 32-pixel-wide images (the U-Net's 32x32 and 16x16 levels): the layout the conv kernel's
+ * per-wave weight loads read as contiguous 1 KB runs, so a weight's bytes are re-laid once
+ * per weight update instead of being gathered per K-step. wf: the forward weight; wf_dgrad:
+ * the data gradient's (transposed, taps mirrored). Same bytes as the OHWI weight, permuted:
+ * 2 KB blocks, block (kc * R*S + t) * (rows / 16) + rb holds at byte h * 1024 + l * 16 + b
+ * row 16 rb + (l % 16), K byte 128 kc + 32 (l / 16) + 16 h + b of tap t, where forward rows
+ * are Cout and K is Cin (w[co][t][ci]) and data-gradient rows are Cin and K is Cout
+ * (w[co][R*S-1-t][ci]). Either output may be NULL. Cin, Cout multiples of 128.
+ * No reference counterpart: it replaces the per-call weight transpose the data gradient
+ * needs (transpose_fp8_2d's role for dy, diffusion/fp8_kernels.py:321-337, applied to w). */
+int64_t dpa_weight_frag_bytes(int Cout, int R, int S, int Cin);
+int dpa_weight_frag_fp8(const void* wq, void* wf, void* wf_dgrad, int Cout, int R, int S,
+                        int Cin, void* stream);
+
+/* dpa_conv2d_fwd_fp8 / dpa_conv2d_dgrad_fp8 for R = S = 3, stride 1, pad 1, W in {16, 32},
+ * H a multiple of 256 / W, with the weight in its fragment layout (dpa_weight_frag_fp8):
+ * identical results. Other shapes return DPA_ERR_SHAPE. y / dx 16-B aligned. */
+int dpa_conv2d_fwd_fp8_wf(const void* xq, const void* wf, const float* x_scale,
+                          const float* w_scale, const float* bias, void* y, int N, int H,
+                          int W, int Cin, int Cout, void* stream);
+int dpa_conv2d_dgrad_fp8_wf(const void* dyq, const void* wf_dgrad, const float* dy_scale,
+                            const float* w_scale, void* dx, int N, int H, int W, int Cin,
+                            int Cout, void* stream);
+
 /* Bytes of workspace dpa_conv2d_dgrad_fp8 needs (the transposed weight, Cout*R*S*Cin). */
 int64_t dpa_conv2d_dgrad_workspace_bytes(int Cin, int Cout, int R, int S);
 

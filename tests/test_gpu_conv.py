@@ -252,3 +252,89 @@ def test_split_k_gemm_and_linear_dgrad(K):
                            (dx1, dx_ref, "dgrad single")):
         frac = assert_bf16_close(bits(got.cpu()), ref, name)
         assert frac > 0.97, (name, frac)
+
+
+def frag_layout_reference(wq_ohwi: np.ndarray, transpose: bool) -> np.ndarray:
+    """The fragment-native weight layout restated with numpy from its definition: 2 KB blocks,
+    block (kc * T + t) * (rows / 16) + rb holds at byte h * 1024 + l * 16 + b row 16 rb + l % 16,
+    K byte 128 kc + 32 (l // 16) + 16 h + b of tap t; forward rows = Cout, K = Cin; data
+    gradient rows = Cin, K = Cout with the taps mirrored."""
+    cout, kh, kw, cin = wq_ohwi.shape
+    t_ = kh * kw
+    w = wq_ohwi.reshape(cout, t_, cin)
+    if transpose:
+        w = w[:, ::-1, :].transpose(2, 1, 0)      # [Cin][T][Cout], taps mirrored
+    rows, _, k = w.shape
+    # [rows, T, K] -> [kc, t, rb, h, fq, frow, b]
+    v = w.reshape(rows // 16, 16, t_, k // 128, 4, 2, 16)   # rb, frow, t, kc, fq, h, b
+    v = v.transpose(3, 2, 0, 5, 4, 1, 6)                      # kc, t, rb, h, fq, frow, b
+    return np.ascontiguousarray(v).reshape(-1)
+
+
+@pytest.mark.parametrize("cout,cin", [(128, 128), (256, 128), (256, 512), (128, 256)])
+def test_weight_frag_layout_bytes(cout, cin):
+    """dpa_weight_frag_fp8 permutes the OHWI e4m3 bytes into the fragment layout (forward)
+    and the transposed, mirrored one (data gradient), bit for bit."""
+    L = dpa_mod("_lib")
+    rng = np.random.default_rng(cout + cin)
+    wq = rng.integers(0, 256, size=(cout, 3, 3, cin), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0   # no NaN codes needed; the layout only moves bytes
+    d = torch.from_numpy(wq.copy()).cuda()
+    wf = torch.empty(d.numel(), dtype=torch.uint8, device="cuda")
+    wt = torch.empty_like(wf)
+    assert L.query("dpa_weight_frag_bytes", cout, 3, 3, cin) == d.numel()
+    L.call("dpa_weight_frag_fp8", d.data_ptr(), wf.data_ptr(), wt.data_ptr(), cout, 3, 3, cin,
+           torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(wf.cpu().numpy(), frag_layout_reference(wq, False))
+    np.testing.assert_array_equal(wt.cpu().numpy(), frag_layout_reference(wq, True))
+
+
+HCONV_SHAPES = [(128, 128, 32, 32), (128, 256, 32, 32), (256, 256, 16, 16), (512, 256, 16, 16),
+                (512, 128, 32, 32), (256, 256, 32, 32)]
+
+
+@pytest.mark.parametrize("shape", HCONV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fragment_weight_convs_vs_oracle(K, shape):
+    """dpa_conv2d_fwd_fp8_wf / dpa_conv2d_dgrad_fp8_wf with the weight prepared by
+    dpa_weight_frag_fp8: against the exact oracle, and bit-identical to the OHWI entries
+    (the same kernel arithmetic; only the weight fetch differs)."""
+    L = dpa_mod("_lib")
+    cin, cout, h, w = shape
+    n = 2
+    xq, xs, wq, ws, dyq, dys = quantized_inputs(K, n, cin, cout, h, w, seed=sum(shape) + 7)
+    stream = torch.cuda.current_stream().cuda_stream
+    wf = torch.empty(wq.numel(), dtype=torch.uint8, device="cuda")
+    wt = torch.empty_like(wf)
+    L.call("dpa_weight_frag_fp8", wq.data_ptr(), wf.data_ptr(), wt.data_ptr(), cout, 3, 3, cin,
+           stream)
+    y = torch.empty((n, cout, h, w), dtype=torch.bfloat16, device="cuda",
+                    memory_format=torch.channels_last)
+    dx = torch.empty((n, cin, h, w), dtype=torch.bfloat16, device="cuda",
+                     memory_format=torch.channels_last)
+    L.call("dpa_conv2d_fwd_fp8_wf", xq.data_ptr(), wf.data_ptr(), xs.data_ptr(), ws.data_ptr(),
+           None, y.data_ptr(), n, h, w, cin, cout, stream)
+    L.call("dpa_conv2d_dgrad_fp8_wf", dyq.data_ptr(), wt.data_ptr(), dys.data_ptr(),
+           ws.data_ptr(), dx.data_ptr(), n, h, w, cin, cout, stream)
+    y_ohwi = K.conv2d_fwd_fp8_prequantized(xq, wq, xs, ws)
+    dx_ohwi = K.conv2d_bwd_input_fp8_prequantized(dyq, wq, dys, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_ohwi.view(torch.int16))
+    assert torch.equal(dx.view(torch.int16), dx_ohwi.view(torch.int16))
+    xb, wb, db = (nhwc_bits(t.cpu().view(torch.uint8)) for t in (xq, wq, dyq))
+    tag = f"{shape}"
+    e1 = assert_bf16_close(nhwc_bits(y.cpu()), O.conv2d_fwd(xb, wb, f32(xs), f32(ws)), "fwd_wf " + tag)
+    e2 = assert_bf16_close(nhwc_bits(dx.cpu()), O.conv2d_dgrad(db, wb, f32(dys), f32(ws), (h, w)),
+                           "dgrad_wf " + tag)
+    assert min(e1, e2) > 0.97, (e1, e2)
+
+
+def test_fragment_weight_entries_refuse_other_shapes():
+    """The _wf entries serve only the halo-patch shapes (W 16 or 32, rows a multiple of
+    256 / W); other shapes and misaligned outputs return an error before any launch."""
+    L = dpa_mod("_lib").load(build_if_missing=False)
+    fake, nul = 0x1000, None
+    assert L.dpa_conv2d_fwd_fp8_wf(fake, fake, fake, fake, nul, fake, 2, 8, 8, 256, 256, nul) == -4
+    assert L.dpa_conv2d_dgrad_fp8_wf(fake, fake, fake, fake, fake, 2, 12, 32, 128, 128, nul) == -4
+    assert L.dpa_conv2d_fwd_fp8_wf(fake, fake, fake, fake, nul, 0x1008, 2, 32, 32, 128, 128, nul) == -3
+    assert L.dpa_weight_frag_fp8(fake, fake, nul, 100, 3, 3, 128, nul) == -4
