@@ -101,16 +101,15 @@ class ConvWorkload:
     def quantize(self):
         """x and dy: quantize_fp8 (amax + cast each). The weight: its e4m3 copy, scale and the
         data gradient's transposed copy in one grouped weight preparation (two launches, in
-        place of quantize_fp8's two and the transpose)."""
+        place of quantize_fp8's two and the transpose); for the halo-patch kernel's shapes both
+        copies are written in its fragment layouts."""
         K = self.K
         if self.wprep is None:
             WP = importlib.import_module("diffusion-profiled_amd.weight_prep")
-            self.wprep = WP.TensorPrep([self.wt])
+            self.wprep = WP.TensorPrep([self.wt], frag=[self.frag])
         self.xq, self.xs = K.quantize_fp8(self.x)
         self.wprep.run()
         self.wq, self.wq_t, self.ws = self.wprep.q[0], self.wprep.qt[0], self.wprep.scale(0)
-        if self.frag:
-            self.wf, self.wf_t = K.weight_frag_fp8(self.wq)
         self.dyq, self.dys = K.quantize_fp8(self.dy)
 
     @property
@@ -119,14 +118,14 @@ class ConvWorkload:
                                   self.stride, self.pad)
 
     def fwd(self):
-        if self.frag:
-            return self.K.conv2d_fp8_fwd_wf(self.xq, self.wf, self.xs, self.ws, self.cout)
+        if self.frag:   # q / qt hold the halo-patch kernel's fragment layouts
+            return self.K.conv2d_fp8_fwd_wf(self.xq, self.wq, self.xs, self.ws, self.cout)
         return self.K.conv2d_fp8_fwd_general(self.xq, self.wq, self.xs, self.ws, self.stride, self.pad)
 
     def dgrad(self):
         """The data-gradient GEMM kernel alone (the transposed weight comes from quantize)."""
         if self.frag:
-            return self.K.conv2d_fp8_dgrad_wf(self.dyq, self.wf_t, self.dys, self.ws, self.cin)
+            return self.K.conv2d_fp8_dgrad_wf(self.dyq, self.wq_t, self.dys, self.ws, self.cin)
         return self.K.conv2d_fp8_dgrad_general(self.dyq, self.wq, self.dys, self.ws, (self.h, self.w),
                                                self.stride, self.pad, weight_t=self.wq_t)
 

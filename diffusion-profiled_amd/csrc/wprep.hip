@@ -12,7 +12,9 @@
 //   window_max_grouped_kernel   hist[i] = max(window i)            (torch.max of each window)
 //   wprep_amax_kernel           per-block |bf16(w)| maxima         (partial_amax_kernel)
 //   wprep_cast_kernel           q = e4m3(clamp(bf16(w) / scale)), the transposed copy, the
-//                               scale used, this amax's scale and its window record
+//                               scale used, this amax's scale and its window record (with
+//                               DPA_WP_FRAG both copies in the halo-patch conv's fragment
+//                               layouts: forward, and data gradient with the taps mirrored)
 // with scale = *prev_scale (delayed scaling: the window maximum) or the scale of this
 // weight's own amax (current scaling). bf16(w) is the round-to-nearest-even cast autocast
 // performs, so every byte and scale equals the per-layer path's. Each block takes one tile
@@ -76,6 +78,14 @@ __device__ __forceinline__ uint4 wp_bf16x8(const DpaWeightEntry& E, int64_t off)
   o.z = f32_to_bf16_bits(b.x) | (f32_to_bf16_bits(b.y) << 16);
   o.w = f32_to_bf16_bits(b.z) | (f32_to_bf16_bits(b.w) << 16);
   return o;
+}
+
+// Byte offset of (row, tap t, K index k) in the fragment-native layout of a [rows][taps][K]
+// operand (dpa_weight_frag_fp8): 2 KB blocks (kc * taps + t) * (rows / 16) + row / 16, byte
+// (k % 32) / 16 * 1024 + ((k % 128) / 32 * 16 + row % 16) * 16 + k % 16.
+__device__ __forceinline__ int64_t wp_frag_off(int rows, int taps, int row, int t, int k) {
+  const int64_t blk = ((int64_t)(k >> 7) * taps + t) * (rows >> 4) + (row >> 4);
+  return blk * 2048 + ((k >> 4) & 1) * 1024 + ((((k >> 5) & 3) << 4) + (row & 15)) * 16 + (k & 15);
 }
 
 __device__ __forceinline__ uint32_t wp_block_max(uint32_t v, uint32_t* red) {
@@ -143,12 +153,16 @@ __global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
   }
   const float r = quant_recip(scale);
   uint8_t* q = (uint8_t*)E.q;
+  const bool frag = (E.flags & DPA_WP_FRAG) != 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     uint2 o = uint2{0u, 0u};
     if (ok[h]) {
       o = r != 0.0f ? quant8_rcp(v[h], scale, r) : quant8(v[h], scale);
-      *reinterpret_cast<uint2*>(q + off[h]) = o;
+      // 8 consecutive input channels: 8 contiguous bytes in either layout
+      const int64_t dst = frag ? wp_frag_off(E.cout, E.taps, T.co0 + row[h], T.tap, T.ci0 + c8[h])
+                               : off[h];
+      *reinterpret_cast<uint2*>(q + dst) = o;
     }
     tile[row[h]][c8[h] / 4] = o.x;
     tile[row[h]][c8[h] / 4 + 1] = o.y;
@@ -170,8 +184,9 @@ __global__ __launch_bounds__(kWpThreads) void wprep_cast_kernel(
       const uint32_t word = tile[cc + j][cr >> 2];
       w |= ((word >> (8 * (cr & 3))) & 0xffu) << (8 * j);
     }
-    uint8_t* dst = qt + ((int64_t)ci * E.taps + T.tap) * E.cout + co;
-    if (co + 4 <= E.cout && (E.cout & 3) == 0) {
+    uint8_t* dst = frag ? qt + wp_frag_off(E.cin, E.taps, ci, E.taps - 1 - T.tap, co)
+                        : qt + ((int64_t)ci * E.taps + T.tap) * E.cout + co;
+    if (frag || (co + 4 <= E.cout && (E.cout & 3) == 0)) {
       *reinterpret_cast<uint32_t*>(dst) = w;
     } else {
       for (int j = 0; j < 4 && co + j < E.cout; ++j) dst[j] = (uint8_t)(w >> (8 * j));
@@ -227,6 +242,7 @@ extern "C" int dpa_weight_prep_plan(DpaWeightEntry* entries, int count) {
     if (E.window && !E.pos) return DPA_ERR_NULL;
     if (E.cout <= 0 || E.taps <= 0 || E.cin <= 0 || E.n <= 0) return DPA_ERR_SIZE;
     if (E.n != (int64_t)E.cout * E.taps * E.cin || E.cin % 8 != 0) return DPA_ERR_SHAPE;
+    if ((E.flags & DPA_WP_FRAG) && (E.cin % 128 != 0 || E.cout % 128 != 0)) return DPA_ERR_SHAPE;
     if (!aligned(E.w, 16) || !aligned(E.q, 8)) return DPA_ERR_ALIGN;
     E.blk0 = (int32_t)blocks;
     E.nblk = (int32_t)(ceil_div(E.cout, kWpTile) * E.taps * ceil_div(E.cin, kWpTile));

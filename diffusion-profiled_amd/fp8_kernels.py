@@ -861,7 +861,11 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
         x_scale, dy_scale = hist[0], hist[2]
         x_fp8 = quantize_fp8_delayed_deferred(x, x_scale, parts[0], parts[1])
         ctx.parts = parts
+        ctx.cin_cout = (weight.shape[1], weight.shape[0])
         ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale, dy_scale)
+        if wq.dtype == torch.uint8:      # fragment layouts of the halo-patch kernel
+            fwd_shapes(x_fp8, weight, FP8_DTYPE)
+            return conv2d_fp8_fwd_wf(x_fp8, wq, x_scale, w_scale, weight.shape[0])
         return conv2d_fwd_fp8_prequantized(x_fp8, wq, x_scale, w_scale)
 
     @staticmethod
@@ -872,9 +876,12 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
             dy = dy.to(torch.bfloat16)
         x_fp8, wq, wq_t, x_scale, w_scale, dy_scale = ctx.saved_tensors
         dy_fp8 = quantize_fp8_delayed_deferred(dy, dy_scale, ctx.parts[2], ctx.parts[3])
-        batch, cin, cout, height, width = xgrad_shapes(dy_fp8, wq, FP8_DTYPE)
-        dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, (height, width), 1, 1,
-                                      weight_t=wq_t)
+        if wq.dtype == torch.uint8:
+            dx = conv2d_fp8_dgrad_wf(dy_fp8, wq_t, dy_scale, w_scale, ctx.cin_cout[0])
+        else:
+            batch, cin, cout, height, width = xgrad_shapes(dy_fp8, wq, FP8_DTYPE)
+            dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, (height, width), 1, 1,
+                                          weight_t=wq_t)
         dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale, out_f32=True)
         return dx, dw, None, None, None, None, None
 
@@ -892,6 +899,10 @@ class Conv2dFP8GeneralPrepared(torch.autograd.Function):
         ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale)
         ctx.stride, ctx.padding = stride, padding
         ctx.input_hw = (x.shape[2], x.shape[3])
+        ctx.k, ctx.cin = weight.shape[2], weight.shape[1]
+        if wq.dtype == torch.uint8:      # fragment layouts of the halo-patch kernel
+            assert stride == 1 and padding == 1 and ctx.k == 3
+            return conv2d_fp8_fwd_wf(x_fp8, wq, x_scale, w_scale, weight.shape[0])
         return conv2d_fp8_fwd_general(x_fp8, wq, x_scale, w_scale, stride, padding)
 
     @staticmethod
@@ -900,11 +911,14 @@ class Conv2dFP8GeneralPrepared(torch.autograd.Function):
         x_fp8, wq, wq_t, x_scale, w_scale = ctx.saved_tensors
         dy = dy.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
         dy_fp8, dy_scale = quantize_fp8(dy)
-        k = wq.shape[2]
+        k = ctx.k
         dx = None
         if ctx.needs_input_grad[0]:
-            dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, ctx.input_hw,
-                                          ctx.stride, ctx.padding, weight_t=wq_t)
+            if wq.dtype == torch.uint8:
+                dx = conv2d_fp8_dgrad_wf(dy_fp8, wq_t, dy_scale, w_scale, ctx.cin)
+            else:
+                dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, ctx.input_hw,
+                                              ctx.stride, ctx.padding, weight_t=wq_t)
         dw = conv2d_fp8_wgrad_general(x_fp8, dy_fp8, x_scale, dy_scale, k, ctx.stride,
                                       ctx.padding, out_f32=True)
         return dx, dw, None, None, None, None, None

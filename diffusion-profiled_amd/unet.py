@@ -76,13 +76,20 @@ class _PreparedFP8Weight:
     _fp8_prepared = None
     _fp8_plan = None
 
-    def _note_fp8_mode(self, mode: str, w: torch.Tensor) -> None:
+    _fp8_frag = False
+
+    def _note_fp8_mode(self, mode: str, w: torch.Tensor, x: torch.Tensor | None = None) -> None:
+        """Record the layer's FP8 path; for a 3x3 conv whose input shape takes the halo-patch
+        kernel, also that its prepared weight should be in that kernel's fragment layouts."""
         if self._fp8_mode is not None or not w.is_cuda or w.dtype != torch.float32:
             return
         dense = (w.is_contiguous(memory_format=torch.channels_last) if w.ndim == 4
                  else w.is_contiguous())
         if dense:
             self._fp8_mode = mode
+            if x is not None and w.ndim == 4 and w.shape[2] == 3:
+                n, cin, h, wd = x.shape
+                self._fp8_frag = K.hconv_shape(n, cin, w.shape[0], h, wd)
 
     def _prepared(self, mode: str):
         plan = self._fp8_plan
@@ -142,7 +149,7 @@ class Conv2dFP8(_PreparedFP8Weight, nn.Module):
                 if pw is not None:
                     return K.Conv2dFP8DelayedPrepared.apply(
                         x, self.conv.weight, pw.q, pw.qt, pw.scale, pw.hist, pw.parts)
-                self._note_fp8_mode("delayed", self.conv.weight)
+                self._note_fp8_mode("delayed", self.conv.weight, x)
                 return K.Conv2dFP8DelayedWindowed.apply(
                     x, self.conv.weight, self.amax_window_acts, self.amax_window_weights,
                     self.amax_window_dy, self.window_pos)
@@ -164,7 +171,7 @@ class Conv2dFP8(_PreparedFP8Weight, nn.Module):
             if pw is not None:
                 return K.Conv2dFP8GeneralPrepared.apply(x, self.conv.weight, pw.q, pw.qt,
                                                         pw.scale, 1, 1)
-            self._note_fp8_mode("current", self.conv.weight)
+            self._note_fp8_mode("current", self.conv.weight, x)
             return K.conv2d_fp8(x, self.conv.weight, 1, 1)
         return self.conv(x)
 

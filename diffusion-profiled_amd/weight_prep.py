@@ -54,6 +54,8 @@ class PreparedWeight:
     scale: torch.Tensor    # [1] fp32: the scale q was cast with
     hist: torch.Tensor | None  # [3] fp32 window maxima (acts, weights, dy), delayed layers
     parts: tuple | None = None  # delayed layers: (x partials, x count, dy partials, dy count)
+    # q / qt hold the halo-patch conv's fragment layouts (flat uint8): forward, data gradient
+    frag: bool = False
 
 
 def _fp8_weight(module) -> torch.Tensor:
@@ -84,7 +86,15 @@ class WeightPrep:
         for i, m in enumerate(layers):
             w = _fp8_weight(m)
             assert w.dtype == torch.float32 and w.device == dev
-            if w.ndim == 4:
+            frag = bool(getattr(m, "_fp8_frag", False))
+            if w.ndim == 4 and frag:
+                # the layer's convs run the halo-patch kernel: fragment layouts, same bytes
+                cout, cin, kh, kw = w.shape
+                assert w.is_contiguous(memory_format=torch.channels_last)
+                q = torch.empty(w.numel(), device=dev, dtype=torch.uint8)
+                qt = torch.empty(w.numel(), device=dev, dtype=torch.uint8)
+                taps = kh * kw
+            elif w.ndim == 4:
                 cout, cin, kh, kw = w.shape
                 assert w.is_contiguous(memory_format=torch.channels_last)
                 q = torch.empty((cout, cin, kh, kw), device=dev, dtype=FP8_DTYPE,
@@ -102,6 +112,7 @@ class WeightPrep:
             e.scale_used = self.scales[2 * i].data_ptr()
             e.cur_scale = self.scales[2 * i + 1].data_ptr()
             e.n, e.cout, e.taps, e.cin = w.numel(), cout, taps, cin
+            e.flags = 2 if frag and w.ndim == 4 else 0        # DPA_WP_FRAG
             hist = parts = None
             if m._fp8_mode == "delayed":
                 hist = self.hist[3 * d:3 * d + 3]
@@ -125,7 +136,8 @@ class WeightPrep:
                 dw.pos = m.window_pos.data_ptr()
                 dw.len = m.amax_window_acts.numel()
                 d += 1
-            m._fp8_prepared = PreparedWeight(q, qt, self.scales[2 * i:2 * i + 1], hist, parts)
+            m._fp8_prepared = PreparedWeight(q, qt, self.scales[2 * i:2 * i + 1], hist, parts,
+                                             frag and w.ndim == 4)
             m._fp8_plan = self
             self._keep += [q, qt]
         self.active = False
@@ -179,16 +191,25 @@ class TensorPrep:
     them in two launches: ``quantize_fp8`` of each weight plus ``weight_transpose_fp8``,
     bit-identical. Buffers are allocated once; run() refreshes them from the weights."""
 
-    def __init__(self, weights: list):
+    def __init__(self, weights: list, frag: list | None = None):
+        """``frag[i]``: weight i feeds the halo-patch conv, so q / qt hold its forward and
+        data-gradient fragment layouts (flat uint8) instead of OHWI / [Cin][R][S][Cout]."""
         assert weights
         dev = weights[0].device
         self.weights = weights
+        self.frag = [bool(f) for f in (frag or [False] * len(weights))]
         self.scales = torch.zeros(len(weights), device=dev, dtype=torch.float32)
         self.q, self.qt = [], []
         entries = (DpaWeightEntry * len(weights))()
         for i, w in enumerate(weights):
             assert w.dtype in (torch.float32, torch.bfloat16) and w.device == dev
-            if w.ndim == 4:
+            if w.ndim == 4 and self.frag[i]:
+                cout, cin, kh, kw = w.shape
+                assert w.is_contiguous(memory_format=torch.channels_last)
+                q = torch.empty(w.numel(), device=dev, dtype=torch.uint8)
+                qt = torch.empty(w.numel(), device=dev, dtype=torch.uint8)
+                taps = kh * kw
+            elif w.ndim == 4:
                 cout, cin, kh, kw = w.shape
                 assert w.is_contiguous(memory_format=torch.channels_last)
                 q = torch.empty((cout, cin, kh, kw), device=dev, dtype=FP8_DTYPE,
@@ -205,7 +226,8 @@ class TensorPrep:
             e.w, e.q, e.qt = w.data_ptr(), q.data_ptr(), qt.data_ptr()
             e.scale_used = self.scales[i].data_ptr()
             e.n, e.cout, e.taps, e.cin = w.numel(), cout, taps, cin
-            e.flags = 1 if w.dtype == torch.bfloat16 else 0       # DPA_WP_BF16
+            e.flags = ((1 if w.dtype == torch.bfloat16 else 0)                 # DPA_WP_BF16
+                       | (2 if w.ndim == 4 and self.frag[i] else 0))          # DPA_WP_FRAG
             self.q.append(q)
             self.qt.append(qt)
         blocks = _lib.load().dpa_weight_prep_plan(ctypes.addressof(entries), len(weights))

@@ -326,6 +326,8 @@ int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float
  * rule as dpa_quantize_fp8_bf16 (current scaling) or dpa_quantize_fp8_delayed_bf16 (delayed).
  * ---------------------------------------------------------------------------------------- */
 #define DPA_WP_BF16 1          /* DpaWeightEntry.flags: w holds bf16, not fp32 */
+#define DPA_WP_FRAG 2          /* q and qt in the fragment layouts of dpa_weight_frag_fp8
+                                  (forward / data gradient); Cin, Cout multiples of 128 */
 typedef struct DpaWeightEntry {
   const float* w;           /* weight (fp32, or bf16 with DPA_WP_BF16), FP8 memory order:
                                [Cout][R][S][Cin] or [N][K] */
@@ -340,7 +342,7 @@ typedef struct DpaWeightEntry {
   int64_t n;                /* elements = cout * taps * cin (cin % 8 == 0) */
   int32_t cout, taps, cin;  /* taps = R * S (1 for a linear) */
   int32_t blk0, nblk;       /* filled in by dpa_weight_prep_plan */
-  int32_t flags;            /* DPA_WP_BF16 or 0 */
+  int32_t flags;            /* DPA_WP_BF16 | DPA_WP_FRAG, or 0 */
 } DpaWeightEntry;
 
 /* Assigns each entry its blocks (host array, in place); returns the total block count (> 0)

@@ -186,3 +186,28 @@ def test_tensor_prep_bf16_weights_equal_quantize_and_transpose():
             qt_ref = K.weight_transpose_fp8(q4)
             assert torch.equal(tp.qt[i].view(torch.uint8).flatten(),
                                qt_ref.view(torch.uint8).flatten()), (rnd, i)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+def test_tensor_prep_fragment_layouts_equal_quantize_and_frag(dtype):
+    """TensorPrep with frag=True (DPA_WP_FRAG): q and qt are the halo-patch kernel's forward
+    and data-gradient fragment layouts of quantize_fp8(bf16(w)), byte for byte, beside an
+    OHWI entry in the same plan; the scale is quantize_fp8's."""
+    g = torch.Generator().manual_seed(11)
+    ws = [(torch.randn((256, 128, 3, 3), generator=g) * 0.05).to(dtype),
+          (torch.randn((128, 256, 3, 3), generator=g) * 2.0).to(dtype),
+          (torch.randn((128, 128, 3, 3), generator=g)).to(dtype)]
+    ws = [w.cuda().contiguous(memory_format=torch.channels_last) for w in ws]
+    tp = WP.TensorPrep(ws, frag=[True, True, False])
+    tp.run()
+    torch.cuda.synchronize()
+    for i, w in enumerate(ws):
+        q_ref, s_ref = K.quantize_fp8_tensor(w.to(torch.bfloat16))
+        assert float(tp.scale(i)) == float(s_ref), i
+        if i < 2:
+            wf, wt = K.weight_frag_fp8(q_ref)
+            torch.cuda.synchronize()
+            assert tp.q[i].dtype == torch.uint8 and torch.equal(tp.q[i], wf), i
+            assert torch.equal(tp.qt[i], wt), i
+        else:
+            assert torch.equal(tp.q[i].view(torch.uint8), q_ref.view(torch.uint8))
