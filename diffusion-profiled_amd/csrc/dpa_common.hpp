@@ -157,6 +157,12 @@ __device__ __forceinline__ us2 absmax8(us2 acc, uint4 v) {
   return acc;
 }
 
+// The delayed-scaling cast of 8 bf16 with a window scale (r = quant_recip(scale)): the same
+// bytes as the standalone cast kernel writes for them.
+__device__ __forceinline__ uint2 quant8_delayed(uint4 v, float scale, float r) {
+  return r != 0.0f ? quant8_rcp(v, scale, r) : quant8(v, scale);
+}
+
 // Amax-window state of a delayed-scaling module (diffusion/unet.py:82-91 and
 // diffusion/fp8_kernels.py:888-889): window[pos] = scale and, for the last tensor of the
 // forward, pos = (pos + 1) % len. A pos outside [0, len) (never produced by this update)
@@ -184,6 +190,25 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
+}
+
+// One u32 amax partial per workgroup for a producer kernel that casts its output: the
+// workgroup max of acc (packed bf16 magnitudes) goes to partials[blk]; workgroup 0 also stores
+// the partial count nblk. Call from every thread (uniform); red holds one u32 per wave.
+__device__ __forceinline__ void store_amax_partial(us2 acc, uint32_t* red, uint32_t* partials,
+                                                   uint32_t* count, uint32_t blk,
+                                                   uint32_t nblk) {
+  uint32_t m = acc.x > acc.y ? acc.x : acc.y;
+  m = wave_max_u32(m);
+  const int nw = (int)(blockDim.x >> 6);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+    for (int i = 1; i < nw; ++i) r = r > red[i] ? r : red[i];
+    partials[blk] = r;
+    if (blk == 0) *count = nblk;
+  }
 }
 
 // ---------------------------------------------------------------------------------------

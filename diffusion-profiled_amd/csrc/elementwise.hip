@@ -72,6 +72,49 @@ __global__ __launch_bounds__(kEwThreads) void residual_f32_bwd_kernel(
   gb[i] = uint2{pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w)};
 }
 
+// The join's backward when the bf16 operand b is the output of a delayed-scaling FP8 conv:
+// b's gradient bf16(g * inv) is not stored but cast for that conv's weight and input
+// gradients, e4m3(gb / *scale) (the standalone cast's bytes), with one amax partial of gb per
+// workgroup; a's gradient is stored as in the plain backward (fp32 g * inv for the fp32 form,
+// the same bf16 values for the bf16 form). Grid-strided over groups of 8 elements.
+constexpr int kResQBlocks = 1024;
+
+template <bool kF32>
+__global__ __launch_bounds__(kEwThreads) void residual_bwd_q_kernel(
+    const void* __restrict__ g, void* __restrict__ ga, uint8_t* __restrict__ q,
+    const float* __restrict__ scale_p, uint32_t* __restrict__ part, uint32_t* __restrict__ count,
+    int64_t n8, float inv) {
+  __shared__ uint32_t red[kEwThreads / 64];
+  const float scale = *scale_p;
+  const float r = quant_recip(scale);
+  us2 acc = {0, 0};
+  for (int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * kEwThreads) {
+    uint4 gb;
+    if constexpr (kF32) {
+      const float4* gp = static_cast<const float4*>(g) + 2 * i;
+      const float4 v0 = gp[0], v1 = gp[1];
+      const float4 s0 = float4{v0.x * inv, v0.y * inv, v0.z * inv, v0.w * inv};
+      const float4 s1 = float4{v1.x * inv, v1.y * inv, v1.z * inv, v1.w * inv};
+      float4* ap = static_cast<float4*>(ga) + 2 * i;
+      ap[0] = s0;
+      ap[1] = s1;
+      gb = uint4{pack_bf16x2(s0.x, s0.y), pack_bf16x2(s0.z, s0.w), pack_bf16x2(s1.x, s1.y),
+                 pack_bf16x2(s1.z, s1.w)};
+    } else {
+      const uint4 v = static_cast<const uint4*>(g)[i];
+      gb = uint4{pack_bf16x2(bf16_lo(v.x) * inv, bf16_hi(v.x) * inv),
+                 pack_bf16x2(bf16_lo(v.y) * inv, bf16_hi(v.y) * inv),
+                 pack_bf16x2(bf16_lo(v.z) * inv, bf16_hi(v.z) * inv),
+                 pack_bf16x2(bf16_lo(v.w) * inv, bf16_hi(v.w) * inv)};
+      static_cast<uint4*>(ga)[i] = gb;
+    }
+    st_nt8(q + 8 * i, quant8_delayed(gb, scale, r));
+    acc = absmax8(acc, gb);
+  }
+  store_amax_partial(acc, red, part, count, blockIdx.x, gridDim.x);
+}
+
 // Decoder input of the U-Net (diffusion/unet.py:389-392): y = cat([up(a), h], channels) in
 // NHWC, fp32 (autocast runs F.interpolate in fp32 and the concatenation promotes), where
 // up(a) is a 2x nearest upsampling of a (or a itself). One pass reads a and h once and writes
@@ -335,5 +378,36 @@ extern "C" int dpa_residual_scale_bf16(const void* a, const void* b, void* y, in
   residual_scale_kernel<<<(unsigned)ceil_div(n8, (int64_t)kEwThreads), kEwThreads, 0,
                           (hipStream_t)stream>>>((const uint4*)a, (const uint4*)b, (uint4*)y, n8,
                                                  inv);
+  return launch_status();
+}
+
+static int64_t residual_q_blocks(int64_t n) {
+  const int64_t b = ceil_div(n / 8, (int64_t)kEwThreads);
+  return b < kResQBlocks ? b : kResQBlocks;
+}
+
+extern "C" int dpa_residual_scale_fp8_partials(int64_t n) {
+  return n > 0 && n % 8 == 0 ? (int)residual_q_blocks(n) : 0;
+}
+
+extern "C" int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, void* gbq,
+                                          const float* gb_scale, uint32_t* gb_partials,
+                                          int gb_partials_cap, uint32_t* gb_count, int64_t n,
+                                          float inv, void* stream) {
+  if (!g || !ga || !gbq || !gb_scale || !gb_partials || !gb_count) return DPA_ERR_NULL;
+  if (g_dtype != DPA_DTYPE_BF16 && g_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (n <= 0 || n % 8 != 0) return DPA_ERR_SIZE;
+  const int64_t nb = residual_q_blocks(n);
+  if (gb_partials_cap < nb) return DPA_ERR_WORKSPACE;
+  if (!aligned(g, 16) || !aligned(ga, 16) || !aligned(gbq, 8) || !aligned(gb_scale, 4) ||
+      !aligned(gb_partials, 4) || !aligned(gb_count, 4))
+    return DPA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  if (g_dtype == DPA_DTYPE_F32)
+    residual_bwd_q_kernel<true><<<(unsigned)nb, kEwThreads, 0, s>>>(
+        g, ga, (uint8_t*)gbq, gb_scale, gb_partials, gb_count, n / 8, inv);
+  else
+    residual_bwd_q_kernel<false><<<(unsigned)nb, kEwThreads, 0, s>>>(
+        g, ga, (uint8_t*)gbq, gb_scale, gb_partials, gb_count, n / 8, inv);
   return launch_status();
 }

@@ -51,6 +51,13 @@ struct GnArgs {
   const void* dx_add;  // bwd: a gradient added to dx (chunked and small forms), or null
   int dx_add_bf16;     // bwd: dx_add is bf16 while x and dx are fp32
   uint16_t* x_bf16;    // fwd: fp32 x also written as bf16 here (chunked and small forms), or null
+  // Producer-fused cast for a delayed-scaling consumer (chunked and small forms): instead of
+  // the bf16 output (fwd) or bf16 dx (bwd), e4m3(bf16 value / *q_scale) goes to q, and each
+  // workgroup leaves the amax of its bf16 values in q_part[workgroup] (count in *q_count)
+  uint8_t* q;
+  const float* q_scale;
+  uint32_t* q_part;
+  uint32_t* q_count;
   int N, HW, C, G, cpg;
   float eps;
 };
@@ -530,9 +537,32 @@ __device__ __forceinline__ void unpack_x(const uint4 (&v)[NL][kChU], int u, floa
   }
 }
 
+// The producer-fused cast in one thread (GnArgs::q): the window scale, its reciprocal for the
+// fast quotient, and the running amax of the bf16 values cast.
+struct GnQ {
+  float s = 1.0f, r = 0.0f;
+  us2 acc = {0, 0};
+  __device__ __forceinline__ explicit GnQ(const GnArgs& p) {
+    if (p.q) {
+      s = *p.q_scale;
+      r = quant_recip(s);
+    }
+  }
+  // the 8 bf16 values v of element offset off
+  __device__ __forceinline__ void put(const GnArgs& p, int64_t off, uint4 v) {
+    st_nt8(p.q + off, quant8_delayed(v, s, r));
+    acc = absmax8(acc, v);
+  }
+  // the workgroup's amax partial (every thread; red: one u32 per wave)
+  __device__ __forceinline__ void finish(const GnArgs& p, uint32_t* red) const {
+    const uint32_t blk = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    store_amax_partial(acc, red, p.q_part, p.q_count, blk, gridDim.x * gridDim.y * gridDim.z);
+  }
+};
+
 // dx of 8 channels at element offset off, in x's type; dx(e) gives channel e's value
 template <bool kF32, typename F>
-__device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
+__device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx, GnQ& qo) {
   // with dx_add: dx + add as torch's gradient accumulation forms it (one fp32 add; in bf16 the
   // sum of the two bf16 gradients, rounded once more)
   const bool add = p.dx_add != nullptr;
@@ -574,7 +604,10 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx) {
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
-    st_nt16(static_cast<uint16_t*>(p.out) + off, uint4{o[0], o[1], o[2], o[3]});
+    if (p.q)
+      qo.put(p, off, uint4{o[0], o[1], o[2], o[3]});
+    else
+      st_nt16(static_cast<uint16_t*>(p.out) + off, uint4{o[0], o[1], o[2], o[3]});
   }
 }
 
@@ -664,6 +697,7 @@ template <bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs p,
                                                                    const float2* __restrict__ cs,
                                                                    int nchunk) {
+  __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float2 gstat[kSlab / 4];
   __shared__ float2 lcs[kMaxChunks * (kSlab / 4)];
   const int n = blockIdx.y, chunk = blockIdx.z;
@@ -723,6 +757,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
   const bool drop = p.drop_seed != nullptr;
   const uint64_t seed = drop ? *p.drop_seed : 0;
+  GnQ qo(p);
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8];
@@ -746,8 +781,14 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
-    if (ok[u]) st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    if (ok[u]) {
+      if (p.q)
+        qo.put(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, uint4{o[0], o[1], o[2], o[3]});
+      else
+        st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    }
   }
+  if (p.q) qo.finish(p, qred);
 }
 
 // The backward terms of one pixel's 8 channels (see gn_silu_bwd_kernel): g = d u / d zp
@@ -860,6 +901,7 @@ template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const GnArgs p,
                                                                        const float4* __restrict__ cp,
                                                                        int nchunk) {
+  __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float4 tot[kSlab];
   __shared__ float4 slice[4][kSlab];
   __shared__ float hs[2][16];
@@ -878,6 +920,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   chunk_load(in.src, in.stride, chunk * kChunkPx, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
+  GnQ qo(p);
 
   // channel totals over the chunks: four interleaved slices of chunks per channel (loads
   // in flight together), then the slices in order (deterministic)
@@ -962,8 +1005,9 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
       const float gxh = g[e] * st.fsc[e] * st.gm[e];
       return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
     };
-    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx);
+    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
   }
+  if (p.q) qo.finish(p, qred);
 }
 
 // ---- small images (HW <= 128 pixels: the 8x8 and 4x4 levels): one workgroup per (image,
@@ -973,6 +1017,7 @@ constexpr int kSmallMaxHW = kChunkPx;
 
 template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p) {
+  __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float red[(kChPLN / 8) * 8 * 2];
   __shared__ float hs[16];
   const int n = blockIdx.y;
@@ -1059,6 +1104,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
   const bool drop = p.drop_seed != nullptr;
   const uint64_t seed = drop ? *p.drop_seed : 0;
+  GnQ qo(p);
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     const uint32_t kb =
@@ -1077,12 +1123,19 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
       }
       o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
     }
-    if (ok[u]) st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    if (ok[u]) {
+      if (p.q)
+        qo.put(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, uint4{o[0], o[1], o[2], o[3]});
+      else
+        st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+    }
   }
+  if (p.q) qo.finish(p, qred);
 }
 
 template <bool kFilm, bool kF32>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p) {
+  __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float red[(kChPLN / 8) * 8 * 16];
   __shared__ float hs[2][16];
   const int n = blockIdx.y;
@@ -1100,6 +1153,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   chunk_load(in.src, in.stride, 0, pl, p.HW, v, ok, pxs);
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
+  GnQ qo(p);
   // per-channel S1 = sum g, S2 = sum g * xhat over the image (every lane gets the totals)
   float acc[16];
 #pragma unroll
@@ -1177,8 +1231,9 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
       const float gxh = g[e] * st.fsc[e] * st.gm[e];
       return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
     };
-    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx);
+    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
   }
+  if (p.q) qo.finish(p, qred);
 }
 
 static int gn_chunks(int HW) {
@@ -1199,6 +1254,38 @@ static bool gn_shape_ok(int N, int HW, int C, int G) {
 }  // namespace dpa
 
 using namespace dpa;
+
+// The producer-fused e4m3 output of the fp8 entry points (GnArgs::q).
+struct GnQOut {
+  void* q;
+  const float* scale;
+  uint32_t* part;
+  int cap;
+  uint32_t* count;
+};
+
+// Workgroups of the launch that writes the output (one amax partial each), 0 for the forms
+// without the fused cast (128 < HW < 256 and HW > 8192 pixels).
+static int64_t gn_q_blocks(int N, int HW, int C) {
+  const int nchunk = gn_chunks(HW);
+  if (nchunk > 0) return (int64_t)(C / kSlab) * N * nchunk;
+  return HW <= kSmallMaxHW ? (int64_t)(C / kSlab) * N : 0;
+}
+
+static int gn_set_q(GnArgs& a, const GnQOut* qo, int64_t nblk) {
+  if (!qo) return DPA_OK;
+  if (!qo->q || !qo->scale || !qo->part || !qo->count) return DPA_ERR_NULL;
+  if (nblk <= 0) return DPA_ERR_SHAPE;
+  if (qo->cap < nblk) return DPA_ERR_WORKSPACE;
+  if (!aligned(qo->q, 8) || !aligned(qo->scale, 4) || !aligned(qo->part, 4) ||
+      !aligned(qo->count, 4))
+    return DPA_ERR_ALIGN;
+  a.q = (uint8_t*)qo->q;
+  a.q_scale = qo->scale;
+  a.q_part = qo->part;
+  a.q_count = qo->count;
+  return DPA_OK;
+}
 
 static int64_t gn_fwd_workspace(int N, int HW, int G) {
   return (int64_t)N * gn_chunks(HW) * G * (int64_t)sizeof(float2);
@@ -1222,8 +1309,10 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
                   const float* film_shift, const void* film_wb, void* out, float* mean,
                   float* rstd, int N, int HW, int C, int G, float eps, void* stream,
                   void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false,
-                  const void* drop_seed = nullptr, float drop_p = 0.0f, void* x_bf16 = nullptr) {
-  if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
+                  const void* drop_seed = nullptr, float drop_p = 0.0f, void* x_bf16 = nullptr,
+                  const GnQOut* qo = nullptr) {
+  if (!x || !gamma || !beta || (!out && !qo) || !mean || !rstd) return DPA_ERR_NULL;
+  if (qo && out) return DPA_ERR_SHAPE;  // one output: bf16 or e4m3
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
   if (!gn_shape_ok(N, HW, C, G)) return DPA_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(out, 16) || !aligned(film_wb, 2)) return DPA_ERR_ALIGN;
@@ -1249,6 +1338,12 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   a.x_bf16 = (uint16_t*)x_bf16;
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
+  if (qo) {
+    if (!chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+    const int qst = gn_set_q(a, qo, gn_q_blocks(N, HW, C));
+    if (qst != DPA_OK) return qst;
+    a.out = qo->q;  // not written: the kernels store through a.q
+  }
   hipStream_t s = (hipStream_t)stream;
   if (chunked) {
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
@@ -1358,7 +1453,9 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
                   float* dfilm_scale, float* dfilm_shift, void* dfilm_wb, void* workspace,
                   int64_t workspace_bytes, int N, int HW, int C, int G, void* stream,
                   bool x_f32 = false, const void* drop_seed = nullptr, float drop_p = 0.0f,
-                  const void* dx_add = nullptr, bool dx_add_bf16 = false) {
+                  const void* dx_add = nullptr, bool dx_add_bf16 = false,
+                  const GnQOut* qo = nullptr) {
+  if (qo) dx = qo->q;  // the e4m3 dx replaces the bf16 one
   if (!x || !dout || !gamma || !beta || !mean || !rstd || !dx || !dgamma || !dbeta)
     return DPA_ERR_NULL;
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1396,6 +1493,12 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   a.dx_add_bf16 = x_f32 && dx_add_bf16;
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
+  if (qo) {
+    if (x_f32 || dx_add) return DPA_ERR_SHAPE;  // e4m3 of a bf16 dx, nothing added
+    if (!chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+    const int qst = gn_set_q(a, qo, gn_q_blocks(N, HW, C));
+    if (qst != DPA_OK) return qst;
+  }
   const bool film = a.fs || a.wb;
   int st = DPA_OK;
   if (chunked) {
@@ -1490,4 +1593,49 @@ extern "C" int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, 
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
                 stream, x_dtype == DPA_DTYPE_F32, drop_seed, drop_p, dx_add,
                 dx_add_dtype == DPA_DTYPE_BF16);
+}
+
+extern "C" int dpa_gn_silu_fp8_partials(int N, int HW, int C, int G) {
+  if (!gn_shape_ok(N, HW, C, G)) return 0;
+  const int64_t nb = gn_q_blocks(N, HW, C);
+  return nb <= INT32_MAX ? (int)nb : 0;
+}
+
+extern "C" int dpa_gn_silu_fwd_fp8(const void* x, int x_dtype, const float* gamma,
+                                   const float* beta, const float* film_scale,
+                                   const float* film_shift, const void* film_wb, void* q,
+                                   const float* q_scale, uint32_t* q_partials,
+                                   int q_partials_cap, uint32_t* q_count, float* mean,
+                                   float* rstd, void* workspace, int64_t workspace_bytes, int N,
+                                   int HW, int C, int G, float eps, const void* drop_seed,
+                                   float drop_p, void* x_bf16, void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  if (!q) return DPA_ERR_NULL;
+  if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
+    return DPA_ERR_WORKSPACE;
+  if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
+  const GnQOut qo{q, q_scale, q_partials, q_partials_cap, q_count};
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, nullptr, mean, rstd, N, HW, C,
+                G, eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
+                drop_p, x_bf16, &qo);
+}
+
+extern "C" int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float* gamma,
+                                   const float* beta, const float* film_scale,
+                                   const float* film_shift, const void* film_wb,
+                                   const float* mean, const float* rstd, void* dxq,
+                                   const float* dx_scale, uint32_t* dx_partials,
+                                   int dx_partials_cap, uint32_t* dx_count, float* dgamma,
+                                   float* dbeta, float* dfilm_scale, float* dfilm_shift,
+                                   void* dfilm_wb, void* workspace, int64_t workspace_bytes,
+                                   int N, int HW, int C, int G, const void* drop_seed,
+                                   float drop_p, void* stream) {
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  if (!dxq) return DPA_ERR_NULL;
+  const GnQOut qo{dxq, dx_scale, dx_partials, dx_partials_cap, dx_count};
+  return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dxq, dgamma,
+                dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
+                stream, false, drop_seed, drop_p, nullptr, false, &qo);
 }

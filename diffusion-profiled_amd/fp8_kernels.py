@@ -184,6 +184,53 @@ def quantize_fp8_delayed_deferred(tensor: torch.Tensor, prev_scale: torch.Tensor
     return quantized
 
 
+_ZEROS: dict[tuple, torch.Tensor] = {}
+
+
+def placeholder(shape, dtype: torch.dtype, device) -> torch.Tensor:
+    """A tensor of the given shape that holds no data (one shared zero element, all strides
+    0): what autograd carries where a producer handed the e4m3 operand to its FP8 conv
+    directly. No launch after the first per device and dtype."""
+    key = (torch.device(device), dtype)
+    z = _ZEROS.get(key)
+    if z is None:
+        z = _ZEROS[key] = torch.zeros((), dtype=dtype, device=device)
+    return z.expand(shape)
+
+
+def is_placeholder(t: torch.Tensor) -> bool:
+    return t.numel() > 1 and all(s == 0 for s in t.stride())
+
+
+class Fp8Handoff:
+    """The e4m3 operand of a delayed-scaling FP8 conv written by the kernel that produces it
+    (diffusion/unet.py:151, :157-161 feeding diffusion/fp8_kernels.py:856, :885-893): cast
+    with the conv's window scale, its block maxima left in the conv's deferred-window buffers,
+    which is what ``quantize_fp8_delayed_deferred`` does in a pass of its own.
+
+    For a gradient the producer's backward sets ``q`` and gives autograd a ``placeholder`` for
+    the bf16 gradient; the conv's backward ``take``s ``q``. The placeholder reaches the conv
+    unchanged only when the conv's output has no other consumer, which ``take`` checks."""
+
+    __slots__ = ("scale", "partials", "count", "q")
+
+    def __init__(self, scale: torch.Tensor, partials: torch.Tensor, count: torch.Tensor):
+        self.scale, self.partials, self.count = scale, partials, count
+        self.q: torch.Tensor | None = None
+
+    def fill_from_bf16(self, t: torch.Tensor) -> None:
+        """The unfused form: cast a bf16 tensor the producer had to write."""
+        t = t.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
+        self.q = quantize_fp8_delayed_deferred(t, self.scale, self.partials, self.count)
+
+    def take(self, grad: torch.Tensor) -> torch.Tensor:
+        if self.q is None or not is_placeholder(grad):
+            raise RuntimeError("FP8 hand-off: the conv's output gradient did not come from its "
+                               "producer alone (another consumer or no fused producer backward)")
+        q, self.q = self.q, None
+        return q
+
+
 def window_max3(w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
     """``torch.stack([w0.max(), w1.max(), w2.max()])`` for three equal-length fp32 windows in
     one launch (diffusion/unet.py:72-73, fp8_kernels.py:849)."""
@@ -849,18 +896,26 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
     quantizations cast with hist[0] / hist[2] and leave their block maxima in the layer's
     persistent buffers (``parts`` = x partials, x count, dy partials, dy count); the weight
     preparation of the next step (or ``WeightPrep.flush``) writes their window records and
-    advances the position, which gives the per-call path's window state."""
+    advances the position, which gives the per-call path's window state.
+
+    xq: the e4m3 input written by its producer (``Fp8Handoff``; x is then a placeholder);
+    dy_handoff: an ``Fp8Handoff`` whose producer backward writes the e4m3 dy."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, wq: torch.Tensor,
                 wq_t: torch.Tensor, w_scale: torch.Tensor, hist: torch.Tensor,
-                parts: tuple) -> torch.Tensor:
-        x = x.to(torch.bfloat16)
-        assert x.is_contiguous(memory_format=torch.channels_last)
+                parts: tuple, xq: torch.Tensor | None = None,
+                dy_handoff: Fp8Handoff | None = None) -> torch.Tensor:
         x_scale, dy_scale = hist[0], hist[2]
-        x_fp8 = quantize_fp8_delayed_deferred(x, x_scale, parts[0], parts[1])
+        if xq is not None:
+            x_fp8 = xq
+        else:
+            x = x.to(torch.bfloat16)
+            assert x.is_contiguous(memory_format=torch.channels_last)
+            x_fp8 = quantize_fp8_delayed_deferred(x, x_scale, parts[0], parts[1])
         ctx.parts = parts
+        ctx.dy_handoff = dy_handoff
         ctx.cin_cout = (weight.shape[1], weight.shape[0])
         ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale, dy_scale)
         if wq.dtype == torch.uint8:      # fragment layouts of the halo-patch kernel
@@ -871,11 +926,14 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
     @staticmethod
     @custom_bwd(device_type="cuda")
     def backward(ctx: Any, dy: torch.Tensor) -> Any:
-        dy = dy.contiguous(memory_format=torch.channels_last)
-        if dy.dtype != torch.bfloat16:
-            dy = dy.to(torch.bfloat16)
         x_fp8, wq, wq_t, x_scale, w_scale, dy_scale = ctx.saved_tensors
-        dy_fp8 = quantize_fp8_delayed_deferred(dy, dy_scale, ctx.parts[2], ctx.parts[3])
+        if ctx.dy_handoff is not None:
+            dy_fp8 = ctx.dy_handoff.take(dy)
+        else:
+            dy = dy.contiguous(memory_format=torch.channels_last)
+            if dy.dtype != torch.bfloat16:
+                dy = dy.to(torch.bfloat16)
+            dy_fp8 = quantize_fp8_delayed_deferred(dy, dy_scale, ctx.parts[2], ctx.parts[3])
         if wq.dtype == torch.uint8:
             dx = conv2d_fp8_dgrad_wf(dy_fp8, wq_t, dy_scale, w_scale, ctx.cin_cout[0])
         else:
@@ -883,7 +941,7 @@ class Conv2dFP8DelayedPrepared(torch.autograd.Function):
             dx = conv2d_fp8_dgrad_general(dy_fp8, wq, dy_scale, w_scale, (height, width), 1, 1,
                                           weight_t=wq_t)
         dw = conv2d_bwd_weight_fp8_prequantized(x_fp8, dy_fp8, x_scale, dy_scale, out_f32=True)
-        return dx, dw, None, None, None, None, None
+        return dx, dw, None, None, None, None, None, None, None
 
 
 class Conv2dFP8GeneralPrepared(torch.autograd.Function):

@@ -16,6 +16,7 @@ from typing import Any
 import torch
 
 from . import _lib
+from .fp8_kernels import FP8_DTYPE, Fp8Handoff, placeholder
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -120,6 +121,35 @@ def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=Non
     )
 
 
+def fp8_ok(shape, groups: int, hand: Fp8Handoff) -> bool:
+    """Whether the kernels can write this GroupNorm's output (or bf16 dx) as the e4m3 operand
+    of a delayed-scaling conv: a form with the fused cast for the image size, and room for its
+    amax partials in the conv's buffer."""
+    n, c, h, w = shape
+    need = _lib.query("dpa_gn_silu_fp8_partials", n, h * w, c, groups)
+    return 0 < need <= hand.partials.numel()
+
+
+def _fwd_fp8_call(x, gamma, beta, wb, hand: Fp8Handoff, mean, rstd, groups, eps, seed=None,
+                  p_drop=0.0, x_bf16=None) -> None:
+    """The forward writing e4m3(out / hand.scale) to hand.q (no bf16 output) and its amax
+    partials to the hand-off's buffers."""
+    n, c, h, w = x.shape
+    q = torch.empty_like(x, dtype=FP8_DTYPE, memory_format=torch.channels_last)
+    ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    dt = DTYPE_F32 if x.dtype == torch.float32 else DTYPE_BF16
+    _lib.call(
+        "dpa_gn_silu_fwd_fp8",
+        x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), None, None, p(wb), q.data_ptr(),
+        hand.scale.data_ptr(), hand.partials.data_ptr(), hand.partials.numel(),
+        hand.count.data_ptr(), mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c,
+        groups, float(eps), p(seed), float(p_drop), p(x_bf16), _stream(x),
+    )
+    hand.q = q
+
+
 def gn_silu_bwd(x, dout, gamma, beta, mean, rstd, groups, film_scale=None, film_shift=None,
                 dx_add=None):
     """Returns (dx in x's dtype (bf16 or fp32), dgamma, dbeta, dfilm_scale [N,C] | None,
@@ -190,12 +220,22 @@ class GroupNormSiLUTee(torch.autograd.Function):
     bf16 gradient is added to the fp32 dx as autograd would (cast, then one fp32 add)."""
 
     @staticmethod
-    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, skip_bf16: bool = False):
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, skip_bf16: bool = False,
+                hand: Fp8Handoff | None = None):
         xb, _ = _prep_x(x)
         x16 = None
         if skip_bf16 and xb.dtype == torch.float32 and dropout_ok(xb):
             x16 = torch.empty_like(xb, dtype=torch.bfloat16, memory_format=torch.channels_last)
-        out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps, x_bf16=x16)
+        if hand is None:
+            out, mean, rstd = gn_silu_fwd(xb, gamma, beta, groups, eps, x_bf16=x16)
+        else:
+            # the e4m3 conv input goes to hand.q; autograd carries a placeholder for it
+            n = xb.shape[0]
+            mean = torch.empty(n * groups, device=xb.device, dtype=torch.float32)
+            rstd = torch.empty(n * groups, device=xb.device, dtype=torch.float32)
+            _fwd_fp8_call(xb, gamma.float().contiguous(), beta.float().contiguous(), None, hand,
+                          mean, rstd, groups, eps, x_bf16=x16)
+            out = placeholder(xb.shape, torch.bfloat16, xb.device)
         ctx.groups = groups
         ctx.x_dtype = x.dtype
         ctx.save_for_backward(xb, gamma, beta, mean, rstd)
@@ -216,11 +256,13 @@ class GroupNormSiLUTee(torch.autograd.Function):
         dx = dx.to(ctx.x_dtype)
         if dskip is not None and add is None:
             dx = dx + dskip.to(dx.dtype)
-        return dx, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, None
+        return dx, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, None, None
 
 
-def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5, skip_bf16: bool = False):
-    return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps, skip_bf16)
+def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5, skip_bf16: bool = False,
+                        hand: Fp8Handoff | None = None):
+    """With ``hand`` the first output is a placeholder and the e4m3 conv input is ``hand.q``."""
+    return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps, skip_bf16, hand)
 
 
 class GroupNormSiLUFilm(torch.autograd.Function):
@@ -231,23 +273,32 @@ class GroupNormSiLUFilm(torch.autograd.Function):
     the backward recomputes it from the same seed)."""
 
     @staticmethod
-    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0):
+    def forward(ctx: Any, x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0,
+                hand: Fp8Handoff | None = None, dx_hand: Fp8Handoff | None = None):
         n, c, h, w = x.shape
         xb, _ = _prep_x(x)
         wb = film_wb.contiguous()
         assert wb.dtype == torch.bfloat16 and wb.numel() == n * 2 * c
-        out = torch.empty_like(xb, dtype=torch.bfloat16, memory_format=torch.channels_last)
         mean = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         rstd = torch.empty(n * groups, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
         seed = DROPOUT_SEEDS.take(x.device) if p_drop > 0.0 else None
         if seed is not None and not dropout_ok(x):
             raise ValueError(f"fused dropout: no kernel form for {h}x{w} images")
-        _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps, seed, p_drop)
+        if dx_hand is not None and not (xb.dtype == torch.bfloat16
+                                        and fp8_ok(xb.shape, groups, dx_hand)):
+            raise ValueError("FP8 hand-off of dx: needs a bf16 x and a fused-cast form")
+        if hand is None:
+            out = torch.empty_like(xb, dtype=torch.bfloat16, memory_format=torch.channels_last)
+            _fwd_call(xb, g32, b32, None, None, wb, out, mean, rstd, groups, eps, seed, p_drop)
+        else:
+            _fwd_fp8_call(xb, g32, b32, wb, hand, mean, rstd, groups, eps, seed, p_drop)
+            out = placeholder(xb.shape, torch.bfloat16, xb.device)
         ctx.groups = groups
         ctx.x_dtype = x.dtype
         ctx.wb_shape = film_wb.shape
         ctx.p_drop = p_drop
+        ctx.dx_hand = dx_hand
         ctx.save_for_backward(xb, gamma, beta, mean, rstd, wb, seed)
         return out
 
@@ -263,6 +314,24 @@ class GroupNormSiLUFilm(torch.autograd.Function):
         ws_bytes = _lib.query("dpa_gn_silu_bwd_workspace_bytes", n, h * w, c, ctx.groups)
         ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
         dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
+        hand = ctx.dx_hand
+        if hand is not None:
+            # dx is the dy of the delayed-scaling conv that produced x: written as its e4m3
+            # operand, autograd gets a placeholder
+            dxq = torch.empty_like(xb, dtype=FP8_DTYPE, memory_format=torch.channels_last)
+            _lib.call(
+                "dpa_gn_silu_bwd_fp8",
+                xb.data_ptr(), dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+                beta.float().contiguous().data_ptr(), None, None, wb.data_ptr(),
+                mean.data_ptr(), rstd.data_ptr(), dxq.data_ptr(), hand.scale.data_ptr(),
+                hand.partials.data_ptr(), hand.partials.numel(), hand.count.data_ptr(),
+                dgamma.data_ptr(), dbeta.data_ptr(), None, None, dwb.data_ptr(), ws.data_ptr(),
+                ws_bytes, n, h * w, c, ctx.groups, None if seed is None else seed.data_ptr(),
+                float(ctx.p_drop), _stream(xb),
+            )
+            hand.q = dxq
+            return (placeholder(xb.shape, xb.dtype, xb.device), dgamma.to(gamma.dtype),
+                    dbeta.to(beta.dtype), None, None, dwb, None, None, None)
         _lib.call(
             "dpa_gn_silu_bwd_ex",
             xb.data_ptr(), dt, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
@@ -273,11 +342,15 @@ class GroupNormSiLUFilm(torch.autograd.Function):
             None if seed is None else seed.data_ptr(), float(ctx.p_drop), _stream(xb),
         )
         return (dx.to(ctx.x_dtype), dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, dwb,
-                None)
+                None, None, None)
 
 
-def group_norm_silu_film(x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0):
-    return GroupNormSiLUFilm.apply(x, gamma, beta, groups, eps, film_wb, float(p_drop))
+def group_norm_silu_film(x, gamma, beta, groups: int, eps: float, film_wb, p_drop: float = 0.0,
+                         hand: Fp8Handoff | None = None, dx_hand: Fp8Handoff | None = None):
+    """With ``hand`` the output is a placeholder and the e4m3 conv input is ``hand.q``; with
+    ``dx_hand`` the backward writes the e4m3 dx there (the dy of the conv producing x)."""
+    return GroupNormSiLUFilm.apply(x, gamma, beta, groups, eps, film_wb, float(p_drop), hand,
+                                   dx_hand)
 
 
 def group_norm_silu(x, gamma, beta, groups: int, eps: float = 1e-5, film_scale=None, film_shift=None):

@@ -11,6 +11,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .fp8_kernels import FP8_DTYPE, Fp8Handoff, placeholder
 
 # torch divides by a CPU scalar as a product with the fp32 reciprocal of the scalar
 INV_SQRT2 = float(np.float32(1.0) / np.float32(math.sqrt(2.0)))
@@ -35,19 +36,45 @@ def _scale(a: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
     return y
 
 
+def _bwd_fp8(g: torch.Tensor, hand: Fp8Handoff) -> torch.Tensor:
+    """The join's backward writing b's gradient as the e4m3 dy of the conv that produced b
+    (to hand.q); returns a's gradient (g's dtype)."""
+    ga = torch.empty_like(g)
+    gbq = torch.empty_like(g, dtype=FP8_DTYPE)
+    _lib.call("dpa_residual_scale_bwd_fp8", g.data_ptr(), _DT[g.dtype], ga.data_ptr(),
+              gbq.data_ptr(), hand.scale.data_ptr(), hand.partials.data_ptr(),
+              hand.partials.numel(), hand.count.data_ptr(), g.numel(), INV_SQRT2, _stream(g))
+    hand.q = gbq
+    return ga
+
+
+def _fp8_grad_ok(g: torch.Tensor, dtype: torch.dtype, hand: Fp8Handoff) -> bool:
+    n = g.numel()
+    return (g.dtype == dtype and n % 8 == 0 and g.data_ptr() % 16 == 0
+            and 0 < _lib.query("dpa_residual_scale_fp8_partials", n) <= hand.partials.numel())
+
+
 class ResidualScale(torch.autograd.Function):
     @staticmethod
-    def forward(ctx: Any, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def forward(ctx: Any, a: torch.Tensor, b: torch.Tensor,
+                hand: Fp8Handoff | None = None) -> torch.Tensor:
+        ctx.hand = hand
         return _scale(a, b)
 
     @staticmethod
     def backward(ctx: Any, g: torch.Tensor):
         g = g.contiguous(memory_format=torch.channels_last) if g.ndim == 4 else g.contiguous()
+        hand = ctx.hand
+        if hand is not None and _fp8_grad_ok(g, torch.bfloat16, hand):
+            return _bwd_fp8(g, hand), placeholder(g.shape, torch.bfloat16, g.device), None
         if g.dtype != torch.bfloat16 or g.numel() % 8 != 0:
             gs = g / math.sqrt(2.0)
         else:
             gs = _scale(g, None)
-        return gs, gs
+        if hand is not None:             # unfused: cast b's gradient in a pass of its own
+            hand.fill_from_bf16(gs)
+            return gs, placeholder(g.shape, torch.bfloat16, g.device), None
+        return gs, gs, None
 
 
 class ResidualScaleF32(torch.autograd.Function):
@@ -55,27 +82,58 @@ class ResidualScaleF32(torch.autograd.Function):
     rounded to bf16 for b."""
 
     @staticmethod
-    def forward(ctx: Any, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def forward(ctx: Any, a: torch.Tensor, b: torch.Tensor,
+                hand: Fp8Handoff | None = None) -> torch.Tensor:
         y = torch.empty_like(a)
         _lib.call("dpa_residual_scale_f32", a.data_ptr(), b.data_ptr(), y.data_ptr(), a.numel(),
                   INV_SQRT2, _stream(a))
+        ctx.hand = hand
         return y
 
     @staticmethod
     def backward(ctx: Any, g: torch.Tensor):
         g = g.contiguous(memory_format=torch.channels_last) if g.ndim == 4 else g.contiguous()
+        hand = ctx.hand
+        if hand is not None and _fp8_grad_ok(g, torch.float32, hand):
+            return _bwd_fp8(g, hand), placeholder(g.shape, torch.bfloat16, g.device), None
         if g.dtype != torch.float32:
             gs = g.float() / math.sqrt(2.0)
-            return gs, gs.to(torch.bfloat16)
-        ga = torch.empty_like(g)
-        gb = torch.empty_like(g, dtype=torch.bfloat16)
-        _lib.call("dpa_residual_scale_bwd_f32", g.data_ptr(), ga.data_ptr(), gb.data_ptr(),
-                  g.numel(), INV_SQRT2, _stream(g))
-        return ga, gb
+            ga, gb = gs, gs.to(torch.bfloat16)
+        else:
+            ga = torch.empty_like(g)
+            gb = torch.empty_like(g, dtype=torch.bfloat16)
+            _lib.call("dpa_residual_scale_bwd_f32", g.data_ptr(), ga.data_ptr(), gb.data_ptr(),
+                      g.numel(), INV_SQRT2, _stream(g))
+        if hand is not None:             # unfused: cast b's gradient in a pass of its own
+            hand.fill_from_bf16(gb)
+            return ga, placeholder(g.shape, torch.bfloat16, g.device), None
+        return ga, gb, None
 
 
-def residual_join(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """(a + b) / sqrt(2)."""
+def join_fp8_ok(a: torch.Tensor, b_shape) -> bool:
+    """Whether residual_join(a, b) with a hand-off can run for a channels-last bf16 b of
+    shape b_shape (b not formed yet)."""
+    return (a.is_cuda and tuple(a.shape) == tuple(b_shape) and a.ndim == 4
+            and a.is_contiguous(memory_format=torch.channels_last) and a.data_ptr() % 16 == 0
+            and a.dtype in (torch.bfloat16, torch.float32) and a.numel() % 8 == 0)
+
+
+def join_kernel_ok(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether residual_join(a, b) runs as one of the HIP Functions (b bf16)."""
+    return (a.is_cuda and _same_dense(a, b) and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
+            and b.dtype == torch.bfloat16 and a.dtype in (torch.bfloat16, torch.float32)
+            and a.numel() % 8 == 0)
+
+
+def residual_join(a: torch.Tensor, b: torch.Tensor, hand: Fp8Handoff | None = None) -> torch.Tensor:
+    """(a + b) / sqrt(2). With ``hand`` (b bf16, the output of a delayed-scaling FP8 conv, and
+    ``join_kernel_ok``) the backward writes b's gradient to hand.q as that conv's e4m3 dy."""
+    if hand is not None:
+        if not join_kernel_ok(a, b):
+            raise ValueError("FP8 hand-off through the residual join: no kernel for these operands")
+        if a.dtype == torch.bfloat16:
+            return ResidualScale.apply(a, b, hand)
+        return ResidualScaleF32.apply(a, b, hand)
     if a.is_cuda and _same_dense(a, b) and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0:
         if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.numel() % 8 == 0:
             return ResidualScale.apply(a, b)

@@ -33,9 +33,9 @@ import torch.nn.functional as F
 
 from . import fp8_kernels as K
 from .layer_norm import layer_norm_bf16
-from .residual import downsample2, residual_join, upsample_concat
+from .residual import downsample2, join_fp8_ok, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
-from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok
+from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok, fp8_ok as gn_fp8_ok
 from .gn_silu import group_norm_silu, group_norm_silu_film, group_norm_silu_tee
 from .gn_silu import supported as gn_supported
 
@@ -139,7 +139,32 @@ class Conv2dFP8(_PreparedFP8Weight, nn.Module):
         return (self.fp8_convs_enabled and self.fp8_all_convs and x.shape[1] % 128 == 0
                 and weight.shape[0] % 128 == 0)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def fp8_handoffs(self, x_shape) -> tuple[K.Fp8Handoff, K.Fp8Handoff] | None:
+        """Hand-offs (x, dy) for producers that write this conv's e4m3 operands, when an input
+        of x_shape takes the delayed-scaling path with the step's prepared weight; else None."""
+        if not (self.scaling_type == "delayed" and self.fused_window_update
+                and self.fp8_convs_enabled) or "forward" in vars(self):
+            return None                    # (an instance-level forward replaces this path)
+        cout = self.conv.weight.shape[0]
+        if (x_shape[1], cout, x_shape[2], x_shape[3]) not in K.SUPPORTED_UNET_SHAPES:
+            return None
+        pw = self._prepared("delayed")
+        if pw is None:
+            return None
+        return (K.Fp8Handoff(pw.hist[0], pw.parts[0], pw.parts[1]),
+                K.Fp8Handoff(pw.hist[2], pw.parts[2], pw.parts[3]))
+
+    def forward(self, x: torch.Tensor, xq: torch.Tensor | None = None,
+                dy_hand: K.Fp8Handoff | None = None) -> torch.Tensor:
+        """xq: the e4m3 input its producer wrote (x is then a placeholder); dy_hand: the
+        hand-off whose producer backward writes the e4m3 dy (see ``fp8_handoffs``)."""
+        if xq is not None or dy_hand is not None:
+            pw = self._prepared("delayed")
+            assert pw is not None, "FP8 hand-off without the step's prepared weight"
+            if xq is None:
+                x = x.contiguous(memory_format=torch.channels_last)
+            return K.Conv2dFP8DelayedPrepared.apply(
+                x, self.conv.weight, pw.q, pw.qt, pw.scale, pw.hist, pw.parts, xq, dy_hand)
         if self.conv_fp8(x, self.conv.weight):
             x = x.contiguous(memory_format=torch.channels_last)
             if self.scaling_type == "current":
@@ -235,8 +260,23 @@ class TimeEmbed(nn.Module):
         return self.mlp(t)[:, :, None, None]
 
 
+def _conv_handoff(conv: Conv2dFP8, h: torch.Tensor, xh: K.Fp8Handoff | None,
+                  dyh: K.Fp8Handoff | None) -> torch.Tensor:
+    if xh is None and dyh is None:
+        return conv(h)
+    return conv(h, None if xh is None else xh.q, dyh)
+
+
 class ResidualBlock(nn.Module):
-    """diffusion/unet.py:107-161."""
+    """diffusion/unet.py:107-161.
+
+    With ``fp8_handoff`` (delayed scaling, weights prepared for the step) the producers write
+    the e4m3 operands of the block's two FP8 convs directly, cast with the convs' window
+    scales, instead of bf16 tensors that a separate pass casts: GN1 conv_1's input, GN2
+    conv_2's input and, in its backward, conv_1's dy; the join's backward conv_2's dy. The
+    bytes and window records are those of the unfused path."""
+
+    fp8_handoff = True
 
     def __init__(self, config: UNetConfig, in_chann: int, out_chann: int, p_drop: float = 0.0):
         super().__init__()
@@ -259,31 +299,42 @@ class ResidualBlock(nn.Module):
         torch.nn.init.zeros_(self.conv_2.conv.weight)
 
     def forward(self, x: torch.Tensor, t: torch.Tensor):
-        if (self.fused and _on_gpu(x) and gn_supported(x.shape[1], self.norm1.num_groups)
-                and gn_dropout_ok(x)):
+        n, _, hh, ww = x.shape
+        y_shape = (n, self.conv_1.conv.out_channels, hh, ww)     # conv_1's and conv_2's output
+        gpu = self.fused and _on_gpu(x)
+        g1, g2 = self.norm1.num_groups, self.norm2.num_groups
+        fused1 = gpu and gn_supported(x.shape[1], g1) and gn_dropout_ok(x)
+        wb = self.t_embed_wb(t)
+        p_drop = self.dropout.p if self.training else 0.0
+        fused2 = (gpu and wb.dtype == torch.bfloat16 and gn_supported(y_shape[1], g2)
+                  and (p_drop == 0.0 or gn_dropout_ok(x)))
+        c1 = self.conv_1.fp8_handoffs(x.shape) if gpu and self.fp8_handoff else None
+        c2 = self.conv_2.fp8_handoffs(y_shape) if gpu and self.fp8_handoff else None
+        x1 = c1[0] if c1 and fused1 and gn_fp8_ok(x.shape, g1, c1[0]) else None
+        dy1 = c1[1] if c1 and fused2 and gn_fp8_ok(y_shape, g2, c1[1]) else None
+        x2 = c2[0] if c2 and fused2 and gn_fp8_ok(y_shape, g2, c2[0]) else None
+        if fused1:
             # the skip input's gradient is accumulated inside the GroupNorm backward
             # a 1x1 skip conv rounds its input to bf16 (FP8 path or autocast); the kernel
             # writes that copy as it reads x
             skip16 = (isinstance(self.skip_connection, Conv1x1FP8)
                       and torch.is_autocast_enabled("cuda"))
-            h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias,
-                                           self.norm1.num_groups, self.norm1.eps, skip16)
+            h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias, g1,
+                                           self.norm1.eps, skip16, x1)
         else:
             resid, h = x, norm_silu(self.norm1, x, self.fused)
-        x = self.conv_1(h)
-        wb = self.t_embed_wb(t)
-        p_drop = self.dropout.p if self.training else 0.0
-        if (self.fused and _on_gpu(x) and wb.dtype == torch.bfloat16
-                and gn_supported(x.shape[1], self.norm2.num_groups)
-                and (p_drop == 0.0 or gn_dropout_ok(x))):
+        x = _conv_handoff(self.conv_1, h, x1, dy1)
+        if fused2:
             # the kernel reads (w, b) from wb, forms bf16(w + 1) itself and applies the dropout
-            h = group_norm_silu_film(x, self.norm2.weight, self.norm2.bias,
-                                     self.norm2.num_groups, self.norm2.eps, wb, p_drop)
+            h = group_norm_silu_film(x, self.norm2.weight, self.norm2.bias, g2, self.norm2.eps,
+                                     wb, p_drop, x2, dy1)
         else:
             w, b = torch.chunk(wb, chunks=2, dim=1)
             h = self.dropout(norm_silu(self.norm2, x, self.fused, w + 1, b))
-        x = self.conv_2(h)
-        return residual_join(self.skip_connection(resid), x)
+        skip = self.skip_connection(resid)
+        dy2 = c2[1] if c2 and join_fp8_ok(skip, y_shape) else None
+        x = _conv_handoff(self.conv_2, h, x2, dy2)
+        return residual_join(skip, x, dy2)
 
 
 class _Attention(torch.autograd.Function):

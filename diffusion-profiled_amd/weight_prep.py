@@ -23,6 +23,9 @@ import torch
 from . import _lib
 from .fp8_kernels import FP8_DTYPE
 
+# amax partials per deferred window record that a producer-fused cast may leave
+PRODUCER_PARTIALS = 16384
+
 
 class DpaDeferredWindow(ctypes.Structure):
     """include/dpa_fp8.h ``DpaDeferredWindow``."""
@@ -73,8 +76,10 @@ class WeightPrep:
         self.n_delayed = len(delayed)
         self.scales = torch.zeros(2 * len(layers), device=dev, dtype=torch.float32)
         self.hist = torch.zeros(max(3 * self.n_delayed, 1), device=dev, dtype=torch.float32)
-        # deferred window records of the delayed layers' x / dy quantizations
-        cap = _lib.query("dpa_quant_partials_count", 1 << 40)   # the partial-count cap
+        # deferred window records of the delayed layers' x / dy quantizations: room for the
+        # standalone cast's partials and for those of the producers that cast for the layer
+        # (one per GroupNorm workgroup: 8192 for 512 channels of 32x32 images at batch 128)
+        cap = max(_lib.query("dpa_quant_partials_count", 1 << 40), PRODUCER_PARTIALS)
         self.dparts = torch.zeros((max(self.n_delayed, 1), 2, cap), device=dev, dtype=torch.int32)
         self.dcounts = torch.zeros((max(self.n_delayed, 1), 2), device=dev, dtype=torch.int32)
         deferred = (DpaDeferredWindow * max(self.n_delayed, 1))()

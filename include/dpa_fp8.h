@@ -28,6 +28,9 @@
  *                                     nn.Linear sites of diffusion/unet.py:171-172
  *   dpa_gn_silu_fwd_bf16 / _bwd    <- nn.GroupNorm + F.silu (+ FiLM) of diffusion/unet.py:151,
  *                                     :157-159 (Inductor-fused in the reference)
+ *   dpa_gn_silu_fwd_fp8 / _bwd_fp8, dpa_residual_scale_bwd_fp8
+ *                                  <- those producers with the delayed-scaling cast of the
+ *                                     conv they feed folded in (fp8_kernels.py:856, :885-893)
  */
 #ifndef DPA_FP8_H
 #define DPA_FP8_H
@@ -316,6 +319,36 @@ int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float
                        float* dfilm_shift, void* dfilm_wb, void* workspace,
                        int64_t workspace_bytes, int N, int HW, int C, int G, const void* drop_seed, float drop_p, void* stream);
 
+/* Producer-fused quantization for a delayed-scaling FP8 conv. Replaces the conv's separate
+ * input cast (diffusion/fp8_kernels.py:856, quantize_fp8_delayed at :518-556 with its
+ * partial_amax_kernel_delayed :69-87) after the GroupNorm+SiLU producers of
+ * diffusion/unet.py:151 and :157-160, and its dy cast (:885-893) after the GroupNorm
+ * backward that produces conv_1's dy. In delayed scaling the scale is the window's, known
+ * before the producer runs, so the producer writes the conv operand directly:
+ *   q = e4m3(clamp(bf16 value / *q_scale))   (the bf16-then-e4m3 double rounding)
+ * instead of the bf16 output (fwd) or bf16 dx (bwd), and each workgroup stores the amax of
+ * its bf16 values as bf16 magnitude bits in q_partials[workgroup], workgroup 0 the count in
+ * *q_count: the layout dpa_quantize_fp8_delayed_deferred_bf16 leaves for
+ * dpa_delayed_windows_finalize. Bytes and window record equal those of the unfused pair
+ * (bf16 entry, then the deferred cast). Arguments otherwise as dpa_gn_silu_fwd_ex /
+ * dpa_gn_silu_bwd_ex; the backward takes bf16 x and no dx_add. Only the chunked
+ * (256..8192 pixels) and small (<= 128 pixels) forms cast: other image sizes return
+ * DPA_ERR_SHAPE. q_partials_cap < dpa_gn_silu_fp8_partials(...) returns DPA_ERR_WORKSPACE. */
+int dpa_gn_silu_fp8_partials(int N, int HW, int C, int G);
+int dpa_gn_silu_fwd_fp8(const void* x, int x_dtype, const float* gamma, const float* beta,
+                        const float* film_scale, const float* film_shift, const void* film_wb,
+                        void* q, const float* q_scale, uint32_t* q_partials, int q_partials_cap,
+                        uint32_t* q_count, float* mean, float* rstd, void* workspace,
+                        int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
+                        const void* drop_seed, float drop_p, void* x_bf16, void* stream);
+int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float* gamma, const float* beta,
+                        const float* film_scale, const float* film_shift, const void* film_wb,
+                        const float* mean, const float* rstd, void* dxq, const float* dx_scale,
+                        uint32_t* dx_partials, int dx_partials_cap, uint32_t* dx_count,
+                        float* dgamma, float* dbeta, float* dfilm_scale, float* dfilm_shift,
+                        void* dfilm_wb, void* workspace, int64_t workspace_bytes, int N, int HW,
+                        int C, int G, const void* drop_seed, float drop_p, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Grouped FP8 weight preparation. No single counterpart in the reference: it performs, for a
  * model's whole FP8 weight set in three launches per step, what the reference does per layer
@@ -438,6 +471,18 @@ int dpa_residual_scale_f32(const float* a, const void* b, float* y, int64_t n, f
 /* Its backward: ga = g * inv (fp32), gb = bf16(g * inv), one pass over g. */
 int dpa_residual_scale_bwd_f32(const float* g, float* ga, void* gb, int64_t n, float inv,
                                void* stream);
+/* The join's backward when b is the output of a delayed-scaling FP8 conv (the conv_2 of
+ * diffusion/unet.py:160-161): b's gradient bf16(g * inv) is cast for that conv instead of
+ * stored -- gbq = e4m3(clamp(gb / *gb_scale)) with one amax partial per workgroup, as the
+ * fused GroupNorm entries above (replacing the conv's dy cast, diffusion/fp8_kernels.py:
+ * 885-893) -- and ga is stored as in the plain backward: fp32 g * inv for an fp32 g
+ * (g_dtype DPA_DTYPE_F32, the dpa_residual_scale_bwd_f32 form) or the bf16 values
+ * bf16(g * inv) for a bf16 g (the backward of dpa_residual_scale_bf16). n % 8 == 0;
+ * gb_partials_cap >= dpa_residual_scale_fp8_partials(n). */
+int dpa_residual_scale_fp8_partials(int64_t n);
+int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, void* gbq,
+                               const float* gb_scale, uint32_t* gb_partials, int gb_partials_cap,
+                               uint32_t* gb_count, int64_t n, float inv, void* stream);
 
 /* Decoder input of the U-Net: y = cat([up(a), h], dim=1) in NHWC, fp32, where up is the 2x
  * nearest upsampling (up = 1) or the identity (up = 0) -- diffusion/unet.py:389-392,
