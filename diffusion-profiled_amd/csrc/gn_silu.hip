@@ -145,25 +145,47 @@ __device__ __forceinline__ float group_sum(const float* hs, int half_idx, int cp
   return s;
 }
 
+// 8 consecutive floats (two 16-B loads when the address allows, as it does for torch's tensors)
+__device__ __forceinline__ void load8f(const float* src, float (&v)[8]) {
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const float4 a = reinterpret_cast<const float4*>(src)[0];
+    const float4 b = reinterpret_cast<const float4*>(src)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = src[e];
+  }
+}
+
 // FiLM scale/shift of channels ch..ch+7 of image n: fp32 [N][C] pairs, or the bf16 time
 // projection [N][2C] with scale bf16(w + 1) (the reference adds 1 in bf16) and shift b; no FiLM
 // gives 1 and 0.
 __device__ __forceinline__ bool load_film(const GnArgs& p, int n, int ch, float (&fsc)[8],
                                           float (&fsh)[8]) {
   if (p.fs) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      fsc[e] = p.fs[(int64_t)n * p.C + ch + e];
-      fsh[e] = p.fb[(int64_t)n * p.C + ch + e];
-    }
+    load8f(p.fs + (int64_t)n * p.C + ch, fsc);
+    load8f(p.fb + (int64_t)n * p.C + ch, fsh);
     return true;
   }
   if (p.wb) {
     const uint16_t* w = p.wb + (int64_t)n * 2 * p.C + ch;
+    float wf[8];
+    if ((reinterpret_cast<uintptr_t>(w) & 15) == 0) {  // (uniform: base alignment)
+      unpack8(*reinterpret_cast<const uint4*>(w), wf);
+      unpack8(*reinterpret_cast<const uint4*>(w + p.C), fsh);
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      fsc[e] = bf16_bits_to_f32((uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(w[e]) + 1.0f));
-      fsh[e] = bf16_bits_to_f32(w[p.C + e]);
+      for (int e = 0; e < 8; ++e) {
+        wf[e] = bf16_bits_to_f32(w[e]);
+        fsh[e] = bf16_bits_to_f32(w[p.C + e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const uint32_t pk = pack_bf16x2(wf[e] + 1.0f, wf[e + 1] + 1.0f);
+      fsc[e] = __uint_as_float(pk << 16);
+      fsc[e + 1] = __uint_as_float(pk & 0xffff0000u);
     }
     return true;
   }
@@ -599,11 +621,15 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx, GnQ
       float a[8];
       unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.dx_add) + off), a);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(f32_to_bf16_bits(v[e]) << 16) + a[e];
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t w = pack_bf16x2(v[e], v[e + 1]);
+        v[e] = __uint_as_float(w << 16) + a[e];
+        v[e + 1] = __uint_as_float(w & 0xffff0000u) + a[e + 1];
+      }
     }
     uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(v[e]) | (f32_to_bf16_bits(v[e + 1]) << 16);
+    for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(v[e], v[e + 1]);
     if (p.q)
       qo.put(p, off, uint4{o[0], o[1], o[2], o[3]});
     else
@@ -616,8 +642,43 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx, GnQ
 __device__ __forceinline__ void store_x_bf16(const GnArgs& p, int64_t off, const float (&f)[8]) {
   uint32_t o[4];
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) o[e >> 1] = f32_to_bf16_bits(f[e]) | (f32_to_bf16_bits(f[e + 1]) << 16);
+  for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(f[e], f[e + 1]);
   st_nt16(p.x_bf16 + off, uint4{o[0], o[1], o[2], o[3]});
+}
+
+// The forward's per-channel affine of this thread's 8 channels: out = silu(x A + B) with
+// A = rstd gamma and B = beta - mean A, both times the FiLM scale (plus its shift in B) --
+// normalise, affine and FiLM in one fma per element.
+template <bool kFilm>
+__device__ __forceinline__ void fwd_affine(const GnArgs& p, int n, int ch, const float (&mu)[2],
+                                           const float (&rs)[2], float (&A)[8], float (&B)[8]) {
+  float fsc[8], fsh[8], gm[8], bt[8];
+  if (kFilm) load_film(p, n, ch, fsc, fsh);
+  load8f(p.gamma + ch, gm);
+  load8f(p.beta + ch, bt);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = rs[e >> 2] * gm[e];
+    const float b = __builtin_fmaf(-mu[e >> 2], a, bt[e]);
+    A[e] = kFilm ? fsc[e] * a : a;
+    B[e] = kFilm ? __builtin_fmaf(fsc[e], b, fsh[e]) : b;
+  }
+}
+
+// 8 outputs silu(f A + B) (dropout: kept ones times drop_scale, the rest 0), packed bf16
+template <bool kDrop>
+__device__ __forceinline__ uint4 fwd_out8(const float (&f)[8], const float (&A)[8],
+                                          const float (&B)[8], uint32_t keep, float drop_scale) {
+  float z[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float t = __builtin_fmaf(f[e], A[e], B[e]);
+    float o = t * sigmoid_hw(t);
+    if (kDrop) o = (keep >> e) & 1u ? o * drop_scale : 0.0f;
+    z[e] = o;
+  }
+  return uint4{pack_bf16x2(z[0], z[1]), pack_bf16x2(z[2], z[3]), pack_bf16x2(z[4], z[5]),
+               pack_bf16x2(z[6], z[7])};
 }
 
 __device__ __forceinline__ int chunk_pixels(int HW, int chunk) {
@@ -693,7 +754,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_stats_kernel(const GnArgs
 
 // Forward, launch 2: merge the chunk statistics of the slab's groups in chunk order, then
 // normalise, affine, FiLM, SiLU, bf16 for this workgroup's chunk. Chunk 0 writes mean/rstd.
-template <bool kF32>
+template <bool kF32, bool kFilm, bool kDrop>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs p,
                                                                    const float2* __restrict__ cs,
                                                                    int nchunk) {
@@ -727,8 +788,9 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
       const float nb = (float)(chunk_pixels(p.HW, k) * p.cpg);
       const float nt = na + nb;
       const float d = b.x - mean;
-      mean += d * (nb / nt);
-      m2 += b.y + d * d * (na * nb / nt);
+      const float wgt = nb / nt;
+      mean += d * wgt;
+      m2 += b.y + d * d * (na * wgt);
       na = nt;
     }
     const float rs = 1.0f / sqrtf(m2 / na + p.eps);
@@ -746,71 +808,61 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
     mu[h] = st.x;
     rs[h] = st.y;
   }
-  float a[8], b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    a[e] = p.gamma[ch + e];
-    b[e] = p.beta[ch + e];
-  }
-  float fsc[8], fsh[8];
-  const bool film = load_film(p, n, ch, fsc, fsh);
+  float A[8], B[8];
+  fwd_affine<kFilm>(p, n, ch, mu, rs, A, B);
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
-  const bool drop = p.drop_seed != nullptr;
-  const uint64_t seed = drop ? *p.drop_seed : 0;
+  const uint64_t seed = kDrop ? *p.drop_seed : 0;
   GnQ qo(p);
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8];
     unpack_x<kF32>(v, u, f);
+    const int64_t off = ((int64_t)n * p.HW + pxs[u]) * p.C + ch;
     if constexpr (kF32) {
-      if (p.x_bf16 && ok[u]) store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f);
+      if (p.x_bf16 && ok[u]) store_x_bf16(p, off, f);
     }
-    const uint32_t kb =
-        drop ? drop_keep8(seed, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, p.drop_keep) : 0u;
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float z[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int ee = e + k;
-        float t = (f[ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
-        if (film) t = fsc[ee] * t + fsh[ee];
-        z[k] = t * sigmoid_hw(t);
-        if (drop) z[k] = (kb >> ee) & 1u ? z[k] * p.drop_scale : 0.0f;
-      }
-      o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
-    }
+    const uint32_t kb = kDrop ? drop_keep8(seed, off, p.drop_keep) : 0u;
+    const uint4 o = fwd_out8<kDrop>(f, A, B, kb, p.drop_scale);
     if (ok[u]) {
       if (p.q)
-        qo.put(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, uint4{o[0], o[1], o[2], o[3]});
+        qo.put(p, off, o);
       else
-        st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+        st_nt16(ob + (int64_t)pxs[u] * p.C, o);
     }
   }
   if (p.q) qo.finish(p, qred);
 }
 
-// The backward terms of one pixel's 8 channels (see gn_silu_bwd_kernel): g = d u / d zp
-// times dout, z = GN output; returns xhat, g and gz = g * fs.
+struct GnBwdSetup {
+  float mu[2], rs[2], nmr[2], gm[8], bt[8], fsc[8], fsh[8], gC[8];  // nmr = -mu rs, gC = fs gm
+};
+
+// The backward terms of one pixel's 8 channels (see gn_silu_bwd_kernel): xhat, and g = dout
+// times d silu(zp) / d zp at zp = fs (xhat gamma + beta) + fb (no FiLM: fs = 1, fb = 0).
+template <bool kFilm>
 __device__ __forceinline__ void bwd_terms(const float (&f)[8], const float (&d)[8],
-                                          const float (&mu)[2], const float (&rs)[2],
-                                          const float (&gm)[8], const float (&bt)[8],
-                                          const float (&fsc)[8], const float (&fsh)[8],
-                                          float (&xh)[8], float (&z)[8], float (&g)[8]) {
+                                          const GnBwdSetup& st, float (&xh)[8], float (&g)[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    xh[e] = (f[e] - mu[e >> 2]) * rs[e >> 2];
-    z[e] = xh[e] * gm[e] + bt[e];
-    const float zp = fsc[e] * z[e] + fsh[e];
+    xh[e] = __builtin_fmaf(f[e], st.rs[e >> 2], st.nmr[e >> 2]);
+    const float z = __builtin_fmaf(xh[e], st.gm[e], st.bt[e]);
+    const float zp = kFilm ? __builtin_fmaf(st.fsc[e], z, st.fsh[e]) : z;
     const float sg = sigmoid_hw(zp);
-    g[e] = d[e] * (sg * (1.0f + zp * (1.0f - sg)));
+    g[e] = d[e] * (sg * __builtin_fmaf(zp, 1.0f - sg, 1.0f));
   }
 }
 
-struct GnBwdSetup {
-  float mu[2], rs[2], gm[8], bt[8], fsc[8], fsh[8];
-};
+// dout of 8 channels, masked and scaled by the forward's dropout
+template <bool kDrop>
+__device__ __forceinline__ void bwd_dout(uint4 v, uint64_t seed, int64_t off, const GnArgs& p,
+                                         float (&d)[8]) {
+  unpack8(v, d);
+  if (kDrop) {
+    const uint32_t kb = drop_keep8(seed, off, p.drop_keep);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
+  }
+}
 
 template <bool kFilm>
 __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnBwdSetup& st) {
@@ -820,11 +872,8 @@ __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnB
     st.mu[h] = p.mean[n * p.G + g];
     st.rs[h] = p.rstd[n * p.G + g];
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    st.gm[e] = p.gamma[ch + e];
-    st.bt[e] = p.beta[ch + e];
-  }
+  load8f(p.gamma + ch, st.gm);
+  load8f(p.beta + ch, st.bt);
   if (kFilm) {
     load_film(p, n, ch, st.fsc, st.fsh);
   } else {  // compile-time identity: the FiLM terms fold away
@@ -834,13 +883,17 @@ __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnB
       st.fsh[e] = 0.0f;
     }
   }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) st.nmr[h] = -st.mu[h] * st.rs[h];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) st.gC[e] = kFilm ? st.fsc[e] * st.gm[e] : st.gm[e];
 }
 
 // Backward, launch 1: grid (C / 64, N, chunks). cp[chunk][n][c] = chunk sums of
 // (gz, gz * xhat, g * z, g) of channel c. FiLM scale/shift, gamma and beta are constant per
 // (image, channel), so all four follow from S1 = sum g and S2 = sum g * xhat:
 // (fs S1, fs S2, gamma S2 + beta S1, S1); only those two sums are accumulated.
-template <bool kFilm, bool kF32>
+template <bool kFilm, bool kF32, bool kDrop>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnArgs p,
                                                                       float4* __restrict__ cp) {
   constexpr int NS = 16;
@@ -851,8 +904,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const bool drop = p.drop_seed != nullptr;
-  const uint64_t seed = drop ? *p.drop_seed : 0;
+  const uint64_t seed = kDrop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -865,15 +917,10 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
   for (int k = 0; k < NS; ++k) acc[k] = 0.f;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
-    float f[8], d[8], xh[8], z[8], g[8];
+    float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    unpack8(v[in.kN - 1][u], d);
-    if (drop) {
-      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
-    }
-    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    bwd_terms<kFilm>(f, d, st, xh, g);
     if (ok[u]) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -897,7 +944,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_sums_kernel(const GnA
 // Backward, launch 2: per-channel totals over the chunks in order, group means of
 // gxh = gz * gamma and gxh * xhat, then dx for this chunk. Chunk 0 writes the per-image
 // channel partials of dgamma/dbeta and the FiLM gradients.
-template <bool kFilm, bool kF32>
+template <bool kFilm, bool kF32, bool kDrop>
 __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const GnArgs p,
                                                                        const float4* __restrict__ cp,
                                                                        int nchunk) {
@@ -911,8 +958,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const bool drop = p.drop_seed != nullptr;
-  const uint64_t seed = drop ? *p.drop_seed : 0;
+  const uint64_t seed = kDrop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -991,19 +1037,13 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   }
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
-    float f[8], d[8], xh[8], z[8], g[8];
+    float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    unpack8(v[in.kN - 1][u], d);
-    if (drop) {
-      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
-    }
-    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    bwd_terms<kFilm>(f, d, st, xh, g);
     auto dx = [&](int e) __attribute__((always_inline)) {
       const int h = e >> 2;
-      const float gxh = g[e] * st.fsc[e] * st.gm[e];
-      return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
+      return st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
     };
     if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
   }
@@ -1015,7 +1055,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
 // inputs once (the one-launch form's passes re-read them) ----
 constexpr int kSmallMaxHW = kChunkPx;
 
-template <bool kFilm, bool kF32>
+template <bool kFilm, bool kF32, bool kDrop>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p) {
   __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float red[(kChPLN / 8) * 8 * 2];
@@ -1086,54 +1126,27 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
       }
     }
   }
-  float a[8], b[8], fsc[8], fsh[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    a[e] = p.gamma[ch + e];
-    b[e] = p.beta[ch + e];
-  }
-  if (kFilm) {
-    load_film(p, n, ch, fsc, fsh);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      fsc[e] = 1.0f;
-      fsh[e] = 0.0f;
-    }
-  }
+  float A[8], B[8];
+  fwd_affine<kFilm>(p, n, ch, mu, rs, A, B);
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
-  const bool drop = p.drop_seed != nullptr;
-  const uint64_t seed = drop ? *p.drop_seed : 0;
+  const uint64_t seed = kDrop ? *p.drop_seed : 0;
   GnQ qo(p);
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
-    const uint32_t kb =
-        drop ? drop_keep8(seed, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, p.drop_keep) : 0u;
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      float z[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int ee = e + k;
-        float t = (f[u][ee] - mu[ee >> 2]) * rs[ee >> 2] * a[ee] + b[ee];
-        if (kFilm) t = fsc[ee] * t + fsh[ee];
-        z[k] = t * sigmoid_hw(t);
-        if (drop) z[k] = (kb >> ee) & 1u ? z[k] * p.drop_scale : 0.0f;
-      }
-      o[e >> 1] = f32_to_bf16_bits(z[0]) | (f32_to_bf16_bits(z[1]) << 16);
-    }
+    const int64_t off = ((int64_t)n * p.HW + pxs[u]) * p.C + ch;
+    const uint32_t kb = kDrop ? drop_keep8(seed, off, p.drop_keep) : 0u;
+    const uint4 o = fwd_out8<kDrop>(f[u], A, B, kb, p.drop_scale);
     if (ok[u]) {
       if (p.q)
-        qo.put(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, uint4{o[0], o[1], o[2], o[3]});
+        qo.put(p, off, o);
       else
-        st_nt16(ob + (int64_t)pxs[u] * p.C, uint4{o[0], o[1], o[2], o[3]});
+        st_nt16(ob + (int64_t)pxs[u] * p.C, o);
     }
   }
   if (p.q) qo.finish(p, qred);
 }
 
-template <bool kFilm, bool kF32>
+template <bool kFilm, bool kF32, bool kDrop>
 __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p) {
   __shared__ uint32_t qred[8 * kChPLN / 64];
   __shared__ float red[(kChPLN / 8) * 8 * 16];
@@ -1144,8 +1157,7 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
-  const bool drop = p.drop_seed != nullptr;
-  const uint64_t seed = drop ? *p.drop_seed : 0;
+  const uint64_t seed = kDrop ? *p.drop_seed : 0;
   const GnSrc<kF32, true> in(p, base);
   uint4 v[in.kN][kChU];
   bool ok[kChU];
@@ -1160,15 +1172,10 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   for (int k = 0; k < 16; ++k) acc[k] = 0.f;
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
-    float f[8], d[8], xh[8], z[8], g[8];
+    float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    unpack8(v[in.kN - 1][u], d);
-    if (drop) {
-      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
-    }
-    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    bwd_terms<kFilm>(f, d, st, xh, g);
     if (ok[u]) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1217,19 +1224,13 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   }
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
-    float f[8], d[8], xh[8], z[8], g[8];
+    float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    unpack8(v[in.kN - 1][u], d);
-    if (drop) {
-      const uint32_t kb = drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * p.drop_scale : 0.0f;
-    }
-    bwd_terms(f, d, st.mu, st.rs, st.gm, st.bt, st.fsc, st.fsh, xh, z, g);
+    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    bwd_terms<kFilm>(f, d, st, xh, g);
     auto dx = [&](int e) __attribute__((always_inline)) {
       const int h = e >> 2;
-      const float gxh = g[e] * st.fsc[e] * st.gm[e];
-      return st.rs[h] * (gxh - m1[h] - xh[e] * m2[h]);
+      return st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
     };
     if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
   }
@@ -1254,6 +1255,30 @@ static bool gn_shape_ok(int N, int HW, int C, int G) {
 }  // namespace dpa
 
 using namespace dpa;
+
+#include <type_traits>
+
+// Calls f(bool_constant<a>, bool_constant<b>, bool_constant<c>): one launch site for the
+// eight compile-time variants of a kernel.
+template <typename F>
+static void dispatch3(bool a, bool b, bool c, F f) {
+  auto lc = [&](auto A, auto B) {
+    if (c)
+      f(A, B, std::true_type{});
+    else
+      f(A, B, std::false_type{});
+  };
+  auto lb = [&](auto A) {
+    if (b)
+      lc(A, std::true_type{});
+    else
+      lc(A, std::false_type{});
+  };
+  if (a)
+    lb(std::true_type{});
+  else
+    lb(std::false_type{});
+}
 
 // The producer-fused e4m3 output of the fp8 entry points (GnArgs::q).
 struct GnQOut {
@@ -1354,23 +1379,18 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
       gn_chunk_stats_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
     int st = launch_status();
     if (st != DPA_OK) return st;
-    if (x_f32)
-      gn_chunk_apply_kernel<true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
-    else
-      gn_chunk_apply_kernel<false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
+    dispatch3(x_f32, a.fs || a.wb, a.drop_seed != nullptr, [&](auto F32, auto FILM, auto DROP) {
+      gn_chunk_apply_kernel<decltype(F32)::value, decltype(FILM)::value, decltype(DROP)::value>
+          <<<cgrid, 8 * kChPLN, 0, s>>>(a, cs, nchunk);
+    });
     return launch_status();
   }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
   if (HW <= kSmallMaxHW) {
-    const bool film = a.fs || a.wb;
-    if (film && x_f32)
-      gn_small_fwd_kernel<true, true><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else if (film)
-      gn_small_fwd_kernel<true, false><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else if (x_f32)
-      gn_small_fwd_kernel<false, true><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else
-      gn_small_fwd_kernel<false, false><<<grid, 8 * kChPLN, 0, s>>>(a);
+    dispatch3(a.fs || a.wb, x_f32, a.drop_seed != nullptr, [&](auto FILM, auto F32, auto DROP) {
+      gn_small_fwd_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
+          <<<grid, 8 * kChPLN, 0, s>>>(a);
+    });
     return launch_status();
   }
   const int pln = gn_pixel_lanes(HW);
@@ -1505,34 +1525,23 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
     // chunk sums after the 2*N*C per-image partials (16-B aligned: 8*N*C bytes, C % 64 == 0)
     float4* cp = (float4*)((float*)workspace + (int64_t)2 * N * C);
     dim3 cgrid((unsigned)(C / kSlab), (unsigned)N, (unsigned)nchunk);
-    if (film && x_f32)
-      gn_chunk_bwd_sums_kernel<true, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-    else if (film)
-      gn_chunk_bwd_sums_kernel<true, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-    else if (x_f32)
-      gn_chunk_bwd_sums_kernel<false, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
-    else
-      gn_chunk_bwd_sums_kernel<false, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    const bool drop = a.drop_seed != nullptr;
+    dispatch3(film, x_f32, drop, [&](auto FILM, auto F32, auto DROP) {
+      gn_chunk_bwd_sums_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
+          <<<cgrid, 8 * kChPLN, 0, s>>>(a, cp);
+    });
     st = launch_status();
     if (st != DPA_OK) return st;
-    if (film && x_f32)
-      gn_chunk_bwd_apply_kernel<true, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
-    else if (film)
-      gn_chunk_bwd_apply_kernel<true, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
-    else if (x_f32)
-      gn_chunk_bwd_apply_kernel<false, true><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
-    else
-      gn_chunk_bwd_apply_kernel<false, false><<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    dispatch3(film, x_f32, drop, [&](auto FILM, auto F32, auto DROP) {
+      gn_chunk_bwd_apply_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
+          <<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
+    });
   } else if (HW <= kSmallMaxHW) {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-    if (film && x_f32)
-      gn_small_bwd_kernel<true, true><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else if (film)
-      gn_small_bwd_kernel<true, false><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else if (x_f32)
-      gn_small_bwd_kernel<false, true><<<grid, 8 * kChPLN, 0, s>>>(a);
-    else
-      gn_small_bwd_kernel<false, false><<<grid, 8 * kChPLN, 0, s>>>(a);
+    dispatch3(film, x_f32, a.drop_seed != nullptr, [&](auto FILM, auto F32, auto DROP) {
+      gn_small_bwd_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
+          <<<grid, 8 * kChPLN, 0, s>>>(a);
+    });
   } else {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
     const int pln = gn_pixel_lanes(HW);
