@@ -147,6 +147,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 12 + [c_int] + [c_void_p] * 7 + [c_int64] + [c_int] * 4
         + [c_void_p, c_float, c_void_p],
     ),
+    "dpa_grouped_quantize_fp8_bf16": (c_int, [c_void_p, c_void_p, c_int, c_int] + [c_void_p] * 4),
+    "dpa_grouped_linear_fwd_fp8": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_grouped_linear_wgrad_fp8_f32": (c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p]),
+    "dpa_grouped_linear_dgrad_workspace_bytes": (c_int64, [c_int] * 3),
+    "dpa_grouped_linear_dgrad_fp8": (
+        c_int, [c_void_p] * 6 + [c_int] * 3 + [c_void_p, c_int64, c_void_p],
+    ),
     "dpa_residual_scale_fp8_partials": (c_int, [c_int64]),
     "dpa_residual_scale_bwd_fp8": (
         c_int, [c_void_p, c_int] + [c_void_p] * 4 + [c_int, c_void_p, c_int64, c_float, c_void_p],

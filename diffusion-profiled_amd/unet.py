@@ -32,6 +32,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import fp8_kernels as K
+from . import grouped as GR
 from .layer_norm import layer_norm_bf16
 from .residual import downsample2, join_fp8_ok, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
@@ -250,13 +251,20 @@ def norm_silu(norm: nn.GroupNorm, x: torch.Tensor, fused: bool, film_scale=None,
 
 
 class TimeEmbed(nn.Module):
-    """diffusion/unet.py:97-104."""
+    """diffusion/unet.py:97-104. ``_pre``: this forward's projection, computed with the other
+    blocks' in one grouped launch (UNet._group_films), taken by the next call."""
+
+    _pre = None
 
     def __init__(self, embed_channels: int, channels: int, fp8: bool = False):
         super().__init__()
         self.mlp = LinearFP8(embed_channels, channels, bias=False, fp8=fp8)
 
     def forward(self, t: torch.Tensor):
+        pre = self._pre
+        if pre is not None:
+            self._pre = None
+            return pre[:, :, None, None]
         return self.mlp(t)[:, :, None, None]
 
 
@@ -568,8 +576,42 @@ class UNet(nn.Module):
                 plan.active = False
                 plan.x_cache.clear()
 
+    # the FiLM projections of all residual blocks (the same t_emb) as one grouped FP8 op
+    group_films = True
+
+    def _group_films(self, t_emb: torch.Tensor) -> list:
+        """Runs every block's FiLM projection in one GroupedLinearFP8 when all of them take the
+        prepared FP8 linear path, leaving each result on its TimeEmbed; returns those modules."""
+        if not self.group_films or not t_emb.is_cuda or t_emb.ndim != 2:
+            return []
+        embeds = [m.t_embed_wb for m in self.modules() if isinstance(m, ResidualBlock)]
+        layers = []
+        for e in embeds:
+            lin = e.mlp
+            if (not isinstance(lin, LinearFP8) or not lin.fp8 or "forward" in vars(lin)
+                    or "forward" in vars(e) or lin.bias is not None):
+                return []
+            pw = lin._prepared("linear")
+            if pw is None:
+                return []
+            layers.append((pw.q, pw.qt, pw.scale))
+        if not GR.supported(t_emb.shape[0], t_emb.shape[1], [e.mlp.out_features for e in embeds]):
+            return []
+        outs = GR.grouped_linear_fp8(t_emb, layers, [e.mlp.weight for e in embeds])
+        for e, o in zip(embeds, outs):
+            e._pre = o
+        return embeds
+
     def _forward(self, x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
         t_emb = self.time_embed(self._timestep(t))
+        grouped = self._group_films(t_emb)
+        try:
+            return self._stages(x, t_emb)
+        finally:
+            for e in grouped:
+                e._pre = None
+
+    def _stages(self, x: torch.Tensor, t_emb: torch.Tensor) -> torch.Tensor:
         act = self.conv_in(x)
         hs = []
         for i, stage in enumerate(self.down_stages):

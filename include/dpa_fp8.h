@@ -427,6 +427,36 @@ int dpa_conv2d_wgrad_fp8_f32(const void* xq, const void* dyq, const float* x_sca
                              int R, int S, int stride, int pad, int split_k, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Grouped FP8 linear layers over one shared input x [M][K]: the FiLM projections of the U-Net's
+ * residual blocks (diffusion/unet.py:101-104, :135 -- every block's Linear(512, 2C) reads the
+ * same time embedding). No single counterpart in the reference (its Linears run per layer);
+ * per layer i (n_i output features) the arithmetic is the per-layer FP8 recipe with the
+ * layer's own per-tensor scales, one launch for all layers per direction:
+ *   quantize: q_i = e4m3(src_i / s_i), s_i = amax(src_i) > 0 ? RN32(amax / 448) : 1, as
+ *             dpa_quantize_fp8_bf16 (bytes and scales identical), written into one
+ *             concatenated [R][sum n_i] buffer q and/or its transpose qt [sum n_i][R];
+ *   forward:  y_i = bf16(RN32(acc * RN32(s_x s_wi))), y_i [M][n_i], w_i [n_i][K] e4m3;
+ *   wgrad:    dw_i = bf16(RN32(acc * RN32(s_x s_dyi))) stored as fp32 [n_i][K], from the
+ *             transposes xq_t [K][M] and dyq_t [sum n_i][M];
+ *   dgrad:    dx = bf16(sum_i RN32(acc_i * RN32(s_dyi s_wi))), the layers summed in fp32 in
+ *             order, from dyq [M][sum n_i] and the transposed weights w_i^T [K][n_i].
+ * At most 32 layers; n_i % 64 == 0 (dgrad: % 128), M % 64 == 0 (wgrad: % 128), K % 128 == 0.
+ * ---------------------------------------------------------------------------------------- */
+int dpa_grouped_quantize_fp8_bf16(const void* const* src, const int* n, int nseg, int R,
+                                  void* q, void* qt, float* scale, void* stream);
+int dpa_grouped_linear_fwd_fp8(const void* xq, const float* x_scale, const void* const* wq,
+                               const float* const* w_scale, void* const* y, const int* n,
+                               int nseg, int M, int K, void* stream);
+int dpa_grouped_linear_wgrad_fp8_f32(const void* xq_t, const float* x_scale, const void* dyq_t,
+                                     const float* dy_scale, float* const* dw, const int* n,
+                                     int nseg, int M, int K, void* stream);
+int64_t dpa_grouped_linear_dgrad_workspace_bytes(int nseg, int M, int K);
+int dpa_grouped_linear_dgrad_fp8(const void* dyq, const float* dy_scale, const void* const* wq_t,
+                                 const float* const* w_scale, void* dx, const int* n, int nseg,
+                                 int M, int K, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * LayerNorm over the channel axis of bf16 token rows [rows][C], fp32 statistics (biased
  * variance), bf16 out: the attention block's nn.LayerNorm (diffusion/unet.py:182, applied at
  * :186 to the [B, H*W, C] view of the channels-last activation; autocast runs it in fp32 and

@@ -330,11 +330,17 @@ def test_fragment_weight_convs_vs_oracle(K, shape):
 
 
 def test_fragment_weight_entries_refuse_other_shapes():
-    """The _wf entries serve only the halo-patch shapes (W 16 or 32, rows a multiple of
-    256 / W); other shapes and misaligned outputs return an error before any launch."""
+    """The _wf entries serve only the halo-patch shapes (W 16 or 32, rows a multiple of the
+    tile's row count); other shapes and misaligned outputs return an error before any launch.
+    The pointers are real buffers large enough for every call, so a call that were accepted
+    by mistake would fail the assertion, not read unmapped memory."""
     L = dpa_mod("_lib").load(build_if_missing=False)
-    fake, nul = 0x1000, None
-    assert L.dpa_conv2d_fwd_fp8_wf(fake, fake, fake, fake, nul, fake, 2, 8, 8, 256, 256, nul) == -4
-    assert L.dpa_conv2d_dgrad_fp8_wf(fake, fake, fake, fake, fake, 2, 12, 32, 128, 128, nul) == -4
-    assert L.dpa_conv2d_fwd_fp8_wf(fake, fake, fake, fake, nul, 0x1008, 2, 32, 32, 128, 128, nul) == -3
-    assert L.dpa_weight_frag_fp8(fake, fake, nul, 100, 3, 3, 128, nul) == -4
+    mb = 1 << 20
+    buf = torch.zeros(3 * mb, device="cuda", dtype=torch.uint8)
+    sc = torch.ones(2, device="cuda", dtype=torch.float32)
+    act, wgt, out, s, nul = buf.data_ptr(), buf.data_ptr() + mb, buf.data_ptr() + 2 * mb, sc.data_ptr(), None
+    assert L.dpa_conv2d_fwd_fp8_wf(act, wgt, s, s, nul, out, 2, 8, 8, 256, 256, nul) == -4
+    assert L.dpa_conv2d_dgrad_fp8_wf(act, wgt, s, s, out, 2, 10, 32, 128, 128, nul) == -4
+    assert L.dpa_conv2d_fwd_fp8_wf(act, wgt, s, s, nul, out + 8, 2, 32, 32, 128, 128, nul) == -3
+    assert L.dpa_weight_frag_fp8(wgt, act, nul, 100, 3, 3, 128, nul) == -4
+    torch.cuda.synchronize()
