@@ -4,7 +4,7 @@ Import with ``importlib.import_module("diffusion-profiled_amd")`` (the directory
 hyphen). The kernels live in ``lib/libdpa_fp8.so`` (C ABI: ``include/dpa_fp8.h``), built
 from ``csrc/*.hip`` by ``build.build_library()``.
 """
-from . import _lib, build, fp8_kernels, gn_silu  # noqa: F401
+from . import _lib, attention, build, fp8_kernels, gn_silu  # noqa: F401
 from . import ddpm, unet, trainer  # noqa: F401
 from .fp8_kernels import (  # noqa: F401
     FP8_DTYPE,

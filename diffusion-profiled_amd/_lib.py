@@ -96,6 +96,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "dpa_layernorm_fwd_ex": (c_int, [c_void_p, c_int] + [c_void_p] * 5 + [c_int64, c_int, c_float, c_void_p]),
     "dpa_layernorm_bwd_ex": (c_int, [c_void_p, c_int] + [c_void_p] * 8 + [c_int64, c_int64, c_int, c_void_p]),
+    "dpa_attention_fwd_bf16": (c_int, [c_void_p] * 3 + [c_int] * 4 + [c_void_p]),
+    "dpa_attention_bwd_bf16": (c_int, [c_void_p] * 5 + [c_int] * 4 + [c_void_p]),
     "dpa_residual_scale_bf16": (c_int, [c_void_p] * 3 + [c_int64, c_float, c_void_p]),
     "dpa_residual_scale_f32": (c_int, [c_void_p] * 3 + [c_int64, c_float, c_void_p]),
     "dpa_residual_scale_bwd_f32": (c_int, [c_void_p] * 3 + [c_int64, c_float, c_void_p]),

@@ -12,12 +12,15 @@ underneath differs:
   run as one fused HIP kernel each way (``gn_silu``).
 * With ``UNetConfig.fp8_linears`` the bias-free linears (time MLP, FiLM projection, qkv, out)
   and the 1x1 skip convs use the FP8 GEMM with current scaling.
-* Attention (diffusion/unet.py:181-203) is the reference's ``scaled_dot_product_attention``
-  on the GPU, limited to its fused kernels; ``_Attention`` (dense batched products, no
-  transposed-view operands) serves the CPU.
+* Attention (diffusion/unet.py:181-203): on the GPU the HIP self-attention kernels
+  (``attention``: q, k, v read in place from the qkv projection, head dim 64, up to 256
+  tokens), other shapes the reference's ``scaled_dot_product_attention`` limited to its fused
+  kernels; ``_Attention`` (dense batched products, no transposed-view operands) serves the CPU.
+  The attention LayerNorm, the residual joins, the decoder's upsample+concat and the encoder's
+  downsample are HIP kernels too.
 
-The torch ops around them (LayerNorm, interpolate, concat, the 3->128 and 128->3 convs whose
-channel counts the FP8 kernels do not take) stay in PyTorch-ROCm, as in the reference.
+The torch ops left (the 3->128 and 128->3 convs whose channel counts the FP8 kernels do not
+take, the time embedding's sinusoid) stay in PyTorch-ROCm, as in the reference.
 """
 from __future__ import annotations
 
@@ -33,6 +36,8 @@ import torch.nn.functional as F
 
 from . import fp8_kernels as K
 from . import grouped as GR
+from .attention import self_attention_qkv
+from .attention import supported as attn_supported
 from .layer_norm import layer_norm_bf16
 from .residual import downsample2, join_fp8_ok, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
@@ -383,6 +388,7 @@ class _Attention(torch.autograd.Function):
 
 
 _GPU_SDPA = True  # False: the dense formulation below on the GPU too
+_HIP_SDPA = True  # False: torch's fused SDPA kernels instead of the HIP self-attention
 
 
 def _fused_sdpa():
@@ -427,7 +433,12 @@ class CHWAttention(nn.Module):
             return t.reshape(b, h * w, self.nh, hd).transpose(1, 2).reshape(b * self.nh, h * w, hd)
 
         dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else q.dtype
-        if _on_gpu(x) and _GPU_SDPA:
+        if _on_gpu(x) and _GPU_SDPA and _HIP_SDPA and dt == torch.bfloat16 \
+                and attn_supported(h * w, c, self.nh):
+            # the HIP kernel: q, k, v read in place from qkv, the output written as
+            # "b l (nh hd)" (diffusion/unet.py:188-198 without the rearranges)
+            o = self_attention_qkv(qkv, self.nh)
+        elif _on_gpu(x) and _GPU_SDPA:
             # the reference's F.scaled_dot_product_attention (diffusion/unet.py:196), limited to
             # the fused (memory-efficient / flash) kernels: the math fallback would run bf16
             # batched products on transposed views

@@ -485,6 +485,24 @@ int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout, const flo
                          float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
                          int C, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Self-attention of the attention block, softmax(q k^T / sqrt(64)) v per (image, head), bf16
+ * in and out, fp32 softmax: replaces F.scaled_dot_product_attention with its head rearranges
+ * (diffusion/unet.py:188-198): q, k, v are read in place from the qkv projection's output
+ * qkv [B][L][3C] (q = columns [0, C), k = [C, 2C), v = [2C, 3C), head h at h*64 of each),
+ * the output is written as out [B][L][C] ("b nh l hd -> b l (nh hd)"), and
+ * lse [B*heads][L] (fp32, base-2 log-sum-exp of the scaled scores) is kept for the backward.
+ * Backward: dout [B][L][C] -> dqkv [B][L][3C] (dq, dk, dv in the qkv layout), recomputing the
+ * probabilities from lse. Deterministic (no atomics).
+ * C == 64 * heads; L % 16 == 0, 16 <= L <= 256 (the U-Net's 16x16, 8x8 and 4x4 token grids);
+ * qkv, out (backward), dout 16-B aligned; out (forward) and dqkv 8-B aligned.
+ * ---------------------------------------------------------------------------------------- */
+int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, int B, int L, int C,
+                           int heads, void* stream);
+int dpa_attention_bwd_bf16(const void* qkv, const void* out, const void* dout,
+                           const float* lse, void* dqkv, int B, int L, int C, int heads,
+                           void* stream);
+
 /* Residual join y = (a + b) / sqrt(2) of bf16 tensors in one pass (diffusion/unet.py:161 and
  * :203, under autocast), with torch's roundings: bf16(bf16(a + b) * inv), inv = RN32(1/sqrt 2)
  * passed by the caller. b == NULL gives y = bf16(a * inv) (the backward). n % 8 == 0,

@@ -90,6 +90,17 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_quantize_fp8_bf16_noalloc(fake, 0, fake, fake, nul) == -2
     assert lib.dpa_quantize_fp8_bf16_noalloc(fake, 16, fake, ctypes.c_void_p(0x1002), nul) == -3
     assert lib.dpa_quantize_fp8_bf16_noalloc_scratch_bytes() == lib.dpa_quant_workspace_bytes(1 << 40)
+    # self-attention: NULL, batch 0, heads that do not make 64-wide heads, L outside
+    # {16, 32, ..., 256}, misaligned qkv
+    assert lib.dpa_attention_fwd_bf16(nul, fake, fake, 2, 64, 256, 4, nul) == -1
+    assert lib.dpa_attention_fwd_bf16(fake, fake, fake, 0, 64, 256, 4, nul) == -2
+    assert lib.dpa_attention_fwd_bf16(fake, fake, fake, 2, 64, 256, 2, nul) == -4
+    assert lib.dpa_attention_fwd_bf16(fake, fake, fake, 2, 72, 256, 4, nul) == -4
+    assert lib.dpa_attention_fwd_bf16(fake, fake, fake, 2, 272, 256, 4, nul) == -4
+    assert lib.dpa_attention_fwd_bf16(ctypes.c_void_p(0x1008), fake, fake, 2, 64, 256, 4, nul) == -3
+    assert lib.dpa_attention_bwd_bf16(fake, fake, nul, fake, fake, 2, 64, 256, 4, nul) == -1
+    assert lib.dpa_attention_bwd_bf16(fake, fake, fake, fake, fake, 2, 8, 256, 4, nul) == -4
+    assert lib.dpa_attention_bwd_bf16(fake, fake, ctypes.c_void_p(0x1008), fake, fake, 2, 64, 256, 4, nul) == -3
     # workspace too small
     assert lib.dpa_quantize_fp8_bf16(fake, 16, fake, fake, fake, 8, nul) == -5
     assert lib.dpa_conv2d_dgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -5
