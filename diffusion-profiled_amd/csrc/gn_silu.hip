@@ -542,8 +542,8 @@ struct GnSrc {
 };
 
 // x of pixel u from the loaded parts
-template <bool kF32, int NL>
-__device__ __forceinline__ void unpack_x(const uint4 (&v)[NL][kChU], int u, float (&f)[8]) {
+template <bool kF32, int NL, int U>
+__device__ __forceinline__ void unpack_x(const uint4 (&v)[NL][U], int u, float (&f)[8]) {
   if constexpr (kF32) {
     const uint4 a = v[0][u], b = v[1][u];
     f[0] = __uint_as_float(a.x);
@@ -864,6 +864,17 @@ __device__ __forceinline__ void bwd_dout(uint4 v, uint64_t seed, int64_t off, co
   }
 }
 
+// the same with the keep bits already formed (the resident backward hashes once per pixel)
+template <bool kDrop>
+__device__ __forceinline__ void bwd_dout_kb(uint4 v, uint32_t kb, float drop_scale,
+                                            float (&d)[8]) {
+  unpack8(v, d);
+  if (kDrop) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * drop_scale : 0.0f;
+  }
+}
+
 template <bool kFilm>
 __device__ __forceinline__ void gn_bwd_setup(const GnArgs& p, int n, int ch, GnBwdSetup& st) {
 #pragma unroll
@@ -1050,15 +1061,39 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_bwd_apply_kernel(const Gn
   if (p.q) qo.finish(p, qred);
 }
 
-// ---- small images (HW <= 128 pixels: the 8x8 and 4x4 levels): one workgroup per (image,
-// slab) holds all of its pixels in registers, so the forward and the backward each read their
-// inputs once (the one-launch form's passes re-read them) ----
-constexpr int kSmallMaxHW = kChunkPx;
+// ---- resident form (HW <= kResMaxHW: the 32x32, 16x16, 8x8 and 4x4 levels): one workgroup
+// per (image, slab) of PLN pixel lanes x 8 granules holds all of the slab's pixels in
+// registers (U per lane, packed as loaded), so the forward and the backward each read their
+// inputs once and write their outputs once; every pass unpacks from those registers ----
+constexpr int kResMaxHW = 1024;
 
-template <bool kFilm, bool kF32, bool kDrop>
-__global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p) {
-  __shared__ uint32_t qred[8 * kChPLN / 64];
-  __shared__ float red[(kChPLN / 8) * 8 * 2];
+// v unchanged, but opaque to the optimiser (no value numbering across this point)
+__device__ __forceinline__ void opaque_u4(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
+// Lane pl's pixels pl + PLN u; pixels past HW load pixel HW - 1 (a valid address) with ok false.
+template <int NL, int PLN, int U>
+__device__ __forceinline__ void res_load(const uint8_t* const (&src)[NL], const int (&stride)[NL],
+                                         int pl, int HW, uint4 (&v)[NL][U], bool (&ok)[U],
+                                         int (&pxs)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int px = pl + u * PLN;
+    ok[u] = px < HW;
+    pxs[u] = ok[u] ? px : HW - 1;
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+      v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * stride[l]);
+}
+
+template <int PLN, int U, bool kFilm, bool kF32, bool kDrop>
+__global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
+  __shared__ uint32_t qred[PLN / 8];
+  __shared__ float red[(PLN / 8) * 8 * 2];
   __shared__ float hs[16];
   const int n = blockIdx.y;
   const int c0 = blockIdx.x * kSlab;
@@ -1066,28 +1101,31 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   const int pl = threadIdx.x >> 3;
   const int ch = c0 + gq * 8;
   const GnSrc<kF32, false> in(p, (int64_t)n * p.HW * p.C + ch);
-  uint4 v[in.kN][kChU];
-  bool ok[kChU];
-  int pxs[kChU];
-  chunk_load(in.src, in.stride, 0, pl, p.HW, v, ok, pxs);
-  float f[kChU][8];
-#pragma unroll
-  for (int u = 0; u < kChU; ++u) unpack_x<kF32>(v, u, f[u]);
+  uint4 v[in.kN][U];
+  bool ok[U];
+  int pxs[U];
+  res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
   if constexpr (kF32) {
     if (p.x_bf16) {
 #pragma unroll
-      for (int u = 0; u < kChU; ++u)
-        if (ok[u]) store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f[u]);
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) {
+          float f[8];
+          unpack_x<kF32>(v, u, f);
+          store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f);
+        }
     }
   }
   float sm[2] = {0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < kChU; ++u)
+  for (int u = 0; u < U; ++u)
     if (ok[u]) {
-      sm[0] += (f[u][0] + f[u][1]) + (f[u][2] + f[u][3]);
-      sm[1] += (f[u][4] + f[u][5]) + (f[u][6] + f[u][7]);
+      float f[8];
+      unpack_x<kF32>(v, u, f);
+      sm[0] += (f[0] + f[1]) + (f[2] + f[3]);
+      sm[1] += (f[4] + f[5]) + (f[6] + f[7]);
     }
-  slab_reduce<2, kChPLN>(sm, red);
+  slab_reduce<2, PLN>(sm, red);
   if (pl == 0) {
     hs[2 * gq] = sm[0];
     hs[2 * gq + 1] = sm[1];
@@ -1099,15 +1137,17 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   __syncthreads();
   float q[2] = {0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < kChU; ++u)
+  for (int u = 0; u < U; ++u)
     if (ok[u]) {
+      float f[8];
+      unpack_x<kF32>(v, u, f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float d = f[u][e] - mu[e >> 2];
+        const float d = f[e] - mu[e >> 2];
         q[e >> 2] += d * d;
       }
     }
-  slab_reduce<2, kChPLN>(q, red);
+  slab_reduce<2, PLN>(q, red);
   if (pl == 0) {
     hs[2 * gq] = q[0];
     hs[2 * gq + 1] = q[1];
@@ -1132,10 +1172,12 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   const uint64_t seed = kDrop ? *p.drop_seed : 0;
   GnQ qo(p);
 #pragma unroll
-  for (int u = 0; u < kChU; ++u) {
+  for (int u = 0; u < U; ++u) {
+    float f[8];
+    unpack_x<kF32>(v, u, f);
     const int64_t off = ((int64_t)n * p.HW + pxs[u]) * p.C + ch;
     const uint32_t kb = kDrop ? drop_keep8(seed, off, p.drop_keep) : 0u;
-    const uint4 o = fwd_out8<kDrop>(f[u], A, B, kb, p.drop_scale);
+    const uint4 o = fwd_out8<kDrop>(f, A, B, kb, p.drop_scale);
     if (ok[u]) {
       if (p.q)
         qo.put(p, off, o);
@@ -1146,10 +1188,21 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_fwd_kernel(const GnArgs p
   if (p.q) qo.finish(p, qred);
 }
 
-template <bool kFilm, bool kF32, bool kDrop>
-__global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p) {
-  __shared__ uint32_t qred[8 * kChPLN / 64];
-  __shared__ float red[(kChPLN / 8) * 8 * 16];
+// The backward keeps x in registers and, at 16 pixels per lane (where x and dout together
+// would exceed the register file), dout in LDS: DMA'd there at the start (lane i of a wave's
+// u-th transfer at 16-B slot u * 8 PLN + thread), read back by the same thread in both passes.
+template <int PLN, int U>
+struct GnResDout {
+  static constexpr bool kLds = U >= 16;
+  static constexpr int kBytes = kLds ? U * 8 * PLN * 16 : 16;
+};
+
+template <int PLN, int U, bool kFilm, bool kF32, bool kDrop>
+__global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
+  using DL = GnResDout<PLN, U>;
+  __shared__ __attribute__((aligned(16))) uint8_t dls[DL::kBytes];
+  __shared__ uint32_t qred[PLN / 8];
+  __shared__ float red[(PLN / 8) * 8 * 16];
   __shared__ float hs[2][16];
   const int n = blockIdx.y;
   const int c0 = blockIdx.x * kSlab;
@@ -1158,11 +1211,28 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   const int ch = c0 + gq * 8;
   const int64_t base = (int64_t)n * p.HW * p.C + ch;
   const uint64_t seed = kDrop ? *p.drop_seed : 0;
-  const GnSrc<kF32, true> in(p, base);
-  uint4 v[in.kN][kChU];
-  bool ok[kChU];
-  int pxs[kChU];
-  chunk_load(in.src, in.stride, 0, pl, p.HW, v, ok, pxs);
+  // x (and, without the LDS copy, dout) in registers
+  const GnSrc<kF32, !DL::kLds> in(p, base);
+  uint4 v[in.kN][U];
+  bool ok[U];
+  int pxs[U];
+  res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
+  if constexpr (DL::kLds) {
+    const uint32_t lbase =
+        __builtin_amdgcn_readfirstlane(LDS_ADDR(dls) + (uint32_t)(threadIdx.x & ~63) * 16);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      dma16_lds(p.dout + base + (int64_t)pxs[u] * p.C, lbase + (uint32_t)(u * 8 * PLN * 16));
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");  // the DMA writes are invisible to the compiler
+  }
+  // dout of pixel u
+  auto dout_u = [&](int u) __attribute__((always_inline)) {
+    if constexpr (DL::kLds)
+      return *reinterpret_cast<const uint4*>(dls + (u * 8 * PLN + threadIdx.x) * 16);
+    else
+      return v[in.kN - 1][u];
+  };
   GnBwdSetup st;
   gn_bwd_setup<kFilm>(p, n, ch, st);
   GnQ qo(p);
@@ -1170,11 +1240,13 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
   float acc[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+  uint32_t keep[U];  // the dropout keep bits of each pixel, hashed once for both passes
 #pragma unroll
-  for (int u = 0; u < kChU; ++u) {
+  for (int u = 0; u < U; ++u) {
     float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    keep[u] = kDrop ? drop_keep8(seed, base + (int64_t)pxs[u] * p.C, p.drop_keep) : 0u;
+    bwd_dout_kb<kDrop>(dout_u(u), keep[u], p.drop_scale, d);
     bwd_terms<kFilm>(f, d, st, xh, g);
     if (ok[u]) {
 #pragma unroll
@@ -1183,8 +1255,11 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
         acc[8 + e] += g[e] * xh[e];
       }
     }
+    // one pixel at a time: the packed inputs stay resident, each pixel's unpacked terms die
+    // before the next pixel's are formed (else the interleaved pixels exceed the registers)
+    __builtin_amdgcn_sched_barrier(0);
   }
-  slab_reduce<16, kChPLN>(acc, red);
+  slab_reduce<16, PLN>(acc, red);
   if (pl == 0) {
     const int64_t nc = (int64_t)p.N * p.C;
     float h1[2] = {0.f, 0.f}, h2[2] = {0.f, 0.f};
@@ -1223,18 +1298,41 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_small_bwd_kernel(const GnArgs p
     m2[h] = group_sum(hs[1], 2 * gq + h, p.cpg) * inv_cnt;
   }
 #pragma unroll
-  for (int u = 0; u < kChU; ++u) {
+  for (int u = 0; u < U; ++u) {
+    // the second pass forms the per-pixel terms again from the packed registers: hidden from
+    // the compiler, which would otherwise keep the first pass's unpacked terms of every
+    // pixel alive across the reduction (8-16 registers per pixel more)
+#pragma unroll
+    for (int l = 0; l < in.kN; ++l) opaque_u4(v[l][u]);
     float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
-    bwd_dout<kDrop>(v[in.kN - 1][u], seed, base + (int64_t)pxs[u] * p.C, p, d);
+    bwd_dout_kb<kDrop>(dout_u(u), keep[u], p.drop_scale, d);
     bwd_terms<kFilm>(f, d, st, xh, g);
     auto dx = [&](int e) __attribute__((always_inline)) {
       const int h = e >> 2;
       return st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
     };
     if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (p.q) qo.finish(p, qred);
+}
+
+// Resident-form geometry for an image of HW pixels: (pixel lanes, pixels per lane), or
+// (0, 0) when HW exceeds kResMaxHW.
+struct GnRes {
+  int pln, u;
+};
+static GnRes gn_res_shape(int HW) {
+  if (HW <= 128) return {32, 4};
+  if (HW <= 256) return {32, 8};
+  if (HW <= kResMaxHW) return {64, 16};
+  return {0, 0};
+}
+// The backward with an fp32 x holds 3 x 16 B per pixel: at 16 pixels per lane that exceeds the
+// register file, so images above 256 pixels take the chunked form.
+static bool gn_res_bwd_ok(int HW, bool x_f32) {
+  return HW <= kResMaxHW && (!x_f32 || HW <= 256);
 }
 
 static int gn_chunks(int HW) {
@@ -1289,12 +1387,12 @@ struct GnQOut {
   uint32_t* count;
 };
 
-// Workgroups of the launch that writes the output (one amax partial each), 0 for the forms
-// without the fused cast (128 < HW < 256 and HW > 8192 pixels).
+// Workgroups of the launch that writes the output (one amax partial each), 0 for the form
+// without the fused cast (HW > 8192 pixels).
 static int64_t gn_q_blocks(int N, int HW, int C) {
+  if (HW <= kResMaxHW) return (int64_t)(C / kSlab) * N;
   const int nchunk = gn_chunks(HW);
-  if (nchunk > 0) return (int64_t)(C / kSlab) * N * nchunk;
-  return HW <= kSmallMaxHW ? (int64_t)(C / kSlab) * N : 0;
+  return nchunk > 0 ? (int64_t)(C / kSlab) * N * nchunk : 0;
 }
 
 static int gn_set_q(GnArgs& a, const GnQOut* qo, int64_t nblk) {
@@ -1353,10 +1451,12 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   a.rstd = rstd;
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = eps;
   const int nchunk = gn_chunks(HW);
-  const bool chunked = nchunk > 0 && workspace && workspace_bytes >= gn_fwd_workspace(N, HW, G) &&
-                       aligned(workspace, 8);
-  // fp32 x and dropout: the chunked form (workspace) or the small-image form
-  if ((x_f32 || drop_seed) && !chunked && HW > kSmallMaxHW)
+  const GnRes rs = gn_res_shape(HW);
+  const bool resident = rs.pln > 0;
+  const bool chunked = !resident && nchunk > 0 && workspace &&
+                       workspace_bytes >= gn_fwd_workspace(N, HW, G) && aligned(workspace, 8);
+  // fp32 x and dropout: the resident form or the chunked form (workspace)
+  if ((x_f32 || drop_seed) && !chunked && !resident)
     return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
   if (x_bf16 && !x_f32) return DPA_ERR_SHAPE;  // the bf16 copy is of an fp32 x
   if (!aligned(x_bf16, 16)) return DPA_ERR_ALIGN;
@@ -1364,7 +1464,7 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
   if (qo) {
-    if (!chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+    if (!chunked && !resident) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
     const int qst = gn_set_q(a, qo, gn_q_blocks(N, HW, C));
     if (qst != DPA_OK) return qst;
     a.out = qo->q;  // not written: the kernels store through a.q
@@ -1386,10 +1486,16 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
     return launch_status();
   }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  if (HW <= kSmallMaxHW) {
+  if (resident) {
     dispatch3(a.fs || a.wb, x_f32, a.drop_seed != nullptr, [&](auto FILM, auto F32, auto DROP) {
-      gn_small_fwd_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
-          <<<grid, 8 * kChPLN, 0, s>>>(a);
+      constexpr bool kF = decltype(FILM)::value, k3 = decltype(F32)::value,
+                     kD = decltype(DROP)::value;
+      if (rs.u == 4)
+        gn_res_fwd_kernel<32, 4, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
+      else if (rs.u == 8)
+        gn_res_fwd_kernel<32, 8, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
+      else
+        gn_res_fwd_kernel<64, 16, kF, k3, kD><<<grid, 8 * 64, 0, s>>>(a);
     });
     return launch_status();
   }
@@ -1504,9 +1610,11 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   a.N = N; a.HW = HW; a.C = C; a.G = G; a.cpg = C / G; a.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   const int nchunk = gn_chunks(HW);
-  const bool chunked =
-      nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) && aligned(workspace, 16);
-  if ((x_f32 || drop_seed || dx_add) && !chunked && HW > kSmallMaxHW)
+  const GnRes rs = gn_res_shape(HW);
+  const bool resident = gn_res_bwd_ok(HW, x_f32);
+  const bool chunked = !resident && nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) &&
+                       aligned(workspace, 16);
+  if ((x_f32 || drop_seed || dx_add) && !chunked && !resident)
     return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
   if (!aligned(dx_add, 16)) return DPA_ERR_ALIGN;
   a.dx_add = dx_add;
@@ -1515,7 +1623,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   if (dst != DPA_OK) return dst;
   if (qo) {
     if (x_f32 || dx_add) return DPA_ERR_SHAPE;  // e4m3 of a bf16 dx, nothing added
-    if (!chunked && HW > kSmallMaxHW) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+    if (!chunked && !resident) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
     const int qst = gn_set_q(a, qo, gn_q_blocks(N, HW, C));
     if (qst != DPA_OK) return qst;
   }
@@ -1536,11 +1644,17 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
       gn_chunk_bwd_apply_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
           <<<cgrid, 8 * kChPLN, 0, s>>>(a, cp, nchunk);
     });
-  } else if (HW <= kSmallMaxHW) {
+  } else if (resident) {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);
     dispatch3(film, x_f32, a.drop_seed != nullptr, [&](auto FILM, auto F32, auto DROP) {
-      gn_small_bwd_kernel<decltype(FILM)::value, decltype(F32)::value, decltype(DROP)::value>
-          <<<grid, 8 * kChPLN, 0, s>>>(a);
+      constexpr bool kF = decltype(FILM)::value, k3 = decltype(F32)::value,
+                     kD = decltype(DROP)::value;
+      if (rs.u == 4)
+        gn_res_bwd_kernel<32, 4, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
+      else if (rs.u == 8)
+        gn_res_bwd_kernel<32, 8, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
+      else if constexpr (!k3)  // an fp32 x above 256 pixels takes the chunked form
+        gn_res_bwd_kernel<64, 16, kF, k3, kD><<<grid, 8 * 64, 0, s>>>(a);
     });
   } else {
     dim3 grid((unsigned)(C / kSlab), (unsigned)N);

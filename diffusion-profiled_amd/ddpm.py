@@ -15,6 +15,8 @@ from math import pi
 import torch
 import torch.nn.functional as F
 
+from . import _lib
+
 
 class EWMAWrapper:
     """diffusion/ddpm.py:10-28."""
@@ -138,4 +140,41 @@ class DiffusionWrapper:
         """Epsilon-prediction MSE (diffusion/ddpm.py:209-215)."""
         noised, _, target, t_tens = self.noise_batch(batch, t, eps)
         eps_pred = self.model(noised, t_tens)
+        if eps_pred.is_cuda:
+            return mse_loss_hip(eps_pred, target)
         return F.mse_loss(eps_pred, target)
+
+
+class MSELossHIP(torch.autograd.Function):
+    """F.mse_loss(pred, target) (mean) as autocast runs it -- both operands in fp32 -- with the
+    loss summed by the HIP library's deterministic two-launch reduction (dpa_mse_loss_f32):
+    torch's multi-block reductions record a memset in a captured graph, and replays of the
+    training step's graph have returned 0 for this loss. The gradient is torch's elementwise
+    2 (pred - target) / n * grad, returned in pred's dtype."""
+
+    @staticmethod
+    def forward(ctx, pred: torch.Tensor, target: torch.Tensor):
+        p = pred if pred.dtype in (torch.bfloat16, torch.float32) else pred.float()
+        tg = target.float()
+        if p.stride() != tg.stride() or not (p.is_contiguous() or p.is_contiguous(
+                memory_format=torch.channels_last)):
+            p, tg = p.contiguous(), tg.contiguous()
+        n = p.numel()
+        out = torch.empty((), device=p.device, dtype=torch.float32)
+        ws_bytes = _lib.query("dpa_mse_loss_workspace_bytes")
+        ws = torch.empty(ws_bytes, device=p.device, dtype=torch.uint8)
+        dt = 1 if p.dtype == torch.float32 else 0  # DPA_DTYPE_F32 / DPA_DTYPE_BF16
+        _lib.call("dpa_mse_loss_f32", p.data_ptr(), dt, tg.data_ptr(), n, out.data_ptr(),
+                  ws.data_ptr(), ws_bytes, torch.cuda.current_stream(p.device).cuda_stream)
+        ctx.save_for_backward(pred, target)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        pred, target = ctx.saved_tensors
+        d = (pred.float() - target.float()) * (2.0 / pred.numel())
+        return (d * grad).to(pred.dtype), None
+
+
+def mse_loss_hip(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    return MSELossHIP.apply(pred, target)

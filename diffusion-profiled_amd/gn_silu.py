@@ -6,8 +6,8 @@ Replaces the two Inductor-fused chains of the reference ResidualBlock
 conv consumes after its ``x.to(torch.bfloat16)`` (diffusion/fp8_kernels.py:835). An fp32 input
 (the residual stream below the first level and the decoder's concatenations are fp32 under
 autocast, as in the reference) is normalised as it is, as autocast's fp32 GroupNorm does, and
-its gradient is returned in fp32 by the kernels, for images the chunked (256+ pixels) and
-small-image (<= 128 pixels) forms take; other inputs are cast to bf16 first.
+its gradient is returned in fp32 by the kernels, for images of up to 8192 pixels (the
+resident form up to 1024 pixels, the chunked form above); other inputs are cast to bf16 first.
 """
 from __future__ import annotations
 
@@ -27,9 +27,10 @@ DTYPE_BF16, DTYPE_F32 = 0, 1  # include/dpa_fp8.h DPA_DTYPE_*
 
 
 def f32_input_ok(x: torch.Tensor) -> bool:
-    """fp32 x that the kernels read directly: chunked form (256..8192 pixels) or small (<= 128)."""
+    """fp32 x that the kernels read directly: resident (<= 1024 pixels) or chunked form
+    (<= 8192 pixels)."""
     hw = x.shape[2] * x.shape[3]
-    return x.dtype == torch.float32 and (hw <= 128 or 256 <= hw <= 64 * 128)
+    return x.dtype == torch.float32 and hw <= 64 * 128
 
 
 def _prep_x(x: torch.Tensor) -> tuple[torch.Tensor, int]:
@@ -66,9 +67,10 @@ def gn_silu_fwd(x, gamma, beta, groups, eps, film_scale=None, film_shift=None, x
 
 
 def dropout_ok(x: torch.Tensor) -> bool:
-    """Images whose GroupNorm+SiLU kernels also apply dropout (the chunked and small forms)."""
+    """Images whose GroupNorm+SiLU kernels also apply dropout (the resident and chunked forms,
+    up to 8192 pixels)."""
     hw = x.shape[2] * x.shape[3]
-    return hw <= 128 or 256 <= hw <= 64 * 128
+    return hw <= 64 * 128
 
 
 def new_dropout_seed(device) -> torch.Tensor:
@@ -106,7 +108,7 @@ DROPOUT_SEEDS = DropoutSeeds()
 
 def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0,
               x_bf16=None):
-    """The workspace form of the forward (chunked for images of 256+ pixels); x bf16 or fp32;
+    """The workspace form of the forward (chunked for images of 1025+ pixels); x bf16 or fp32;
     seed: dropout seed tensor (int64 [1]) or None."""
     n, c, h, w = x.shape
     ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)

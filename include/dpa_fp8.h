@@ -555,6 +555,15 @@ int dpa_downsample2_f32(const void* a, int a_dtype, float* y, int N, int H, int 
 int dpa_downsample2_bwd_f32(const float* gy, void* ga, int a_dtype, int N, int H, int W, int C,
                             void* stream);
 
+/* The training loss mean((pred - target)^2) of the DDPM step (diffusion/ddpm.py:209-215,
+ * F.mse_loss with both operands in fp32 under autocast): pred bf16 or fp32 (DPA_DTYPE_*),
+ * target fp32, same memory order, n elements; *out = fp32 loss. Deterministic (fixed-order
+ * partial sums in the workspace, then one workgroup), two launches, nothing cleared by a
+ * memset -- safe inside a captured HIP graph. */
+int64_t dpa_mse_loss_workspace_bytes(void);
+int dpa_mse_loss_f32(const void* pred, int pred_dtype, const float* target, int64_t n,
+                     float* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Optimizer tail of the training step (train.py:104-149): clip_grad_norm_(max_norm),
  * AdamW (torch.optim.AdamW, :253: betas, eps, weight_decay) and the EMA update (:256,

@@ -67,14 +67,14 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_gn_silu_fwd_ws_bf16(fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 8, 2, 1024, 128, 32, 1e-5, nul) == -5
     assert lib.dpa_gn_silu_fwd_ws_bf16(fake, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 96, 32, 1e-5, nul) == -4
     assert lib.dpa_gn_silu_fwd_ws_bf16(nul, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 128, 32, 1e-5, nul) == -1
-    # fused dropout: p outside [0, 1) and images without a dropout form (12 x 12) are refused
+    # fused dropout: p outside [0, 1) and images without a dropout form (96 x 96) are refused
     assert lib.dpa_gn_silu_fwd_ex(fake, 0, fake, fake, nul, nul, fake, fake, fake, fake, nul, 0, 1, 16, 128, 32, 1e-5, fake, 1.0, nul, nul) == -2
-    assert lib.dpa_gn_silu_fwd_ex(fake, 0, fake, fake, nul, nul, fake, fake, fake, fake, nul, 0, 1, 144, 128, 32, 1e-5, fake, 0.2, nul, nul) == -4
+    assert lib.dpa_gn_silu_fwd_ex(fake, 0, fake, fake, nul, nul, fake, fake, fake, fake, nul, 0, 1, 9216, 128, 32, 1e-5, fake, 0.2, nul, nul) == -4
     assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, fake, fake, fake, fake, nul, 0, fake, fake, nul, nul, fake, fake, 1 << 20, 1, 16, 128, 32, fake, -0.5, nul) == -2
     # dx_add: 16-B aligned, chunked or small-image form only; x_bf16 needs an fp32 x
     assert lib.dpa_gn_silu_fwd_ex(fake, 0, fake, fake, nul, nul, nul, fake, fake, fake, nul, 0, 1, 16, 128, 32, 1e-5, nul, 0.0, fake, nul) == -4
     assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, ctypes.c_void_p(0x1008), 0, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 16, 128, 32, nul, 0.0, nul) == -3
-    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 0, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 144, 128, 32, nul, 0.0, nul) == -4
+    assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 0, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 9216, 128, 32, nul, 0.0, nul) == -4
     # dx_add_dtype: BF16 or F32 only, and an fp32 dx_add only beside an fp32 x
     assert lib.dpa_gn_silu_bwd_ex(fake, 0, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 1, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 1024, 128, 32, nul, 0.0, nul) == -4
     assert lib.dpa_gn_silu_bwd_ex(fake, 1, fake, fake, fake, nul, nul, nul, fake, fake, fake, fake, 2, fake, fake, nul, nul, nul, fake, 1 << 20, 1, 1024, 128, 32, nul, 0.0, nul) == -4
@@ -101,6 +101,12 @@ def test_precondition_errors_return_before_launch(lib):
     assert lib.dpa_attention_bwd_bf16(fake, fake, nul, fake, fake, 2, 64, 256, 4, nul) == -1
     assert lib.dpa_attention_bwd_bf16(fake, fake, fake, fake, fake, 2, 8, 256, 4, nul) == -4
     assert lib.dpa_attention_bwd_bf16(fake, fake, ctypes.c_void_p(0x1008), fake, fake, 2, 64, 256, 4, nul) == -3
+    # the training loss: NULL, n = 0, dtype, workspace, alignment
+    assert lib.dpa_mse_loss_f32(nul, 0, fake, 16, fake, fake, 1024, nul) == -1
+    assert lib.dpa_mse_loss_f32(fake, 0, fake, 0, fake, fake, 1024, nul) == -2
+    assert lib.dpa_mse_loss_f32(fake, 2, fake, 16, fake, fake, 1024, nul) == -4
+    assert lib.dpa_mse_loss_f32(fake, 0, fake, 16, fake, fake, 8, nul) == -5
+    assert lib.dpa_mse_loss_f32(fake, 1, fake, 16, fake, ctypes.c_void_p(0x1002), 1024, nul) == -3
     # workspace too small
     assert lib.dpa_quantize_fp8_bf16(fake, 16, fake, fake, fake, 8, nul) == -5
     assert lib.dpa_conv2d_dgrad_fp8(fake, fake, fake, fake, fake, fake, 10, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -5

@@ -181,11 +181,11 @@ def test_gn_silu_film_from_time_projection_matches_split_form(G, n, c, h, w):
         assert torch.equal(got.detach(), ref.detach()), what
 
 
-@pytest.mark.parametrize("n,c,h,w,film", [(2, 128, 32, 32, True), (3, 256, 16, 16, False)])
+@pytest.mark.parametrize("n,c,h,w,film", [(2, 128, 40, 40, True), (1, 256, 36, 36, False)])
 def test_one_launch_and_chunked_forms_agree(G, n, c, h, w, film):
-    """Images of 256+ pixels run the chunked kernels when given the full workspace; the
-    one-launch kernels (no forward workspace, a backward workspace of only the per-image
-    partials) compute the same quantities with another summation order."""
+    """Images above 1024 pixels (beyond the resident form) run the chunked kernels when given
+    the full workspace; the one-launch kernels (no forward workspace, a backward workspace of
+    only the per-image partials) compute the same quantities with another summation order."""
     L = dpa_mod("_lib")
     x = cl(randn_bf16((n, c, h, w), seed=n + c, std=2.0))
     dout = cl(randn_bf16((n, c, h, w), seed=n + c + 1, std=1e-2))
@@ -286,12 +286,12 @@ def test_gn_silu_fp32_input_vs_oracle(G, n, c, h, w, film):
 
 def test_gn_silu_fp32_autograd_and_fallback(G):
     """Through the autograd Functions: an fp32 input keeps an fp32 gradient, equal to the
-    direct calls; a size outside the fp32 forms (12 x 12 = 144 pixels) is cast to bf16 first,
+    direct calls; a size outside the fp32 forms (96 x 96 = 9216 pixels) is cast to bf16 first,
     as before; the time-projection FiLM form takes fp32 x too."""
     n, c, groups = 2, 256, GROUPS
     g = torch.Generator().manual_seed(11)
     gamma, beta = (1.0 + 0.1 * torch.randn(c, generator=g)).cuda(), (0.1 * torch.randn(c, generator=g)).cuda()
-    for h in (16, 12):
+    for h in (16, 96):
         x = cl(torch.randn((n, c, h, h), generator=g) * 1.5)
         xr = x.clone().requires_grad_(True)
         y = G.group_norm_silu(xr, gamma, beta, groups, 1e-5)
@@ -431,7 +431,7 @@ def test_gn_silu_film_dropout_threshold_band(G, n, c, h, w, x32):
 
 def test_gn_silu_film_dropout_zero_p_and_fresh_masks(G):
     """p = 0 gives the undropped op bit for bit; two calls draw two seeds (different masks);
-    a size without a dropout form (12 x 12) is refused rather than silently undropped."""
+    a size without a dropout form (96 x 96) is refused rather than silently undropped."""
     n, c, h, w = 2, 256, 16, 16
     g = torch.Generator().manual_seed(5)
     x = cl((torch.randn((n, c, h, w), generator=g) + 0.5).to(torch.bfloat16))
@@ -445,19 +445,20 @@ def test_gn_silu_film_dropout_zero_p_and_fresh_masks(G):
     z1, z2 = (d1 == 0) & (a != 0), (d2 == 0) & (a != 0)
     assert 0.45 < z1.float().mean().item() < 0.55
     assert not torch.equal(z1, z2)
-    x12 = cl(torch.randn((n, c, 12, 12), generator=g).to(torch.bfloat16))
-    with pytest.raises(ValueError):
-        G.group_norm_silu_film(x12, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)
+    x96 = cl(torch.randn((n, c, 96, 96), generator=g).to(torch.bfloat16))
+    with pytest.raises(ValueError):  # 9216 pixels: no form with fused dropout
+        G.group_norm_silu_film(x96, gamma.cuda(), beta.cuda(), GROUPS, 1e-5, wb, 0.5)
 
 
 @pytest.mark.parametrize("n,c,h,w,x32", [(2, 128, 32, 32, True), (3, 256, 16, 16, False),
                                          (2, 512, 8, 8, True), (4, 256, 4, 4, False),
-                                         (2, 128, 12, 12, True)], ids=lambda v: str(v))
+                                         (2, 128, 12, 12, True), (1, 128, 96, 96, True)],
+                         ids=lambda v: str(v))
 def test_gn_silu_tee_accumulates_skip_gradient(G, n, c, h, w, x32):
     """GroupNormSiLUTee returns (silu(GroupNorm(x)), x); its backward adds the second output's
     gradient into dx in the kernel. x's gradient equals autograd's own accumulation over the
-    unfused pair (GroupNormSiLU on x and x used again) bit for bit, in fp32 and bf16; 12 x 12
-    (no fused form) takes the separate add."""
+    unfused pair (GroupNormSiLU on x and x used again) bit for bit, in fp32 and bf16; 96 x 96
+    (no fp32 form: x is cast to bf16) takes the separate add."""
     seed = n + c + h + 31
     g = torch.Generator().manual_seed(seed)
     x = torch.randn((n, c, h, w), generator=g) * 2.0 + 0.5

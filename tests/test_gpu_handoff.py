@@ -93,7 +93,9 @@ def test_gn_forward_casts_like_the_unfused_pair(n, c, h, w, x32, film):
         assert K.is_placeholder(out) and out.shape == ref.shape
         assert np.array_equal(q_bytes(hf.q), q_bytes(hu.q)), (s, (n, c, h, w))
         assert amax_bits(hf) == amax_bits(hu)
-        nblk = (c // 64) * n * (1 if h * w <= 128 else -(-(h * w) // 128))
+        # one partial per workgroup: one per (image, 64 channels) up to 1024 pixels (resident
+        # form), one per 128-pixel chunk of those above
+        nblk = (c // 64) * n * (1 if h * w <= 1024 else -(-(h * w) // 128))
         assert int(hf.count.item()) == nblk
         if ref16 is not None:
             assert torch.equal(x16.view(torch.int16), ref16.view(torch.int16))
