@@ -46,7 +46,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg2",
-                    choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1", "cfg4", "cfg5"])
+                    choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1", "cfg4", "cfg5", "gn32",
+                             "attn256"],
+                    help="gn32 / attn256: component lines (profiling evidence) for the fused "
+                         "GroupNorm and the self-attention kernels at cfg5's shapes")
     ap.add_argument("--no-unet", action="store_true", help="skip the U-Net step in the cfg2 line")
     ap.add_argument("--part", default=None,
                     help="profiling mode: run only this part (quantize|fwd|dgrad|wgrad) of the "
@@ -324,6 +327,77 @@ def unet_step_summary(steps, warmup):
     }
 
 
+class GroupNormWorkload:
+    """The residual block's second GroupNorm (diffusion/unet.py:157-160: GroupNorm(32) -> FiLM
+    from the bf16 time projection -> SiLU -> dropout 0.2) at the 32x32 level of cfg5,
+    [128, 128, 32, 32] bf16 channels-last, forward + backward. Algorithmic bytes: 4 B/element
+    forward (x in, y out), 6 B/element backward (x, dout in, dx out)."""
+
+    def __init__(self):
+        self.G = importlib.import_module("diffusion-profiled_amd.gn_silu")
+        n, c, h, w = 128, 128, 32, 32
+        cl = torch.channels_last
+        self.x = seeded((n, c, h, w), 0).cuda().contiguous(memory_format=cl).requires_grad_()
+        g = torch.Generator().manual_seed(1)
+        self.gamma = (1.0 + 0.1 * torch.randn(c, generator=g)).cuda()
+        self.beta = (0.1 * torch.randn(c, generator=g)).cuda()
+        self.wb = (0.3 * torch.randn((n, 2 * c, 1, 1), generator=g)).to(torch.bfloat16).cuda()
+        self.dout = seeded((n, c, h, w), 2, std=1e-2).cuda().contiguous(memory_format=cl)
+        self.elems = n * c * h * w
+        self.name = ("gn32: GroupNorm(32)+FiLM+SiLU+dropout 0.2, [128,128,32,32] bf16 NHWC, "
+                     "fwd+bwd (the residual block's norm2)")
+
+    def fwd(self):
+        return self.G.group_norm_silu_film(self.x, self.gamma, self.beta, 32, 1e-5, self.wb, 0.2)
+
+    def step(self):
+        self.x.grad = None
+        self.fwd().backward(self.dout)
+
+
+class AttentionWorkload:
+    """The attention of cfg5's 16x16 level (diffusion/unet.py:181-203): qkv [128, 256, 768]
+    bf16 (4 heads of 64), forward + backward. FLOP: forward 2 GEMMs (q k^T, p v) of
+    2 L^2 64 per (image, head); backward 5 (q k^T and dO v^T recomputed, dV, dK, dQ)."""
+
+    def __init__(self):
+        self.A = importlib.import_module("diffusion-profiled_amd.attention")
+        b, l, c = 128, 256, 256
+        g = torch.Generator().manual_seed(5)
+        self.qkv = torch.randn((b, l, 3 * c), generator=g).to(torch.bfloat16).cuda().requires_grad_()
+        self.dout = (torch.randn((b, l, c), generator=g) * 1e-2).to(torch.bfloat16).cuda()
+        self.gemm = 2.0 * b * 4 * l * l * 64
+        self.name = "attn256: self-attention, qkv [128,256,768] bf16, 4 heads of 64, fwd+bwd"
+
+    def fwd(self):
+        return self.A.self_attention_qkv(self.qkv, 4)
+
+    def step(self):
+        self.qkv.grad = None
+        self.fwd().backward(self.dout)
+
+
+def component_main(args):
+    """gn32 / attn256: fwd and fwd+bwd device times (HIP events around graph replays)."""
+    wl = GroupNormWorkload() if args.workload == "gn32" else AttentionWorkload()
+    t_fwd = time_part(wl.fwd, args.kernel_reps)
+    t_step = time_part(wl.step, args.kernel_reps)
+    t_bwd = t_step - t_fwd
+    if args.workload == "gn32":
+        kern = {"fwd": {"us": round(t_fwd, 2), "GB/s": round(4 * wl.elems / t_fwd / 1e3, 1)},
+                "bwd": {"us": round(t_bwd, 2), "GB/s": round(6 * wl.elems / t_bwd / 1e3, 1)}}
+        value, unit = round(10 * wl.elems / t_step / 1e3, 1), "GB/s"
+    else:
+        kern = {"fwd": {"us": round(t_fwd, 2), "TFLOP/s": round(2 * wl.gemm / t_fwd / 1e6, 1)},
+                "bwd": {"us": round(t_bwd, 2), "TFLOP/s": round(5 * wl.gemm / t_bwd / 1e6, 1)}}
+        value, unit = round(7 * wl.gemm / t_step / 1e6, 1), "TFLOP/s"
+    print(json.dumps({"metric": f"{args.workload} component throughput", "value": value,
+                      "unit": unit, "n_gpus": 1, "higher_is_better": True,
+                      "ms_per_step": round(t_step / 1e3, 4), "dtype": "bf16 (fp32 statistics)",
+                      "data": "synthetic (seeded N(0,1))", "config": {"workload": wl.name},
+                      "kernels": kern}), flush=True)
+
+
 def model_main(args):
     base = {
         "metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -507,6 +581,8 @@ def main():
         return
     if args.workload in ("cfg4", "cfg5"):
         return model_main(args)
+    if args.workload in ("gn32", "attn256"):
+        return component_main(args)
     wl = make_workload(K, args.workload)
 
     # per-part device times (HIP events on the launch stream)
