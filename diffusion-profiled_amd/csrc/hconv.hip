@@ -72,9 +72,18 @@ __device__ __attribute__((aligned(64))) uint8_t hc_zero16[64];
 __shared__ __attribute__((aligned(1024))) uint8_t hc_patch[2][kHcPatchBytes];
 __shared__ __attribute__((aligned(1024))) uint8_t hc_slot[kHcWaves][kHcSlotBytes];
 
-// Patch pixels sit at a 144-B pitch (128 B of channels + 16 B gap): the 16 pixels of a
-// fragment land on 16 distinct 4-bank groups (36 banks apart mod 64), and every tap's address
-// is the pixel's base plus a wave-uniform offset.
+// Patch pixels sit at a 144-B pitch (128 B of channels + 16 B gap), so consecutive pixels are
+// 9 16-B bank slots apart (64 banks = 16 slots), and every tap's address is the pixel's base
+// plus a wave-uniform offset. gfx950 serves a ds_read_b128 in four 16-lane cycles: per
+// half-wave, the lanes whose bits 2..4 have even parity (0-3, 12-15, 20-27) and the odd ones
+// (4-11, 16-19, 28-31). A fragment's lane l reads column l & 15 at K byte 32 (l >> 4), so a
+// cycle mixes columns 0-3, 12-15 at one K offset with columns 4-11 at the next (2 slots on);
+// with column c on pixel c of the run two columns share a slot in every cycle. Columns 4-11
+// take the run's even pixels and the others its odd pixels (hc_col_px): the slots 9 p of even
+// and odd pixels p are even and odd, the 2-slot shift keeps parity, and no cycle conflicts.
+__device__ __forceinline__ int hc_col_px(int c) {
+  return (c >= 4 && c < 12) ? 2 * (c - 4) : 2 * ((c & 3) | ((c >> 1) & 4)) + 1;
+}
 __device__ __forceinline__ v8i hc_frag2(const uint8_t* base, uint32_t a0) {
   const uint4 lo = *reinterpret_cast<const uint4*>(base + a0);
   const uint4 hi = *reinterpret_cast<const uint4*>(base + a0 + 16);
@@ -188,12 +197,13 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
     }
   };
 
-  // pixel fragment pf: lane (frow, fq) reads patch pixel centre + tap offset, granules 2 fq
-  // and 2 fq + 1; base address per pf, plus (dy * PC + dx) * 144 per tap
+  // pixel fragment pf: lane (frow, fq) reads pixel hc_col_px(frow) of the fragment's 16-pixel
+  // run (patch centre + tap offset), granules 2 fq and 2 fq + 1; base address per pf, plus
+  // (dy * PC + dx) * 144 per tap
   uint32_t abase[kHcPF];
 #pragma unroll
   for (int pf = 0; pf < kHcPF; ++pf) {
-    const int m = wm * kHcWM + pf * 16 + frow;
+    const int m = wm * kHcWM + pf * 16 + hc_col_px(frow);
     const int orow = m >> p.wshift, ocol = m & (p.W - 1);
     abase[pf] = (uint32_t)(((orow + 1) * p.PC + ocol + 1) * kHcPitch + 32 * fq);
   }
@@ -209,11 +219,12 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
     for (int j = 0; j < kHcPF; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // Epilogue per finished tile: bf16(RN32(acc * RN32(sa * sb)) [+ bias]). Lane (frow, fq)
-  // of block (cb, pf) holds channels 16 cb + 4 fq .. + 3 of pixel 16 pf + frow: all of them
-  // go into the wave's slot [128 px][64 B] first (granule g of row r at g ^ ((r >> 2) & 3):
-  // conflict-free both ways), then lane l reads pixel 16 pf + l / 4, granule l % 4 and stores
-  // 16 B nontemporally; a store instruction covers 16 pixels x 64 B. All writes before any
-  // read, so the LDS latency is paid once per tile, not once per fragment.
+  // of block (cb, pf) holds channels 16 cb + 4 fq .. + 3 of pixel 16 pf + hc_col_px(frow):
+  // all of them go into the wave's slot [128 px][64 B] first (granule g of row r at
+  // g ^ ((r >> 2) & 3): conflict-free both ways), then lane l reads pixel 16 pf + l / 4,
+  // granule l % 4 and stores 16 B nontemporally; a store instruction covers 16 pixels x 64 B.
+  // All writes before any read, so the LDS latency is paid once per tile, not once per
+  // fragment.
   uint8_t* slot = hc_slot[wave];
   auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
 #pragma unroll
@@ -228,7 +239,7 @@ __global__ __launch_bounds__(kHcThreads, 1) void hconv_fp8_kernel(const HconvArg
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[c + e];
         }
-        const int r = pf * 16 + frow, g = cb * 2 + (fq >> 1);
+        const int r = pf * 16 + hc_col_px(frow), g = cb * 2 + (fq >> 1);
         *reinterpret_cast<uint2*>(slot + r * 64 + ((g ^ ((r >> 2) & 3)) * 16) + (fq & 1) * 8) =
             uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         acc[cb][pf] = v4f{0.f, 0.f, 0.f, 0.f};
