@@ -60,6 +60,10 @@ def parse():
                          "calibration: a plain copy reads and writes exactly that many bytes)")
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hconv-phases", action="store_true",
+                    help="time attribution of the halo-patch conv on cfg2: builds a copy of "
+                         "csrc/hconv.hip with per-wave clock stamps in a temporary directory "
+                         "and reports where the launch's time goes")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     return ap.parse_args()
 
@@ -549,6 +553,123 @@ def cpu_baseline(wl, seconds):
             "host": host_identity()}
 
 
+# ---- time attribution of the halo-patch conv (a stamped copy of the kernel) ----
+# Markers in csrc/hconv.hip where the copy records s_memrealtime (100 MHz, device-wide) and
+# the shader cycle counter (s_memtime) from lane 0 of every wave: kernel entry, after each
+# chunk barrier, before it, around each tile's epilogue. The library itself carries no
+# instrumentation.
+_HCP_PATCHES = [
+    ("namespace dpa {\n",
+     "namespace dpa {\n__device__ unsigned long long g_hcp[4096 * 128];\n"
+     "#define HCP(slot) do { if ((threadIdx.x & 63) == 0) {"
+     " const unsigned long long i_ = (blockIdx.x * 8 + (threadIdx.x >> 6)) * 16 + (slot);"
+     " g_hcp[i_] = __builtin_amdgcn_s_memrealtime(); g_hcp[i_ + 8] = __builtin_readcyclecounter(); }"
+     " } while (0)\n", "first"),
+    ("  const int tid = threadIdx.x;\n  const int lane = tid & 63;\n",
+     "  HCP(0);\n  const int tid = threadIdx.x;\n  const int lane = tid & 63;\n", "once"),
+    ("    wait_lgkmcnt0();\n    lds_barrier();\n",
+     "    if (gc == 1) HCP(3);\n    wait_lgkmcnt0();\n    lds_barrier();\n    if (gc < 2) HCP(1 + gc);\n",
+     "once"),
+    ("    if (gc - j * p.KC == p.KC - 1) epilogue(cc.m0, cc.n0);\n",
+     "    if (gc - j * p.KC == p.KC - 1) { if (gc < 2) HCP(4 + 2 * gc); epilogue(cc.m0, cc.n0);"
+     " if (gc < 2) HCP(5 + 2 * gc); }\n", "once"),
+]
+_HCP_TAIL = """
+extern "C" int dpa_hcp_conv(const void* act, const void* wf, const float* sa, const float* sb,
+                            void* out, int N, int H, int W, int C, int Cout, int cus, void* s) {
+  return dpa::hconv_run(act, wf, sa, sb, nullptr, out, N, H, W, C, Cout, 0, 1, cus,
+                        (hipStream_t)s);
+}
+extern "C" int dpa_hcp_read(void* dst) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(dpa::g_hcp), sizeof(dpa::g_hcp));
+}
+"""
+
+
+def hconv_phases_main(args):
+    """cfg2 forward and data gradient through a stamped copy of the halo-patch conv, each
+    graph-replayed; prints the launch time (HIP events) split into the workgroups' phases."""
+    import ctypes
+    import subprocess
+    import tempfile
+    import numpy as np
+
+    B = importlib.import_module("diffusion-profiled_amd.build")
+    K = importlib.import_module("diffusion-profiled_amd.fp8_kernels")
+    src = open(os.path.join(B.CSRC_DIR, "hconv.hip")).read()
+    for old, new, mode in _HCP_PATCHES:
+        if src.count(old) < 1 or (mode == "once" and src.count(old) != 1):
+            raise RuntimeError(f"hconv.hip no longer has the marker {old.strip()[:50]!r}")
+        src = src.replace(old, new, 1)
+    src += _HCP_TAIL
+    tmp = tempfile.mkdtemp(prefix="hcp_")
+    gen, lib_path = os.path.join(tmp, "hconv_stamped.hip"), os.path.join(tmp, "libhcp.so")
+    with open(gen, "w") as f:
+        f.write(src)
+    cmd = [B.hipcc(), *B.HIPCC_FLAGS, "-shared", f"-I{B.CSRC_DIR}", gen, "-o", lib_path]
+    print("building the stamped copy:", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True, capture_output=True)
+    lib = ctypes.CDLL(lib_path)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    wl = make_workload(K, "cfg2")
+    wl.quantize()
+    y = torch.empty((wl.n, wl.h, wl.w, wl.cout), device="cuda", dtype=torch.bfloat16)
+    dx = torch.empty((wl.n, wl.h, wl.w, wl.cin), device="cuda", dtype=torch.bfloat16)
+    calls = {
+        "fwd": (wl.xq, wl.wq, wl.xs, wl.ws, y, wl.cin, wl.cout),
+        "dgrad": (wl.dyq, wl.wq_t, wl.dys, wl.ws, dx, wl.cout, wl.cin),
+    }
+    buf = np.zeros(4096 * 128, dtype=np.uint64)
+    out = {}
+    for name, (a, w, sa, sb, o, c, co) in calls.items():
+        def launch():
+            st = torch.cuda.current_stream().cuda_stream
+            r = lib.dpa_hcp_conv(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                                 ctypes.c_void_p(sa.data_ptr()), ctypes.c_void_p(sb.data_ptr()),
+                                 ctypes.c_void_p(o.data_ptr()), wl.n, wl.h, wl.w, c, co, cus,
+                                 ctypes.c_void_p(st))
+            assert r == 0, r
+        us_launch = time_part(launch, args.kernel_reps)
+        # the stamps hold the last launch of the last replay (graph-replayed, as timed)
+        assert lib.dpa_hcp_read(ctypes.c_void_p(buf.ctypes.data)) == 0
+        grid = (cus // 8) * 8
+        raw = buf.reshape(4096, 8, 16)[:grid].astype(np.int64)
+        s = raw[:, :, :8] / 100.0                                       # us
+        cyc = raw[:, :, 8:]                                             # shader cycles
+        w0 = s[:, 0, :]
+        t0 = s[:, :, 0].min()
+        span = s[:, :, 7].max() - t0
+        med = lambda v: round(float(np.median(v)), 2)
+        late = s[:, 4:, :]
+        early = s[:, :4, :]
+        out[name] = {
+            "launch_us (HIP events, graph-replayed)": round(us_launch, 2),
+            "workgroup span_us (first start to last end)": round(float(span), 2),
+            "outside the span (dispatch, end-of-kernel)": round(us_launch - float(span), 2),
+            "start skew_us (last workgroup start)": round(float(s[:, 0, 0].max() - t0), 2),
+            "prologue_us (first patch, barrier)": med(w0[:, 1] - w0[:, 0]),
+            "tile0_us waves 0-3 / 4-7": [med(early[:, :, 4] - early[:, :, 1]),
+                                         med(late[:, :, 4] - late[:, :, 1])],
+            "epilogue0_us waves 0-3 / 4-7": [med(early[:, :, 5] - early[:, :, 4]),
+                                             med(late[:, :, 5] - late[:, :, 4])],
+            "chunk-barrier wait_us (wave 0, after its epilogue)": med(w0[:, 2] - w0[:, 5]),
+            "tile1_us waves 0-3 / 4-7": [med(early[:, :, 6] - early[:, :, 2]),
+                                         med(late[:, :, 6] - late[:, :, 2])],
+            "epilogue1_us waves 0-3 / 4-7": [med(early[:, :, 7] - early[:, :, 6]),
+                                             med(late[:, :, 7] - late[:, :, 6])],
+            "mfma work per tile per SIMD_us at 2.4 GHz": round(2 * 9 * 16 * 32 / 2400.0, 2),
+            "shader clock_GHz over the tiles (s_memtime / s_memrealtime)": round(float(np.median(
+                (cyc[:, :, 6] - cyc[:, :, 1]) / ((s[:, :, 6] - s[:, :, 1]) * 1e3))), 3),
+            "tile0 shader cycles waves 0-3 / 4-7": [int(np.median(cyc[:, :4, 4] - cyc[:, :4, 1])),
+                                                    int(np.median(cyc[:, 4:, 4] - cyc[:, 4:, 1]))],
+            "mfma cycles per tile per SIMD (2 waves x 144 x 32)": 2 * 9 * 16 * 32,
+        }
+    print(json.dumps({"hconv_phases": out, "workload": "cfg2", "clock": "s_memrealtime 100 MHz",
+                      "medians": "over workgroups (and over the four waves of a group)"}),
+          flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -579,6 +700,8 @@ def main():
         torch.cuda.synchronize()
         print(f"{args.workload} {args.part} x {args.reps}", flush=True)
         return
+    if args.hconv_phases:
+        return hconv_phases_main(args)
     if args.workload in ("cfg4", "cfg5"):
         return model_main(args)
     if args.workload in ("gn32", "attn256"):
