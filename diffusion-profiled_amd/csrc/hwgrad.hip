@@ -50,8 +50,15 @@ struct HwgradArgs {
   int nchunks, splits, tiles, ci_tiles, total, per_xcd;
 };
 
-// dy rows (pixels, 128 B): granule g at g ^ ((r >> 1) ^ (r >> 4)) & 7, as in wgrad.hip.
-__device__ __forceinline__ int hw_dyswz(int row) { return ((row >> 1) ^ (row >> 4)) & 7; }
+// dy rows (pixels, 128 B): granule g at g ^ hw_dyswz(r). A fragment read (r = 32 q + 8 s + m,
+// q = lane >> 4, m = (lane & 15) >> 1) is served per half-wave on gfx950, lanes 0-31 then
+// 32-63, over 32 8-B bank slots: the granule must take 8 values across (m >> 1, q & 1) of a
+// half-wave, so bit 2 follows q & 1 (row bit 5) and bit 1 follows q >> 1 (row bit 6), each
+// XOR a bit of s: bit 0 = r1 ^ r4, bit 1 = r2 ^ r6, bit 2 = r5 ^ r3.
+__device__ __forceinline__ int hw_dyswz(int row) {
+  return (((row >> 1) ^ (row >> 4)) & 1) | ((((row >> 2) ^ (row >> 6)) & 1) << 1) |
+         ((((row >> 5) ^ (row >> 3)) & 1) << 2);
+}
 __device__ __forceinline__ constexpr int hw_c(int s) { return ((s & 1) << 2) ^ (s >> 1); }
 
 // x pixels (64 B = 4 granules): granule g at g ^ bit 2 of the pixel index. A transpose read
@@ -278,7 +285,7 @@ __global__ __launch_bounds__(kHwThreads, 1) void hwgrad_partial_kernel(const Hwg
     const int k = lane & 15, q = lane >> 4, m = k >> 1, h = k & 1;
     uint32_t Td[8], T0[8], T1[8];
     {
-      const int L = (m >> 1) ^ (2 * q);
+      const int L = (m >> 1) ^ (2 * (q >> 1)) ^ (4 * (q & 1));  // hw_dyswz(32 q + m)
       const uint32_t lb = (uint32_t)((32 * q + m) * 128 + 8 * h);
 #pragma unroll
       for (int u = 0; u < 8; ++u) Td[u] = lb + 16u * (uint32_t)((u ^ (4 * wo)) ^ L);
