@@ -16,6 +16,7 @@ import torch
 from torch.amp.autocast_mode import custom_bwd, custom_fwd
 
 from . import _lib
+from . import fp8_kernels as _fp8
 
 HEAD_DIM = 64
 
@@ -43,8 +44,15 @@ class SelfAttentionQKV(torch.autograd.Function):
         x = qkv.to(torch.bfloat16).contiguous()
         out = torch.empty((b, l, c), device=x.device, dtype=torch.bfloat16)
         lse = torch.empty((b * heads, l), device=x.device, dtype=torch.float32)
-        _lib.call("dpa_attention_fwd_bf16", x.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                  b, l, c, heads, _stream(x))
+        if _fp8.PRODUCER_AMAX:
+            # one |out| maximum per (image, head) for the out projection's e4m3 cast
+            part = torch.empty(b * heads, device=x.device, dtype=torch.int32)
+            _lib.call("dpa_attention_fwd_amax", x.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                      b, l, c, heads, part.data_ptr(), _stream(x))
+            _fp8.mark_amax_partials(out, part, b * heads)
+        else:
+            _lib.call("dpa_attention_fwd_bf16", x.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                      b, l, c, heads, _stream(x))
         ctx.save_for_backward(x, out, lse)
         ctx.heads = heads
         ctx.in_dtype = qkv.dtype
@@ -57,6 +65,13 @@ class SelfAttentionQKV(torch.autograd.Function):
         b, l, c3 = x.shape
         g = dout.to(torch.bfloat16).contiguous()
         dqkv = torch.empty_like(x)
+        if _fp8.PRODUCER_AMAX and ctx.in_dtype == torch.bfloat16:
+            # one |dqkv| maximum per (image, head) for the qkv projection's e4m3 cast of dy
+            part = torch.empty(b * ctx.heads, device=x.device, dtype=torch.int32)
+            _lib.call("dpa_attention_bwd_amax", x.data_ptr(), out.data_ptr(), g.data_ptr(),
+                      lse.data_ptr(), dqkv.data_ptr(), b, l, c3 // 3, ctx.heads,
+                      part.data_ptr(), _stream(x))
+            return _fp8.mark_amax_partials(dqkv, part, b * ctx.heads), None
         _lib.call("dpa_attention_bwd_bf16", x.data_ptr(), out.data_ptr(), g.data_ptr(),
                   lse.data_ptr(), dqkv.data_ptr(), b, l, c3 // 3, ctx.heads, _stream(x))
         return dqkv.to(ctx.in_dtype), None

@@ -78,8 +78,34 @@ struct AttnArgs {
   const uint16_t* dout; // [B][L][C] bf16 (backward)
   uint16_t* out;        // forward: o; backward: dqkv [B][L][3C]
   float* lse;           // [B * heads][L]: log2 of sum_k 2^(s * log2(e) / 8)
+  uint32_t* amax_part;  // optional: per-workgroup max |out| (bf16 magnitude bits)
   int L, C, heads;
 };
+
+// Four fp32 -> two packed bf16 words, their magnitudes folded into am (u16 max per half).
+__device__ __forceinline__ uint2 att_pack4(float a, float b, float c, float d, us2& am) {
+  const uint2 w = uint2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
+  am = __builtin_elementwise_max(am, __builtin_bit_cast(us2, w.x & 0x7fff7fffu));
+  am = __builtin_elementwise_max(am, __builtin_bit_cast(us2, w.y & 0x7fff7fffu));
+  return w;
+}
+
+// The workgroup's max of what it stored, for the consumer's current-scaling cast; every
+// thread calls it (uniform), NW waves.
+template <int NW>
+__device__ __forceinline__ void att_store_partial(us2 am, uint32_t* part) {
+  __shared__ uint32_t red[NW];
+  uint32_t m = am.x > am.y ? am.x : am.y;
+  m = wave_max_u32(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = r > red[w] ? r : red[w];
+    part[blockIdx.x] = r;
+  }
+}
 
 // ---------------------------------------------------------------------------------------
 // Forward: one workgroup (4 waves) per (image, head); K and V rows of the head in LDS
@@ -138,6 +164,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs p) {
   }
   __syncthreads();
 
+  us2 am = {0, 0};
   for (int q0 = wave * 16; q0 < L; q0 += 64) {
     uint4 nq0 = {0u, 0u, 0u, 0u}, nq1 = {0u, 0u, 0u, 0u};
     if (q0 + 64 < L) {
@@ -204,11 +231,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs p) {
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb)
       *reinterpret_cast<uint2*>(orow + 16 * hb) =
-          uint2{pack_bf16x2(o[hb][0] * il, o[hb][1] * il), pack_bf16x2(o[hb][2] * il, o[hb][3] * il)};
+          att_pack4(o[hb][0] * il, o[hb][1] * il, o[hb][2] * il, o[hb][3] * il, am);
     if (fq == 0) p.lse[(int64_t)bh * L + q0 + frow] = mc + __builtin_amdgcn_logf(l);
     qf0 = nq0;
     qf1 = nq1;
   }
+  if (p.amax_part) att_store_partial<4>(am, p.amax_part);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -328,6 +356,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
   };
   if (kact) load_a(0);
 
+  us2 am = {0, 0};
   for (int q0 = 0, blk = 0; q0 < L; q0 += 32, ++blk) {
     uint16_t* ds = dsb[blk & 1];
     if (kact) {
@@ -392,8 +421,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
       const int q = q0 + 16 * sub + frow;
       if (q < L)
         *reinterpret_cast<uint2*>(dqg + q * S3 + 16 * hb + 4 * fq) =
-            uint2{pack_bf16x2(acc[0] * kAttScale, acc[1] * kAttScale),
-                  pack_bf16x2(acc[2] * kAttScale, acc[3] * kAttScale)};
+            att_pack4(acc[0] * kAttScale, acc[1] * kAttScale, acc[2] * kAttScale,
+                      acc[3] * kAttScale, am);
     }
   }
 
@@ -407,13 +436,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
       for (int hb = 0; hb < 4; ++hb) {
         const v4f k4 = dkt[hb][kb], v4 = dvt[hb][kb];
         *reinterpret_cast<uint2*>(dkg + key * S3 + 16 * hb + 4 * fq) =
-            uint2{pack_bf16x2(k4[0] * kAttScale, k4[1] * kAttScale),
-                  pack_bf16x2(k4[2] * kAttScale, k4[3] * kAttScale)};
+            att_pack4(k4[0] * kAttScale, k4[1] * kAttScale, k4[2] * kAttScale,
+                      k4[3] * kAttScale, am);
         *reinterpret_cast<uint2*>(dvg + key * S3 + 16 * hb + 4 * fq) =
-            uint2{pack_bf16x2(v4[0], v4[1]), pack_bf16x2(v4[2], v4[3])};
+            att_pack4(v4[0], v4[1], v4[2], v4[3], am);
       }
     }
   }
+  if (p.amax_part) att_store_partial<8>(am, p.amax_part);
 }
 
 static int attn_lp(int L) {
@@ -435,8 +465,8 @@ static int attn_check(const void* a, const void* b, const void* c, int B, int L,
 
 using namespace dpa;
 
-extern "C" int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, int B, int L,
-                                      int C, int heads, void* stream) {
+static int attn_fwd(const void* qkv, void* out, float* lse, int B, int L, int C, int heads,
+                    uint32_t* amax_part, void* stream) {
   int st = attn_check(qkv, out, lse, B, L, C, heads);
   if (st != DPA_OK) return st;
   if (!aligned(qkv, 16) || !aligned(out, 8) || !aligned(lse, 4)) return DPA_ERR_ALIGN;
@@ -444,6 +474,7 @@ extern "C" int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, in
   a.qkv = (const uint16_t*)qkv;
   a.out = (uint16_t*)out;
   a.lse = lse;
+  a.amax_part = amax_part;
   a.L = L;
   a.C = C;
   a.heads = heads;
@@ -458,9 +489,24 @@ extern "C" int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, in
   return launch_status();
 }
 
-extern "C" int dpa_attention_bwd_bf16(const void* qkv, const void* out, const void* dout,
-                                      const float* lse, void* dqkv, int B, int L, int C,
-                                      int heads, void* stream) {
+extern "C" int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, int B, int L,
+                                      int C, int heads, void* stream) {
+  return attn_fwd(qkv, out, lse, B, L, C, heads, nullptr, stream);
+}
+
+// dpa_attention_fwd_bf16 that also leaves one amax partial per (image, head) workgroup
+// (B * heads of them: the max |out| as bf16 magnitude bits) for the out projection's
+// current-scaling cast (dpa_quantize_fp8_bf16_from_partials).
+extern "C" int dpa_attention_fwd_amax(const void* qkv, void* out, float* lse, int B, int L, int C,
+                                      int heads, void* amax_partials, void* stream) {
+  if (!amax_partials) return DPA_ERR_NULL;
+  if (!aligned(amax_partials, 4)) return DPA_ERR_ALIGN;
+  return attn_fwd(qkv, out, lse, B, L, C, heads, (uint32_t*)amax_partials, stream);
+}
+
+static int attn_bwd(const void* qkv, const void* out, const void* dout, const float* lse,
+                    void* dqkv, int B, int L, int C, int heads, uint32_t* amax_part,
+                    void* stream) {
   int st = attn_check(qkv, out, dqkv, B, L, C, heads);
   if (st != DPA_OK) return st;
   if (!dout || !lse) return DPA_ERR_NULL;
@@ -473,6 +519,7 @@ extern "C" int dpa_attention_bwd_bf16(const void* qkv, const void* out, const vo
   a.dout = (const uint16_t*)dout;
   a.out = (uint16_t*)dqkv;
   a.lse = (float*)lse;
+  a.amax_part = amax_part;
   a.L = L;
   a.C = C;
   a.heads = heads;
@@ -485,4 +532,21 @@ extern "C" int dpa_attention_bwd_bf16(const void* qkv, const void* out, const vo
     default: attn_bwd_kernel<256><<<grid, 512, 0, s>>>(a); break;
   }
   return launch_status();
+}
+
+extern "C" int dpa_attention_bwd_bf16(const void* qkv, const void* out, const void* dout,
+                                      const float* lse, void* dqkv, int B, int L, int C,
+                                      int heads, void* stream) {
+  return attn_bwd(qkv, out, dout, lse, dqkv, B, L, C, heads, nullptr, stream);
+}
+
+// dpa_attention_bwd_bf16 that also leaves one amax partial per (image, head) workgroup
+// (B * heads: the max |dqkv| over the dq, dk, dv it wrote) for the qkv projection's
+// current-scaling cast of its output gradient.
+extern "C" int dpa_attention_bwd_amax(const void* qkv, const void* out, const void* dout,
+                                      const float* lse, void* dqkv, int B, int L, int C,
+                                      int heads, void* amax_partials, void* stream) {
+  if (!amax_partials) return DPA_ERR_NULL;
+  if (!aligned(amax_partials, 4)) return DPA_ERR_ALIGN;
+  return attn_bwd(qkv, out, dout, lse, dqkv, B, L, C, heads, (uint32_t*)amax_partials, stream);
 }

@@ -40,6 +40,7 @@ struct LnArgs {
   float* mean;
   float* rstd;
   float* part;  // bwd: [blocks][2][C]
+  uint32_t* amax_part;  // fwd, optional: per-workgroup max of |y| (bf16 magnitude bits)
   int64_t rows;
   int C;
   float eps;
@@ -88,15 +89,21 @@ __device__ __forceinline__ void ln_unpack(const LnRaw<V>& r, float (&f)[V]) {
   }
 }
 
+// Returns the packed magnitudes of what it wrote folded into am (u16 max per half).
 template <int V>
-__device__ __forceinline__ void ln_store(uint16_t* row, int lane, const float (&f)[V]) {
+__device__ __forceinline__ void ln_store(uint16_t* row, int lane, const float (&f)[V], us2& am) {
   uint16_t* p = row + lane * V;
   if constexpr (V % 2 == 0) {
 #pragma unroll
-    for (int k = 0; k < V; k += 2)
-      *reinterpret_cast<uint32_t*>(p + k) = pack_bf16x2(f[k], f[k + 1]);
+    for (int k = 0; k < V; k += 2) {
+      const uint32_t w = pack_bf16x2(f[k], f[k + 1]);
+      *reinterpret_cast<uint32_t*>(p + k) = w;
+      am = __builtin_elementwise_max(am, __builtin_bit_cast(us2, w & 0x7fff7fffu));
+    }
   } else {
-    p[0] = (uint16_t)f32_to_bf16_bits(f[0]);
+    const uint32_t b = f32_to_bf16_bits(f[0]);
+    p[0] = (uint16_t)b;
+    am = __builtin_elementwise_max(am, us2{(unsigned short)(b & 0x7fffu), 0});
   }
 }
 
@@ -145,6 +152,10 @@ __device__ __forceinline__ void ln_store(float* row, int lane, const float (&f)[
     for (int k = 0; k < V; ++k) p[k] = f[k];
   }
 }
+template <int V>
+__device__ __forceinline__ void ln_store(float* row, int lane, const float (&f)[V], us2&) {
+  ln_store<V>(row, lane, f);
+}
 
 template <bool kF32>
 using LnXT = typename std::conditional<kF32, float, uint16_t>::type;
@@ -171,6 +182,7 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const LnArgs p) {
     b[k] = p.beta[lane * V + k];
   }
   const float inv_c = 1.0f / (float)p.C;
+  us2 am = {0, 0};
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i;
@@ -190,11 +202,24 @@ __global__ __launch_bounds__(kLnThreads) void ln_fwd_kernel(const LnArgs p) {
 #pragma unroll
     for (int k = 0; k < V; ++k) f[k] = (f[k] - mu) * rs * g[k] + b[k];
     if (r < p.rows) {
-      ln_store<V>(static_cast<uint16_t*>(p.out) + r * p.C, lane, f);
+      ln_store<V>(static_cast<uint16_t*>(p.out) + r * p.C, lane, f, am);
       if (lane == 0) {
         p.mean[r] = mu;
         p.rstd[r] = rs;
       }
+    }
+  }
+  if (p.amax_part) {  // the workgroup's max |y| for the consumer's current-scaling cast
+    __shared__ uint32_t red[kLnWaves];
+    uint32_t m = am.x > am.y ? am.x : am.y;
+    m = wave_max_u32(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t b = red[0];
+#pragma unroll
+      for (int w = 1; w < kLnWaves; ++w) b = b > red[w] ? b : red[w];
+      p.amax_part[blockIdx.x] = b;
     }
   }
 }
@@ -251,7 +276,10 @@ __global__ __launch_bounds__(kLnThreads) void ln_bwd_kernel(const LnArgs p) {
     const float m1 = wave_sum_f32(s1) * inv_c, m2 = wave_sum_f32(s2) * inv_c;
 #pragma unroll
     for (int k = 0; k < V; ++k) f[k] = rs * (d[k] - m1 - f[k] * m2);
-    if (live) ln_store<V>(static_cast<XT*>(p.out) + r * p.C, lane, f);
+    if (live) {
+      us2 unused = {0, 0};
+      ln_store<V>(static_cast<XT*>(p.out) + r * p.C, lane, f, unused);
+    }
   }
   // this block's column sums: the waves in order
 #pragma unroll
@@ -357,7 +385,8 @@ struct LnBwdLaunch {
 using namespace dpa;
 
 static int ln_fwd(const void* x, bool f32, const float* gamma, const float* beta, void* out,
-                  float* mean, float* rstd, int64_t rows, int C, float eps, void* stream) {
+                  float* mean, float* rstd, int64_t rows, int C, float eps, void* stream,
+                  uint32_t* amax_part = nullptr) {
   if (!x || !gamma || !beta || !out || !mean || !rstd) return DPA_ERR_NULL;
   if (!ln_shape_ok(rows, C)) return DPA_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(out, 16)) return DPA_ERR_ALIGN;
@@ -371,6 +400,7 @@ static int ln_fwd(const void* x, bool f32, const float* gamma, const float* beta
   a.rows = rows;
   a.C = C;
   a.eps = eps;
+  a.amax_part = amax_part;
   return ln_dispatch<LnFwdLaunch>(C, (hipStream_t)stream, a, ln_blocks(rows, C), f32);
 }
 
@@ -385,6 +415,25 @@ extern "C" int dpa_layernorm_fwd_ex(const void* x, int x_dtype, const float* gam
                                     int64_t rows, int C, float eps, void* stream) {
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   return ln_fwd(x, x_dtype == DPA_DTYPE_F32, gamma, beta, out, mean, rstd, rows, C, eps, stream);
+}
+
+// The forward's workgroups, one amax partial each (0 for an unsupported shape).
+extern "C" int dpa_layernorm_fwd_partials(int64_t rows, int C) {
+  return ln_shape_ok(rows, C) ? ln_blocks(rows, C) : 0;
+}
+
+// dpa_layernorm_fwd_ex that also leaves the per-workgroup maxima of |out| (bf16 magnitude
+// bits, dpa_layernorm_fwd_partials(rows, C) of them) in amax_partials, for the consumer's
+// current-scaling cast (dpa_quantize_fp8_bf16_from_partials) in place of its amax pass.
+extern "C" int dpa_layernorm_fwd_amax(const void* x, int x_dtype, const float* gamma,
+                                      const float* beta, void* out, float* mean, float* rstd,
+                                      int64_t rows, int C, float eps, void* amax_partials,
+                                      void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (!amax_partials) return DPA_ERR_NULL;
+  if (!aligned(amax_partials, 4)) return DPA_ERR_ALIGN;
+  return ln_fwd(x, x_dtype == DPA_DTYPE_F32, gamma, beta, out, mean, rstd, rows, C, eps, stream,
+                (uint32_t*)amax_partials);
 }
 
 extern "C" int64_t dpa_layernorm_bwd_workspace_bytes(int64_t rows, int C) {

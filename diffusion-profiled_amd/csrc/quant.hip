@@ -339,6 +339,29 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
   return launch_status();
 }
 
+// Current scaling whose amax pass ran inside the producer: partials[0..np) are the per-
+// workgroup maxima of |x| (bf16 magnitude bits) that the kernel writing x left, so only the
+// cast runs here (the same kernel, scale and bytes as dpa_quantize_fp8_bf16).
+extern "C" int dpa_quantize_fp8_bf16_from_partials(const void* x, int64_t n, const void* partials,
+                                                   int np, void* q, float* scale_out,
+                                                   void* stream) {
+  if (!x || !q || !scale_out || !partials) return DPA_ERR_NULL;
+  if (n <= 0 || np <= 0 || np > (1 << 20)) return DPA_ERR_SIZE;
+  if (!aligned(scale_out, 4) || !aligned(x, 2) || !aligned(partials, 4)) return DPA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = aligned(x, 16) && aligned(q, 8);
+  const int gc = vec ? grid_for(n, kCastBlocks) : 1;
+  if (vec)
+    cast_current_kernel<true><<<gc, kQThreads, 0, s>>>((const uint16_t*)x, n,
+                                                       (const uint32_t*)partials, np,
+                                                       (uint8_t*)q, scale_out);
+  else
+    cast_current_kernel<false><<<gc, kQThreads, 0, s>>>((const uint16_t*)x, n,
+                                                        (const uint32_t*)partials, np,
+                                                        (uint8_t*)q, scale_out);
+  return launch_status();
+}
+
 // ---------------------------------------------------------------------------------------
 // Allocation-free current scaling. The amax partials (one u32 per amax workgroup, at most
 // kMaxPartials) live in a file-scope device array, `scratch`, instead of a caller workspace:

@@ -167,6 +167,39 @@ def quantize_fp8_delayed_window(tensor: torch.Tensor, prev_scale: torch.Tensor,
     return quantized, scale
 
 
+# Producer-side amax for current scaling: a kernel that writes a bf16 tensor the FP8 GEMM
+# quantizes next (the attention LayerNorm, the self-attention forward and backward) can leave
+# its per-workgroup maxima of |t| beside it; the GEMM then runs only the cast
+# (dpa_quantize_fp8_bf16_from_partials) instead of the amax pass and the cast
+# (diffusion/fp8_kernels.py:559-601). Same bytes and scale: the maxima are of the very bf16
+# values written. False sends every site through quantize_fp8_tensor.
+PRODUCER_AMAX = True
+
+
+def mark_amax_partials(t: torch.Tensor, partials: torch.Tensor, count: int) -> torch.Tensor:
+    """Record on t (bf16, contiguous, just written) the int32 buffer holding ``count``
+    per-workgroup maxima of |t| (bf16 magnitude bits) that its producer left."""
+    t._dpa_amax = (partials, int(count), t.data_ptr(), t._version, t.numel())
+    return t
+
+
+def quantize_fp8_from_producer(x2: torch.Tensor, src: torch.Tensor):
+    """``quantize_fp8_tensor(x2)`` from the maxima recorded on ``src`` when x2 is src's data
+    unchanged (same address, element count and version), else None."""
+    rec = getattr(src, "_dpa_amax", None)
+    if rec is None or not PRODUCER_AMAX:
+        return None
+    partials, count, ptr, version, numel = rec
+    if (x2.dtype != torch.bfloat16 or not x2.is_contiguous() or x2.data_ptr() != ptr
+            or x2._version != version or x2.numel() != numel):
+        return None
+    q = torch.empty_like(x2, dtype=FP8_DTYPE)
+    scale = torch.empty((), device=x2.device, dtype=torch.float32)
+    _lib.call("dpa_quantize_fp8_bf16_from_partials", x2.data_ptr(), x2.numel(),
+              partials.data_ptr(), count, q.data_ptr(), scale.data_ptr(), _stream(x2))
+    return q, scale
+
+
 def quantize_fp8_delayed_deferred(tensor: torch.Tensor, prev_scale: torch.Tensor,
                                   partials: torch.Tensor, count: torch.Tensor) -> torch.Tensor:
     """``quantize_fp8_delayed``'s cast (scale ``prev_scale``) leaving the block maxima of this
@@ -1019,7 +1052,7 @@ class LinearFP8Prepared(torch.autograd.Function):
             xq, xs = hit[1], hit[2]
         else:
             x2 = x.to(torch.bfloat16).reshape(-1, k).contiguous()
-            xq, xs = quantize_fp8_tensor(x2)
+            xq, xs = quantize_fp8_from_producer(x2, x) or quantize_fp8_tensor(x2)
             if key is not None:
                 x_cache[key] = (x, xq, xs)      # x kept alive: its address is not reused
         b32 = None if bias is None else bias.detach().float().contiguous()
@@ -1035,7 +1068,7 @@ class LinearFP8Prepared(torch.autograd.Function):
         xq, wq, wq_t, xs, wsc = ctx.saved_tensors
         n, k = wq.shape
         dy2 = dy.to(torch.bfloat16).reshape(-1, n).contiguous()
-        dyq, dys = quantize_fp8_tensor(dy2)
+        dyq, dys = quantize_fp8_from_producer(dy2, dy) or quantize_fp8_tensor(dy2)
         dx = dw = db = None
         if ctx.needs_input_grad[0]:
             dx = _linear_dgrad_wt(dyq, wq, wq_t, dys, wsc).reshape(*ctx.lead, k)

@@ -14,6 +14,7 @@ from typing import Any
 import torch
 
 from . import _lib
+from . import fp8_kernels as _fp8
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -41,9 +42,18 @@ class LayerNormBF16(torch.autograd.Function):
         rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
         g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
         dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
-        _lib.call("dpa_layernorm_fwd_ex", xb.data_ptr(), dt, g32.data_ptr(), b32.data_ptr(),
-                  out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, c, float(eps),
-                  _stream(xb))
+        if _fp8.PRODUCER_AMAX:
+            # the per-workgroup maxima of |out| for the qkv projection's e4m3 cast
+            npart = _lib.query("dpa_layernorm_fwd_partials", rows, c)
+            part = torch.empty(npart, device=x.device, dtype=torch.int32)
+            _lib.call("dpa_layernorm_fwd_amax", xb.data_ptr(), dt, g32.data_ptr(),
+                      b32.data_ptr(), out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, c,
+                      float(eps), part.data_ptr(), _stream(xb))
+            _fp8.mark_amax_partials(out, part, npart)
+        else:
+            _lib.call("dpa_layernorm_fwd_ex", xb.data_ptr(), dt, g32.data_ptr(), b32.data_ptr(),
+                      out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, c, float(eps),
+                      _stream(xb))
         ctx.save_for_backward(xb, g32, mean, rstd)
         ctx.x_dtype = x.dtype
         ctx.param_dtypes = (gamma.dtype, beta.dtype)

@@ -70,6 +70,15 @@ int64_t dpa_quant_workspace_bytes(int64_t n);
 int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* scale_out,
                           void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Current scaling whose amax pass ran in the kernel that wrote x: partials[0..np) are that
+ * kernel's per-workgroup maxima of |x| as bf16 magnitude bits (|x| & 0x7fff; the LayerNorm
+ * and attention *_amax entries below leave them). One launch, the cast of
+ * dpa_quantize_fp8_bf16 (quantize_fp8_kernel, diffusion/fp8_kernels.py:105-120, with the
+ * finalize :90-102 over the partials): the same q and scale_out when the partials cover x.
+ * 1 <= np <= 2^20. */
+int dpa_quantize_fp8_bf16_from_partials(const void* x, int64_t n, const void* partials, int np,
+                                        void* q, float* scale_out, void* stream);
+
 /* Current scaling with no workspace argument and no allocation: the same launches, bytes and
  * scale as dpa_quantize_fp8_bf16, with the amax partials in a fixed 4 KB device array of the
  * library (dpa_quantize_fp8_bf16_noalloc_scratch_bytes(); one copy per GPU, held until the
@@ -485,6 +494,15 @@ int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout, const flo
                          float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
                          int C, void* stream);
 
+/* The forward also writing the per-workgroup maxima of |y| (bf16 magnitude bits) to
+ * amax_partials (dpa_layernorm_fwd_partials(rows, C) entries; 0 for an unsupported shape),
+ * for the qkv projection's current-scaling cast (dpa_quantize_fp8_bf16_from_partials) in
+ * place of its amax pass (partial_amax_kernel, diffusion/fp8_kernels.py:54-64). */
+int dpa_layernorm_fwd_partials(int64_t rows, int C);
+int dpa_layernorm_fwd_amax(const void* x, int x_dtype, const float* gamma, const float* beta,
+                           void* out, float* mean, float* rstd, int64_t rows, int C, float eps,
+                           void* amax_partials, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Self-attention of the attention block, softmax(q k^T / sqrt(64)) v per (image, head), bf16
  * in and out, fp32 softmax: replaces F.scaled_dot_product_attention with its head rearranges
@@ -502,6 +520,17 @@ int dpa_attention_fwd_bf16(const void* qkv, void* out, float* lse, int B, int L,
 int dpa_attention_bwd_bf16(const void* qkv, const void* out, const void* dout,
                            const float* lse, void* dqkv, int B, int L, int C, int heads,
                            void* stream);
+
+/* The same with one amax partial per (image, head) workgroup, B * heads of them, in
+ * amax_partials: the max |out| (forward) or |dqkv| (backward) as bf16 magnitude bits, for the
+ * current-scaling cast of the out projection's input and of the qkv projection's output
+ * gradient (dpa_quantize_fp8_bf16_from_partials) in place of their amax passes
+ * (partial_amax_kernel, diffusion/fp8_kernels.py:54-64). */
+int dpa_attention_fwd_amax(const void* qkv, void* out, float* lse, int B, int L, int C,
+                           int heads, void* amax_partials, void* stream);
+int dpa_attention_bwd_amax(const void* qkv, const void* out, const void* dout,
+                           const float* lse, void* dqkv, int B, int L, int C, int heads,
+                           void* amax_partials, void* stream);
 
 /* Residual join y = (a + b) / sqrt(2) of bf16 tensors in one pass (diffusion/unet.py:161 and
  * :203, under autocast), with torch's roundings: bf16(bf16(a + b) * inv), inv = RN32(1/sqrt 2)
