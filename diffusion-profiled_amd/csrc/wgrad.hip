@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
   }
 
   // partial[split][co][tap*Cin + ci]: consumers stage [co][ci] fp32 in LDS, then all eight
-  // waves store contiguous 512-B rows
+  // waves store contiguous 512-B rows (nontemporal: read once, by the reduce)
   if (wave < 4) {
     const int frow = lane & 15, fq = lane >> 4;
 #pragma unroll
@@ -279,8 +279,8 @@ __global__ __launch_bounds__(kWgThreads, 1) void wgrad_partial_kernel(const Wgra
 #pragma unroll 4
   for (int r0 = 0; r0 < kWgTile; r0 += kRowsPerPass) {
     const int co = r0 + threadIdx.x / kChunks;
-    *reinterpret_cast<v4f*>(base + (int64_t)(co0 + co) * kk + ch * 4) =
-        *reinterpret_cast<const v4f*>(wg_smem + co * kWgPPitch + ch * 16);
+    __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(wg_smem + co * kWgPPitch + ch * 16),
+                                reinterpret_cast<v4f*>(base + (int64_t)(co0 + co) * kk + ch * 4));
   }
 }
 
