@@ -107,15 +107,15 @@ class ConvWorkload:
 
     def quantize(self):
         """x and dy: quantize_fp8 (amax + cast each). The weight: its e4m3 copy, scale and the
-        data gradient's transposed copy in one grouped weight preparation (two launches, in
-        place of quantize_fp8's two and the transpose); for the halo-patch kernel's shapes both
-        copies are written in its fragment layouts."""
+        data gradient's transposed copy in a grouped weight preparation whose blocks run inside
+        x's amax and cast launches (two launches for x and the weight, in place of
+        quantize_fp8's two per tensor and the transpose); for the halo-patch kernel's shapes
+        both copies are written in its fragment layouts."""
         K = self.K
         if self.wprep is None:
             WP = importlib.import_module("diffusion-profiled_amd.weight_prep")
             self.wprep = WP.TensorPrep([self.wt], frag=[self.frag])
-        self.xq, self.xs = K.quantize_fp8(self.x)
-        self.wprep.run()
+        self.xq, self.xs = self.wprep.run_with_quantize(self.x)
         self.wq, self.wq_t, self.ws = self.wprep.q[0], self.wprep.qt[0], self.wprep.scale(0)
         self.dyq, self.dys = K.quantize_fp8(self.dy)
 

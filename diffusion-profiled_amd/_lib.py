@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_weight_prep_plan": (c_int, [c_void_p, c_int]),
     "dpa_weight_prep_workspace_bytes": (c_int64, [c_int]),
     "dpa_weight_prep_run": (c_int, [c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),
+    "dpa_quantize_fp8_bf16_with_weight_prep": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p]),
     "dpa_window_max_grouped_f32": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p]),
     "dpa_conv2d_wgrad_fp8_f32": (
         c_int,

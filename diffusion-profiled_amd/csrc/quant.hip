@@ -15,6 +15,7 @@
 // passes keep kUnroll 16-B loads in flight per thread over a grid of a few blocks per CU; the
 // e4m3 output goes out with nontemporal stores (measured ~2 us faster per 16.8M elements).
 #include "dpa_common.hpp"
+#include "wprep_body.hpp"
 
 #include <atomic>
 #include <mutex>
@@ -50,12 +51,14 @@ __device__ __forceinline__ uint32_t reduce_partials(const uint32_t* partials, in
 }
 
 // Vector loop shared by the passes: every 8-element group v < n / 8 is visited once, kUnroll
-// groups (grid-strided) per thread and iteration with all their loads issued first; body(v,
-// data) gets the group index and its 16 bytes of bf16.
+// groups (strided over the nb blocks of the pass, this one being block bid) per thread and
+// iteration with all their loads issued first; body(v, data) gets the group index and its
+// 16 bytes of bf16.
 template <typename Body>
-__device__ __forceinline__ void for_groups(const uint16_t* __restrict__ x, int64_t nv, Body body) {
-  const int64_t gs = (int64_t)gridDim.x * kQThreads;
-  int64_t v = (int64_t)blockIdx.x * kQThreads + threadIdx.x;
+__device__ __forceinline__ void for_groups(const uint16_t* __restrict__ x, int64_t nv, int bid,
+                                           int nb, Body body) {
+  const int64_t gs = (int64_t)nb * kQThreads;
+  int64_t v = (int64_t)bid * kQThreads + threadIdx.x;
   for (; v + (kUnroll - 1) * gs < nv; v += kUnroll * gs) {
     uint4 d[kUnroll];
 #pragma unroll
@@ -66,21 +69,21 @@ __device__ __forceinline__ void for_groups(const uint16_t* __restrict__ x, int64
   for (; v < nv; v += gs) body(v, *reinterpret_cast<const uint4*>(x + 8 * v));
 }
 
-// Pass 1 (current scaling): per-block amax of |x| as bf16 bits.
+// Pass 1 (current scaling): per-block amax of |x| as bf16 bits; block bid of nb.
 template <bool kVec>
-__global__ __launch_bounds__(kQThreads) void amax_partials_kernel(const uint16_t* __restrict__ x,
-                                                                  int64_t n,
-                                                                  uint32_t* __restrict__ partials) {
+__device__ __forceinline__ void amax_partials_block(const uint16_t* __restrict__ x, int64_t n,
+                                                    uint32_t* __restrict__ partials, int bid,
+                                                    int nb) {
   __shared__ uint32_t red[kQThreads / 64];
   us2 acc = {0, 0};
   uint32_t accs = 0;
   int64_t tail = 0;
   if (kVec) {
     const int64_t nv = n >> 3;
-    for_groups(x, nv, [&](int64_t, uint4 d) { acc = absmax8(acc, d); });
+    for_groups(x, nv, bid, nb, [&](int64_t, uint4 d) { acc = absmax8(acc, d); });
     tail = nv << 3;
   }
-  if (blockIdx.x == 0) {  // ragged tail (or everything when x is not 16-B aligned)
+  if (bid == 0) {  // ragged tail (or everything when x is not 16-B aligned)
     for (int64_t j = tail + threadIdx.x; j < n; j += kQThreads) {
       const uint32_t a = x[j] & 0x7fffu;
       accs = accs > a ? accs : a;
@@ -89,7 +92,14 @@ __global__ __launch_bounds__(kQThreads) void amax_partials_kernel(const uint16_t
   uint32_t m = acc.x > acc.y ? acc.x : acc.y;
   m = m > accs ? m : accs;
   m = block_max_u32(m, red);
-  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+  if (threadIdx.x == 0) partials[bid] = m;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kQThreads) void amax_partials_kernel(const uint16_t* __restrict__ x,
+                                                                  int64_t n,
+                                                                  uint32_t* __restrict__ partials) {
+  amax_partials_block<kVec>(x, n, partials, blockIdx.x, gridDim.x);
 }
 
 __device__ __forceinline__ void cast_tail(const uint16_t* __restrict__ x, int64_t from, int64_t n,
@@ -100,30 +110,59 @@ __device__ __forceinline__ void cast_tail(const uint16_t* __restrict__ x, int64_
   }
 }
 
-// Pass 2 (current scaling): scale from the partials, then q = e4m3(clamp(x / scale)).
+// Pass 2 (current scaling): scale from the partials, then q = e4m3(clamp(x / scale));
+// block bid of nb.
 template <bool kVec>
-__global__ __launch_bounds__(kQThreads) void cast_current_kernel(
-    const uint16_t* __restrict__ x, int64_t n, const uint32_t* __restrict__ partials, int np,
-    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+__device__ __forceinline__ void cast_current_block(const uint16_t* __restrict__ x, int64_t n,
+                                                   const uint32_t* __restrict__ partials, int np,
+                                                   uint8_t* __restrict__ q,
+                                                   float* __restrict__ scale_out, int bid, int nb) {
   __shared__ uint32_t red[kQThreads / 64];
   const uint32_t amax_bits = reduce_partials(partials, np, red);
   const float scale = scale_from_amax_bits(amax_bits);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  if (bid == 0 && threadIdx.x == 0) *scale_out = scale;
   int64_t tail = 0;
   if (kVec) {
     const int64_t nv = n >> 3;
     const float r = quant_recip(scale);
     if (r != 0.0f)
-      for_groups(x, nv, [&](int64_t v, uint4 d) {
+      for_groups(x, nv, bid, nb, [&](int64_t v, uint4 d) {
         st_nt8(q + 8 * v, quant8_rcp(d, scale, r));
       });
     else
-      for_groups(x, nv, [&](int64_t v, uint4 d) {
+      for_groups(x, nv, bid, nb, [&](int64_t v, uint4 d) {
         st_nt8(q + 8 * v, quant8(d, scale));
       });
     tail = nv << 3;
   }
-  if (blockIdx.x == 0) cast_tail(x, tail, n, scale, q);
+  if (bid == 0) cast_tail(x, tail, n, scale, q);
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kQThreads) void cast_current_kernel(
+    const uint16_t* __restrict__ x, int64_t n, const uint32_t* __restrict__ partials, int np,
+    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+  cast_current_block<kVec>(x, n, partials, np, q, scale_out, blockIdx.x, gridDim.x);
+}
+
+// Current scaling of x and a grouped weight preparation (wprep_body.hpp) in the same two
+// launches: blocks [0, wb) are the preparation's, the rest x's pass of nb blocks. The passes
+// touch disjoint memory, so each block's work is that of its own launch.
+static_assert(kWpThreads == kQThreads, "the combined launches share one block size");
+
+__global__ __launch_bounds__(kQThreads) void amax_with_wprep_kernel(
+    const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ partials, int nb,
+    const DpaWeightEntry* __restrict__ e, int count, uint32_t* __restrict__ wpart, int wb) {
+  if ((int)blockIdx.x < wb) wprep_amax_block(e, count, wpart, blockIdx.x);
+  else amax_partials_block<true>(x, n, partials, blockIdx.x - wb, nb);
+}
+
+__global__ __launch_bounds__(kQThreads) void cast_with_wprep_kernel(
+    const uint16_t* __restrict__ x, int64_t n, const uint32_t* __restrict__ partials, int np,
+    uint8_t* __restrict__ q, float* __restrict__ scale_out, int nb,
+    const DpaWeightEntry* __restrict__ e, int count, const uint32_t* __restrict__ wpart, int wb) {
+  if ((int)blockIdx.x < wb) wprep_cast_block(e, count, wpart, blockIdx.x);
+  else cast_current_block<true>(x, n, partials, np, q, scale_out, blockIdx.x - wb, nb);
 }
 
 // Delayed scaling, one pass: q = cast(x, *prev_scale) and per-block amax of x. count (if
@@ -141,12 +180,12 @@ __global__ __launch_bounds__(kQThreads) void cast_delayed_kernel(
     const int64_t nv = n >> 3;
     const float r = quant_recip(scale);
     if (r != 0.0f)
-      for_groups(x, nv, [&](int64_t v, uint4 d) {
+      for_groups(x, nv, blockIdx.x, gridDim.x, [&](int64_t v, uint4 d) {
         acc = absmax8(acc, d);
         st_nt8(q + 8 * v, quant8_rcp(d, scale, r));
       });
     else
-      for_groups(x, nv, [&](int64_t v, uint4 d) {
+      for_groups(x, nv, blockIdx.x, gridDim.x, [&](int64_t v, uint4 d) {
         acc = absmax8(acc, d);
         st_nt8(q + 8 * v, quant8(d, scale));
       });
@@ -336,6 +375,44 @@ extern "C" int dpa_quantize_fp8_bf16(const void* x, int64_t n, void* q, float* s
     cast_current_kernel<false><<<gc, kQThreads, 0, s>>>(xp, n, part, np, (uint8_t*)q,
                                                         scale_out);
   }
+  return launch_status();
+}
+
+// Current scaling of x (dpa_quantize_fp8_bf16) and a planned weight preparation
+// (dpa_weight_prep_run) in two launches instead of four: the preparation's blocks run as the
+// first blocks of x's amax launch and of x's cast launch. Same bytes and scales as the two
+// calls; x below the one-workgroup size or unaligned takes exactly those two calls.
+extern "C" int dpa_quantize_fp8_bf16_with_weight_prep(
+    const void* x, int64_t n, void* q, float* scale_out, void* workspace, int64_t workspace_bytes,
+    const DpaWeightEntry* entries_dev, int count, int total_blocks, void* wp_workspace,
+    int64_t wp_workspace_bytes, void* stream) {
+  if (!x || !q || !scale_out || !entries_dev) return DPA_ERR_NULL;
+  if (n <= 0 || count <= 0 || total_blocks <= 0 || total_blocks > 0x7fffffff - 2 * kCastBlocks)
+    return DPA_ERR_SIZE;
+  if (!workspace || workspace_bytes < dpa_quant_workspace_bytes(n)) return DPA_ERR_WORKSPACE;
+  if (!wp_workspace || wp_workspace_bytes < dpa_weight_prep_workspace_bytes(total_blocks))
+    return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 4) || !aligned(scale_out, 4) || !aligned(x, 2) ||
+      !aligned(wp_workspace, 4) || !aligned(entries_dev, 8))
+    return DPA_ERR_ALIGN;
+  const bool vec = aligned(x, 16) && aligned(q, 8);
+  if (!vec || n <= kSmallMaxN) {
+    const int st = dpa_quantize_fp8_bf16(x, n, q, scale_out, workspace, workspace_bytes, stream);
+    if (st != DPA_OK) return st;
+    return dpa_weight_prep_run(entries_dev, count, total_blocks, wp_workspace, wp_workspace_bytes,
+                               stream);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const int np = grid_for(n, kAmaxBlocks), gc = grid_for(n, kCastBlocks);
+  auto* xp = (const uint16_t*)x;
+  auto* part = (uint32_t*)workspace;
+  auto* wpart = (uint32_t*)wp_workspace;
+  amax_with_wprep_kernel<<<(unsigned)(total_blocks + np), kQThreads, 0, s>>>(
+      xp, n, part, np, entries_dev, count, wpart, total_blocks);
+  const int st = launch_status();
+  if (st != DPA_OK) return st;
+  cast_with_wprep_kernel<<<(unsigned)(total_blocks + gc), kQThreads, 0, s>>>(
+      xp, n, part, np, (uint8_t*)q, scale_out, gc, entries_dev, count, wpart, total_blocks);
   return launch_status();
 }
 

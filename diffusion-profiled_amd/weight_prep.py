@@ -249,3 +249,22 @@ class TensorPrep:
         stream = torch.cuda.current_stream(self.table.device).cuda_stream
         _lib.call("dpa_weight_prep_run", self.table.data_ptr(), self.count, self.blocks,
                   self.workspace.data_ptr(), self.ws_bytes, stream)
+
+    def run_with_quantize(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """run() and ``quantize_fp8(x)`` (current scaling, bf16 x) in the same two launches
+        (dpa_quantize_fp8_bf16_with_weight_prep); returns x's (e4m3, scale) as quantize_fp8
+        does, the weights' copies land in q / qt / scales as after run()."""
+        assert x.dtype == torch.bfloat16 and x.device == self.table.device
+        if not (x.is_contiguous() or (x.ndim == 4 and x.is_contiguous(
+                memory_format=torch.channels_last))):
+            x = x.contiguous()
+        n = x.numel()
+        q = torch.empty_like(x, dtype=FP8_DTYPE, memory_format=torch.preserve_format)
+        scale = torch.empty((), device=x.device, dtype=torch.float32)
+        ws_bytes = _lib.query("dpa_quant_workspace_bytes", n)
+        ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.call("dpa_quantize_fp8_bf16_with_weight_prep", x.data_ptr(), n, q.data_ptr(),
+                  scale.data_ptr(), ws.data_ptr(), ws_bytes, self.table.data_ptr(), self.count,
+                  self.blocks, self.workspace.data_ptr(), self.ws_bytes, stream)
+        return q, scale

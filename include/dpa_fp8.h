@@ -396,6 +396,16 @@ int64_t dpa_weight_prep_workspace_bytes(int total_blocks);
  * that call on the same stream. */
 int dpa_weight_prep_run(const DpaWeightEntry* entries_dev, int count, int total_blocks,
                         void* workspace, int64_t workspace_bytes, void* stream);
+/* dpa_quantize_fp8_bf16(x, ...) and dpa_weight_prep_run(entries_dev, ...) in two launches
+ * instead of four: the preparation's blocks run inside x's amax and cast launches, with the
+ * same results as the two calls. For a caller that quantizes an activation and prepares a
+ * weight for the same GEMM, as the reference's conv2d_fwd_fp8 (diffusion/fp8_kernels.py:
+ * 642-650) quantizes x and the weight one after the other (quantize_fp8 :559-601 twice). */
+int dpa_quantize_fp8_bf16_with_weight_prep(const void* x, int64_t n, void* q, float* scale_out,
+                                           void* workspace, int64_t workspace_bytes,
+                                           const DpaWeightEntry* entries_dev, int count,
+                                           int total_blocks, void* wp_workspace,
+                                           int64_t wp_workspace_bytes, void* stream);
 /* hist[i] = max over window i of len floats (torch.max; NaN if the window holds one);
  * windows_dev: device array of count window pointers. One launch for every window. */
 int dpa_window_max_grouped_f32(const float* const* windows_dev, int count, int64_t len,

@@ -57,8 +57,11 @@ def test_precondition_errors_return_before_launch(lib):
     # NULL inputs
     assert lib.dpa_quantize_fp8_bf16(nul, 16, fake, fake, fake, 4096, nul) == -1
     assert lib.dpa_conv2d_fwd_fp8(nul, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 3, 3, 1, 1, nul) == -1
+    assert lib.dpa_quantize_fp8_bf16_with_weight_prep(fake, 16, fake, fake, fake, 4096, nul, 1, 1, fake, 4, nul) == -1
     # bad sizes / shapes
     assert lib.dpa_quantize_fp8_bf16(fake, 0, fake, fake, fake, 4096, nul) == -2
+    assert lib.dpa_quantize_fp8_bf16_with_weight_prep(fake, 16, fake, fake, fake, 4096, fake, 0, 1, fake, 4, nul) == -2
+    assert lib.dpa_quantize_fp8_bf16_with_weight_prep(fake, 16, fake, fake, fake, 4096, fake, 1, 1, fake, 0, nul) == -5
     assert lib.dpa_conv2d_fwd_fp8(fake, fake, fake, fake, nul, fake, 1, 8, 8, 96, 128, 3, 3, 1, 1, nul) == -4
     assert lib.dpa_conv2d_fwd_fp8(fake, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 5, 5, 1, 2, nul) == -4
     assert lib.dpa_conv2d_fwd_fp8(fake, fake, fake, fake, nul, fake, 1, 8, 8, 128, 128, 1, 1, 2, 0, nul) == -4

@@ -211,3 +211,42 @@ def test_tensor_prep_fragment_layouts_equal_quantize_and_frag(dtype):
             assert torch.equal(tp.qt[i], wt), i
         else:
             assert torch.equal(tp.q[i].view(torch.uint8), q_ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("case", ["cfg2", "ragged", "small", "unaligned"])
+def test_quantize_with_weight_prep_equals_the_two_calls(case):
+    """dpa_quantize_fp8_bf16_with_weight_prep (TensorPrep.run_with_quantize): x's e4m3 bytes
+    and scale equal quantize_fp8(x), and the prepared weights (fragment layout, OHWI, 2-D, bf16
+    and fp32) equal run()'s, byte for byte. cfg2's x (the combined launches), a length with a
+    ragged tail of 5, and the fallbacks to the two calls (x of one workgroup, x not 16-B
+    aligned); two rounds, the second after the weights and x change in place."""
+    g = torch.Generator().manual_seed(13)
+    ws = [(torch.randn((128, 128, 3, 3), generator=g) * 0.05).to(torch.bfloat16),
+          (torch.randn((256, 128, 1, 1), generator=g) * 3.0),
+          (torch.randn((768, 256), generator=g)).to(torch.bfloat16)]
+    ws = [w.cuda().contiguous(memory_format=torch.channels_last) if w.ndim == 4 else w.cuda()
+          for w in ws]
+    frag = [True, False, False]
+    n = {"cfg2": 128 * 128 * 32 * 32, "ragged": 3 * 1000 * 1000 + 5, "small": 4000,
+         "unaligned": 1 << 20}[case]
+    base = randn_bf16((n + 1,), seed=17, std=2.0).cuda()
+    x = base[1:] if case == "unaligned" else base[:n]
+    if case == "cfg2":
+        x = x.view(128, 32, 32, 128).permute(0, 3, 1, 2)  # NCHW view, channels-last memory
+    fused, sep = WP.TensorPrep(ws, frag=frag), WP.TensorPrep(ws, frag=frag)
+    for rnd in range(2):
+        if rnd:
+            for w in ws:
+                w.mul_(1.25)
+            x.mul_(-3.0)
+        qx, sx = fused.run_with_quantize(x)
+        qr, sr = K.quantize_fp8_tensor(x)
+        sep.run()
+        torch.cuda.synchronize()
+        assert float(sx) == float(sr), (case, rnd)
+        assert qx.shape == qr.shape and qx.stride() == qr.stride(), (case, rnd)
+        assert torch.equal(qx.view(torch.uint8), qr.view(torch.uint8)), (case, rnd)
+        assert torch.equal(fused.scales, sep.scales), (case, rnd)
+        for i in range(len(ws)):
+            assert torch.equal(fused.q[i].view(torch.uint8), sep.q[i].view(torch.uint8)), (rnd, i)
+            assert torch.equal(fused.qt[i].view(torch.uint8), sep.qt[i].view(torch.uint8)), (rnd, i)
