@@ -25,7 +25,7 @@ namespace dpa {
 constexpr int kQThreads = 256;
 constexpr int kMaxPartials = 1024;
 constexpr int kUnroll = 8;          // uint4 loads in flight per thread
-constexpr int kAmaxBlocks = 512;    // amax pass grid cap (and partial count cap)
+constexpr int kAmaxBlocks = 256;    // amax pass grid cap (and partial count cap)
 constexpr int kCastBlocks = 1024;   // cast pass grid cap
 
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
