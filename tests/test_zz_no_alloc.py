@@ -64,7 +64,7 @@ def check(lib, x: torch.Tensor, what: str):
 
 
 def test_noalloc_matches_workspace_entry_two_calls(lib):
-    """cfg2 activation (512 amax partials), then a smaller tensor with a much larger
+    """cfg2 activation (256 amax partials), then a smaller tensor with a much larger
     magnitude in its last element (its own partials give a different scale), then the
     cfg2 weight: each call bit-identical to the workspace entry point."""
     big = randn_bf16((128, 128, 32, 32), seed=0).cuda().reshape(-1)
