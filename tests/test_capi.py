@@ -204,7 +204,7 @@ def test_deferred_window_entries(lib):
     assert ctypes.sizeof(WP.DpaDeferredWindow) == 64
     assert lib.dpa_quant_partials_count(0) == 0
     assert lib.dpa_quant_partials_count(8) == 1
-    assert lib.dpa_quant_partials_count(1 << 30) == 512
+    assert lib.dpa_quant_partials_count(1 << 30) == 256  # the amax pass's grid cap
     fake, nul = ctypes.c_void_p(0x1000), None
     assert lib.dpa_quantize_fp8_delayed_deferred_bf16(nul, 16, fake, fake, fake, 512, fake, nul) == -1
     assert lib.dpa_quantize_fp8_delayed_deferred_bf16(fake, 0, fake, fake, fake, 512, fake, nul) == -2
