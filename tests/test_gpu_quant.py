@@ -56,9 +56,23 @@ def test_cfg2_weight_and_cfg1_tensors(K):
     check_current(K, randn_bf16((128, 128, 32, 32), seed=2, std=1e-2))  # grad_out scale
 
 
-@pytest.mark.parametrize("n", [1, 7, 8, 15, 16, 17, 255, 4095, 4097, 8191, 8193, 65537, 1 << 20 | 3])
-def test_ragged_sizes(K, n):
-    check_current(K, randn_bf16((n,), seed=n))
+@pytest.mark.parametrize("n", [1, 7, 8, 15, 16, 17, 255, 4095, 4097, 8191, 8193, 16384, 16385,
+                               65537, 1 << 20 | 3])
+@pytest.mark.parametrize("peak", ["none", "first", "last"])
+def test_ragged_sizes(K, n, peak):
+    """n-element tensors on both sides of the single-workgroup limit (16384 elements) and of
+    the 8-element vector groups; the maximum |x| planted in the first or the last element
+    (the vector tail) must reach the scale."""
+    x = randn_bf16((n,), seed=n)
+    assert x.shape == (n,)
+    if peak == "first":
+        x[0] = -40.0
+    elif peak == "last":
+        x[-1] = 40.0
+    check_current(K, x)
+    if peak != "none":
+        q, s = K.quantize_fp8_tensor(x.cuda())
+        assert np.float32(s.item()) == np.float32(40.0) / np.float32(448.0)
 
 
 def test_unaligned_view(K):

@@ -195,4 +195,12 @@ def test_gn_silu_bwd_finite_differences():
         fp = fs.astype(np.float64).copy(); fp[0, j] += eps
         fm = fs.astype(np.float64).copy(); fm[0, j] -= eps
         assert abs((loss(fsv=fp) - loss(fsv=fm)) / (2 * eps) - dfs[0, j]) < 1e-6
+        bp = beta.astype(np.float64).copy(); bp[j] += eps
+        bm = beta.astype(np.float64).copy(); bm[j] -= eps
+        assert abs((loss(bv=bp) - loss(bv=bm)) / (2 * eps) - dbt[j]) < 1e-6
+        sp = fb.astype(np.float64).copy(); sp[0, j] += eps
+        sm = fb.astype(np.float64).copy(); sm[0, j] -= eps
+        assert abs((loss(fbv=sp) - loss(fbv=sm)) / (2 * eps) - dfb[0, j]) < 1e-6
     assert dbt.shape == (c,) and dfb.shape == (n, c)
+    # a planted mistake (the FiLM shift's gradient taken as the beta gradient) is caught
+    assert np.abs(dfb[0] - dbt).max() > 1e-3
