@@ -10,7 +10,19 @@ import ctypes
 import threading
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_void_p
 
+import torch
+
 from . import build as _build
+
+
+@torch.compiler.disable
+def current_stream(t: "torch.Tensor") -> int:
+    """The hipStream_t of torch's current stream on t's device, where every launch goes (so
+    launches order with torch's own kernels and graph capture records them). Dynamo never
+    traces it: under torch.compile a call here ends the graph and the ctypes launch that
+    follows runs eagerly. The FP8 ops call it inside torch.library custom-op bodies, which
+    Dynamo does not enter."""
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 c_float_p = POINTER(c_float)
 

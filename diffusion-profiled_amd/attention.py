@@ -22,7 +22,7 @@ HEAD_DIM = 64
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 def supported(seq_len: int, channels: int, heads: int) -> bool:

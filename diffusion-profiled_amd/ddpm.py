@@ -165,7 +165,7 @@ class MSELossHIP(torch.autograd.Function):
         ws = torch.empty(ws_bytes, device=p.device, dtype=torch.uint8)
         dt = 1 if p.dtype == torch.float32 else 0  # DPA_DTYPE_F32 / DPA_DTYPE_BF16
         _lib.call("dpa_mse_loss_f32", p.data_ptr(), dt, tg.data_ptr(), n, out.data_ptr(),
-                  ws.data_ptr(), ws_bytes, torch.cuda.current_stream(p.device).cuda_stream)
+                  ws.data_ptr(), ws_bytes, _lib.current_stream(p))
         ctx.save_for_backward(pred, target)
         return out
 

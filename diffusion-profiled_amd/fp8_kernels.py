@@ -47,7 +47,7 @@ DW_CONFIG_BY_SHAPE: dict[tuple[int, int, int, int], int | None] = {
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -281,7 +281,8 @@ def quantize_fp8_delayed(tensor: torch.Tensor, prev_scale: torch.Tensor) -> tupl
     assert tensor.dtype == torch.bfloat16 and tensor.is_cuda and tensor.ndim == 4, (
         f"{tensor.dtype} {tensor.is_cuda} {tensor.ndim}"
     )
-    return _quantize_impl(tensor, prev_scale)
+    torch_checks_scale(prev_scale, tensor.device)
+    return _ops.quantize_delayed(tensor, prev_scale)
 
 
 def quantize_fp8(tensor: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -289,13 +290,16 @@ def quantize_fp8(tensor: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     assert tensor.dtype == torch.bfloat16 and tensor.is_cuda and tensor.ndim == 4, (
         f"{tensor.dtype} {tensor.is_cuda} {tensor.ndim}"
     )
-    return _quantize_impl(tensor, None)
+    return _ops.quantize(tensor)
 
 
 def quantize_fp8_tensor(tensor: torch.Tensor, prev_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """``quantize_fp8`` / ``quantize_fp8_delayed`` for a bf16 tensor of any rank."""
     assert tensor.dtype == torch.bfloat16 and tensor.is_cuda, f"{tensor.dtype} {tensor.is_cuda}"
-    return _quantize_impl(tensor, prev_scale)
+    if prev_scale is None:
+        return _ops.quantize(tensor)
+    torch_checks_scale(prev_scale, tensor.device)
+    return _ops.quantize_delayed(tensor, prev_scale)
 
 
 # --------------------------------------------------------------------------------------
@@ -520,7 +524,9 @@ def conv2d_fwd_fp8_prequantized(
 ) -> torch.Tensor:
     """diffusion/fp8_kernels.py:604-639."""
     fwd_shapes(x, weight, FP8_DTYPE)
-    return conv2d_fp8_fwd_general(x, weight, x_scale, weight_scale, stride=1, padding=1)
+    torch_checks_scale(x_scale, x.device)
+    torch_checks_scale(weight_scale, x.device)
+    return _ops.conv_fwd(x, weight, x_scale, weight_scale, 1, 1)
 
 
 def conv2d_fwd_fp8(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
@@ -547,7 +553,7 @@ def conv2d_bwd_input_fp8_prequantized(
     batch, cin, cout, height, width = xgrad_shapes(dy, weight, FP8_DTYPE)
     torch_checks_scale(dy_scale, dy.device)
     torch_checks_scale(weight_scale, dy.device)
-    return conv2d_fp8_dgrad_general(dy, weight, dy_scale, weight_scale, (height, width), 1, 1)
+    return _ops.conv_dgrad(dy, weight, dy_scale, weight_scale, height, width, 1, 1)
 
 
 def conv2d_bwd_input_fp8(dy: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
@@ -575,7 +581,7 @@ def conv2d_bwd_weight_fp8_prequantized(
     if not (x.is_contiguous(memory_format=torch.channels_last)
             and dy.is_contiguous(memory_format=torch.channels_last)):
         raise NotImplementedError
-    return conv2d_fp8_wgrad_general(x, dy, x_scale, dy_scale, 3, 1, 1, split_k, out_f32)
+    return _ops.conv_wgrad(x, dy, x_scale, dy_scale, 3, 1, 1, split_k or 0, out_f32)
 
 
 def conv2d_bwd_weight_fp8(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
@@ -732,7 +738,7 @@ class Conv2dFP8General(torch.autograd.Function):
         ctx.save_for_backward(x_fp8, w_fp8, x_scale, w_scale)
         ctx.stride, ctx.padding = stride, padding
         ctx.input_hw = (x.shape[2], x.shape[3])
-        return conv2d_fp8_fwd_general(x_fp8, w_fp8, x_scale, w_scale, stride, padding)
+        return _ops.conv_fwd(x_fp8, w_fp8, x_scale, w_scale, stride, padding)
 
     @staticmethod
     @custom_bwd(device_type="cuda")
@@ -743,9 +749,10 @@ class Conv2dFP8General(torch.autograd.Function):
         k = w_fp8.shape[2]
         dx = None
         if ctx.needs_input_grad[0]:
-            dx = conv2d_fp8_dgrad_general(dy_fp8, w_fp8, dy_scale, w_scale, ctx.input_hw,
-                                          ctx.stride, ctx.padding)
-        dw = conv2d_fp8_wgrad_general(x_fp8, dy_fp8, x_scale, dy_scale, k, ctx.stride, ctx.padding)
+            dx = _ops.conv_dgrad(dy_fp8, w_fp8, dy_scale, w_scale, ctx.input_hw[0],
+                                 ctx.input_hw[1], ctx.stride, ctx.padding)
+        dw = _ops.conv_wgrad(x_fp8, dy_fp8, x_scale, dy_scale, k, ctx.stride, ctx.padding, 0,
+                             False)
         return dx, dw, None, None
 
 
@@ -894,7 +901,7 @@ class LinearFP8Function(torch.autograd.Function):
         xq, xs = quantize_fp8_tensor(x2)
         wq, wsc = quantize_fp8_tensor(w)
         b32 = None if bias is None else bias.detach().float().contiguous()
-        y = linear_fp8_prequantized(xq, wq, xs, wsc, b32)
+        y = _ops.gemm(xq, wq, xs, wsc, b32)
         ctx.save_for_backward(xq, wq, xs, wsc)
         ctx.lead = lead
         ctx.has_bias = bias is not None
@@ -909,9 +916,9 @@ class LinearFP8Function(torch.autograd.Function):
         dyq, dys = quantize_fp8_tensor(dy2)
         dx = dw = db = None
         if ctx.needs_input_grad[0]:
-            dx = linear_fp8_dgrad_prequantized(dyq, wq, dys, wsc).reshape(*ctx.lead, k)
+            dx = _ops.gemm_dgrad(dyq, wq, dys, wsc).reshape(*ctx.lead, k)
         if ctx.needs_input_grad[1]:
-            dw = linear_fp8_wgrad_prequantized(xq, dyq, xs, dys)
+            dw = _ops.gemm_wgrad(xq, dyq, xs, dys, False)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = dy2.float().sum(0)
         return dx, dw, db
@@ -1081,3 +1088,7 @@ class LinearFP8Prepared(torch.autograd.Function):
 
 def linear_fp8_autograd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     return LinearFP8Function.apply(x, weight, bias)
+
+
+# registers the torch.ops.dpa_fp8 custom ops the reference-named functions above call
+from . import ops as _ops  # noqa: E402

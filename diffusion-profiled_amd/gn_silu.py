@@ -20,7 +20,7 @@ from .fp8_kernels import FP8_DTYPE, Fp8Handoff, placeholder
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 DTYPE_BF16, DTYPE_F32 = 0, 1  # include/dpa_fp8.h DPA_DTYPE_*

@@ -21,7 +21,7 @@ MAX_LAYERS = 32
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 def supported(m: int, k: int, ns) -> bool:

@@ -18,7 +18,7 @@ from . import fp8_kernels as _fp8
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 def supported(c: int) -> bool:

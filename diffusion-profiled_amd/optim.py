@@ -98,7 +98,7 @@ class FusedAdamWEMA:
         ws_bytes = _lib.load().dpa_adamw_ema_workspace_bytes(addr, count)
         if self._ws is None or self._ws.numel() < ws_bytes:
             self._ws = torch.empty(ws_bytes, device=self.step_t.device, dtype=torch.uint8)
-        stream = torch.cuda.current_stream(self.step_t.device).cuda_stream
+        stream = _lib.current_stream(self.step_t)
         _lib.check(_lib.load().dpa_adamw_ema_step(
             addr, count, self.step_t.data_ptr(), self.lr, self.betas[0], self.betas[1], self.eps,
             self.wd, self.max_norm, self.ema_beta, self._ws.data_ptr(), ws_bytes, stream),

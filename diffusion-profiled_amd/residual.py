@@ -18,7 +18,7 @@ INV_SQRT2 = float(np.float32(1.0) / np.float32(math.sqrt(2.0)))
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.current_stream(t)
 
 
 def _same_dense(a: torch.Tensor, b: torch.Tensor) -> bool:

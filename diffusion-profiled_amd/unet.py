@@ -175,7 +175,7 @@ class Conv2dFP8(_PreparedFP8Weight, nn.Module):
             x = x.contiguous(memory_format=torch.channels_last)
             if self.scaling_type == "current":
                 return K.triton_conv2d_fp8(x, self.conv.weight)
-            if self.fused_window_update:
+            if self.fused_window_update and not torch.compiler.is_compiling():
                 pw = self._prepared("delayed")
                 if pw is not None:
                     return K.Conv2dFP8DelayedPrepared.apply(
@@ -558,7 +558,9 @@ class UNet(nn.Module):
     _fp8_seen = False
 
     def _weight_prep(self, x: torch.Tensor):
-        if not self.weight_prep_enabled or not x.is_cuda:
+        if not self.weight_prep_enabled or not x.is_cuda or torch.compiler.is_compiling():
+            # under torch.compile every FP8 layer takes its per-call path: the reference's op
+            # API, registered as torch.library custom ops (ops.py), which the graph holds
             return None
         if self._wprep is None:
             if not self._fp8_seen or torch.cuda.is_current_stream_capturing():

@@ -163,14 +163,14 @@ class WeightPrep:
         """Write the window records the delayed layers' last x / dy quantizations left pending
         (run() does this first; call it before reading or saving the windows)."""
         if self.n_delayed:
-            stream = torch.cuda.current_stream(self.table.device).cuda_stream
+            stream = _lib.current_stream(self.table)
             _lib.call("dpa_delayed_windows_finalize", self.deferred.data_ptr(), self.n_delayed,
                       stream)
 
     def run(self) -> None:
         """The step's weights: the previous step's pending window records, the window maxima
         (delayed layers), then amax + cast of every weight."""
-        stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        stream = _lib.current_stream(self.table)
         self.x_cache.clear()
         self.flush()
         if self.windows is not None:
@@ -246,7 +246,7 @@ class TensorPrep:
         return self.scales[i]
 
     def run(self) -> None:
-        stream = torch.cuda.current_stream(self.table.device).cuda_stream
+        stream = _lib.current_stream(self.table)
         _lib.call("dpa_weight_prep_run", self.table.data_ptr(), self.count, self.blocks,
                   self.workspace.data_ptr(), self.ws_bytes, stream)
 
@@ -263,7 +263,7 @@ class TensorPrep:
         scale = torch.empty((), device=x.device, dtype=torch.float32)
         ws_bytes = _lib.query("dpa_quant_workspace_bytes", n)
         ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-        stream = torch.cuda.current_stream(x.device).cuda_stream
+        stream = _lib.current_stream(x)
         _lib.call("dpa_quantize_fp8_bf16_with_weight_prep", x.data_ptr(), n, q.data_ptr(),
                   scale.data_ptr(), ws.data_ptr(), ws_bytes, self.table.data_ptr(), self.count,
                   self.blocks, self.workspace.data_ptr(), self.ws_bytes, stream)
