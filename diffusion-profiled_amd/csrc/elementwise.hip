@@ -115,7 +115,7 @@ __global__ __launch_bounds__(kEwThreads) void residual_bwd_q_kernel(
   store_amax_partial(acc, red, part, count, blockIdx.x, gridDim.x);
 }
 
-// Decoder input of the U-Net (diffusion/unet.py:389-392): y = cat([up(a), h], channels) in
+// Decoder input of the U-Net (diffusion/unet.py:379-382): y = cat([up(a), h], channels) in
 // NHWC, fp32 (autocast runs F.interpolate in fp32 and the concatenation promotes), where
 // up(a) is a 2x nearest upsampling of a (or a itself). One pass reads a and h once and writes
 // y; the upsampled tensor is never formed. 4 channels per thread.

@@ -1,5 +1,5 @@
 // LayerNorm over the channel axis of token rows, bf16 in and out, fp32 statistics: the
-// attention block's norm (diffusion/unet.py:182, nn.LayerNorm(hidden) on the [B, H*W, C]
+// attention block's norm (diffusion/unet.py:174, nn.LayerNorm(hidden) on the [B, H*W, C]
 // token view of the channels-last activation, run by autocast in fp32 and rounded to bf16 by
 // the qkv projection's cast). Reading the bf16 tokens and writing the bf16 result directly
 // replaces torch's fp32 upcast copy, fp32 LayerNorm and the bf16 downcast copy (and the same

@@ -177,4 +177,12 @@ class MSELossHIP(torch.autograd.Function):
 
 
 def mse_loss_hip(pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """F.mse_loss(pred, target) on the GPU for operands of one shape. F.mse_loss broadcasts
+    other shapes (with a warning); the kernel reads pred.numel() elements of each operand, so
+    a mismatch is refused here rather than read out of bounds."""
+    if pred.shape != target.shape:
+        raise ValueError(f"mse_loss_hip: pred {tuple(pred.shape)} and target "
+                         f"{tuple(target.shape)} differ in shape")
+    if pred.device != target.device:
+        raise ValueError(f"mse_loss_hip: pred on {pred.device}, target on {target.device}")
     return MSELossHIP.apply(pred, target)

@@ -1,7 +1,7 @@
 """LayerNorm on bf16 token rows with fp32 statistics, as an autograd Function (the HIP
 library's dpa_layernorm_*).
 
-Replaces the attention block's ``self.norm(seq)`` (diffusion/unet.py:182, :186), which
+Replaces the attention block's ``self.norm(seq)`` (diffusion/unet.py:174, :187), which
 autocast runs in fp32 (on an fp32 copy of bf16 tokens, or on fp32 tokens of the fp32 residual
 stream as they are) and whose result the qkv projection rounds back to bf16: here the kernel
 reads the bf16 or fp32 tokens and writes that bf16 result; the input gradient comes back in

@@ -150,7 +150,7 @@ _DT = {torch.bfloat16: 0, torch.float32: 1}  # include/dpa_fp8.h DPA_DTYPE_*
 
 class UpsampleConcat(torch.autograd.Function):
     """cat([up(a), h], dim=1), fp32, NHWC, with up the 2x nearest upsampling (or identity):
-    the decoder input of diffusion/unet.py:389-392 in one pass each way."""
+    the decoder input of diffusion/unet.py:379-382 in one pass each way."""
 
     @staticmethod
     def forward(ctx: Any, a: torch.Tensor, h: torch.Tensor, up: bool) -> torch.Tensor:

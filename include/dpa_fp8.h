@@ -85,8 +85,9 @@ int dpa_quantize_fp8_bf16_from_partials(const void* x, int64_t n, const void* pa
  * process ends; its device address is looked up once per device on the first call there).
  * No counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc). Calls no hipMalloc,
- * hipFree or allocating library routine. Every n > 0 fits (the partial count is capped at
- * 1024); a size whose workspace would exceed the array returns DPA_ERR_WORKSPACE. All calls
+ * hipFree or allocating library routine. Every n > 0 fits: the amax pass's grid, and so the
+ * partial count (dpa_quant_partials_count(n)), is at most 256, and the array holds 1024; a
+ * size whose workspace would exceed the array returns DPA_ERR_WORKSPACE. All calls
  * on one GPU share the array: calls that overlap on that GPU (concurrent streams, threads)
  * race and must be serialised by the caller. The stream's device (or the current device for
  * the NULL stream) selects the array. */
@@ -245,11 +246,16 @@ int dpa_gn_silu_fwd_bf16(const void* x, const float* gamma, const float* beta,
                          float* mean, float* rstd, int N, int HW, int C, int G, float eps,
                          void* stream);
 
-/* The same forward with a workspace (size from dpa_gn_silu_fwd_workspace_bytes; 0 for
- * images under 256 pixels). For images of 256+ pixels it runs the chunked form: two
- * launches, each (image, 64-channel slab) spread over workgroups of 128 pixels whose group
- * statistics (chunk mean and squared deviations, merged in chunk order) cross through the
- * workspace. The FiLM is either film_scale/film_shift (fp32 [N, C]) or film_wb (the bf16 time
+/* The same forward with a workspace (size from dpa_gn_silu_fwd_workspace_bytes: 0 under 256
+ * pixels; nonzero from 256, used only above 1024). Which form runs, by image size HW:
+ *   HW <= 1024: the resident form, one launch, one workgroup per (image, 64-channel slab)
+ *     holding the slab's pixels in registers (no workspace read);
+ *   1024 < HW <= 8192 with the workspace: the chunked form, two launches, each (image, slab)
+ *     spread over workgroups of 128 pixels whose group statistics (chunk mean and squared
+ *     deviations, merged in chunk order) cross through the workspace;
+ *   otherwise (HW > 8192, or no workspace): one launch of one workgroup per (image, slab)
+ *     making three passes over the slab.
+ * The FiLM is either film_scale/film_shift (fp32 [N, C]) or film_wb (the bf16 time
  * projection [N, 2C], as in dpa_gn_silu_film_fwd_bf16) or neither. */
 int64_t dpa_gn_silu_fwd_workspace_bytes(int N, int HW, int C, int G);
 int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const float* beta,
@@ -259,8 +265,11 @@ int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const float* beta
                             void* stream);
 
 /* Bytes of workspace dpa_gn_silu_bwd_bf16 needs: per-image channel partial sums (2*N*C fp32)
- * and, for images of 256+ pixels, the chunk sums of the chunked backward (two launches like
- * the forward). A workspace of only 2*N*C floats runs the one-launch form. */
+ * and, from 256 pixels, room for the chunk sums of the chunked backward (two launches like
+ * the forward). The backward runs the resident form up to 1024 pixels (fp32 x: up to 256
+ * pixels, since its 3 x 16 B per pixel exceed the register file at 16 pixels per lane), the
+ * chunked form above that up to 8192 pixels with the full workspace, and the one-launch form
+ * with a workspace of only 2*N*C floats. */
 int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G);
 
 /* Backward of dpa_gn_silu_fwd_bf16 given dout (bf16, same layout as out). Writes dx (bf16)
@@ -296,9 +305,10 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * film_scale/film_shift or film_wb). Under autocast the reference normalises an fp32 input
  * in fp32 (nn.GroupNorm runs in float32, diffusion/unet.py:151, :157) and returns an fp32
  * input gradient; with DPA_DTYPE_F32 the kernels read the fp32 x as it is and write dx in
- * fp32 (the output y stays bf16). fp32 x takes the chunked form (images of 256+ pixels, a
- * workspace of the *_workspace_bytes size) or the small-image form (<= 128 pixels); other
- * sizes return DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE.
+ * fp32 (the output y stays bf16). fp32 x takes the resident form (images of up to 1024
+ * pixels; the backward up to 256) or the chunked form (above that, up to 8192 pixels, with a
+ * workspace of the *_workspace_bytes size); larger images return DPA_ERR_SHAPE, a missing
+ * workspace DPA_ERR_WORKSPACE.
  * Optional dropout of the output (diffusion/unet.py:160, nn.Dropout(p) before conv_2):
  * drop_seed = a uint64 in device memory, NULL for none; an element is kept when its 32-bit
  * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
@@ -306,12 +316,12 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * argument (exact in double; 0xffffffff when that reaches 2^32 - 1), and kept values are
  * scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
  * reference drops the fp32 SiLU output). The backward recomputes the mask from the same seed
- * and p. Dropout takes the chunked or small-image form as fp32 x does; 0 <= p < 1.
+ * and p. Dropout takes the resident or chunked form as fp32 x does; 0 <= p < 1.
  * dx_add (backward; x's dtype and layout, or NULL): a second gradient of x added to dx as
  * autograd accumulates it (fp32: one add; bf16: bf16(dx) + add, rounded to bf16) — the skip
  * path's gradient of the residual block input (diffusion/unet.py:149, :161), which x feeds
  * besides norm1; dx_add_dtype DPA_DTYPE_BF16 with an fp32 x adds a bf16 gradient (autograd's
- * fp32 cast of it, then one fp32 add). Chunked or small-image form only; may alias dx.
+ * fp32 cast of it, then one fp32 add). Resident or chunked form only; may alias dx.
  * Any other dx_add_dtype, or an fp32 dx_add beside a bf16 x, returns DPA_ERR_SHAPE.
  * x_bf16 (forward, fp32 x only, or NULL): also writes x rounded to bf16 (RNE) there — the
  * input the 1x1 skip conv rounds to anyway — so no separate cast pass reads x again. */
@@ -340,9 +350,12 @@ int dpa_gn_silu_bwd_ex(const void* x, int x_dtype, const void* dout, const float
  * *q_count: the layout dpa_quantize_fp8_delayed_deferred_bf16 leaves for
  * dpa_delayed_windows_finalize. Bytes and window record equal those of the unfused pair
  * (bf16 entry, then the deferred cast). Arguments otherwise as dpa_gn_silu_fwd_ex /
- * dpa_gn_silu_bwd_ex; the backward takes bf16 x and no dx_add. Only the chunked
- * (256..8192 pixels) and small (<= 128 pixels) forms cast: other image sizes return
- * DPA_ERR_SHAPE. q_partials_cap < dpa_gn_silu_fp8_partials(...) returns DPA_ERR_WORKSPACE. */
+ * dpa_gn_silu_bwd_ex; the backward takes bf16 x and no dx_add. The resident form (images of
+ * up to 1024 pixels, one partial per (image, 64-channel slab)) and the chunked form (up to
+ * 8192 pixels with the workspace, one partial per 128-pixel chunk of each slab) cast; larger
+ * images return DPA_ERR_SHAPE, a chunked-size image without the workspace
+ * DPA_ERR_WORKSPACE. q_partials_cap < dpa_gn_silu_fp8_partials(...) returns
+ * DPA_ERR_WORKSPACE. */
 int dpa_gn_silu_fp8_partials(int N, int HW, int C, int G);
 int dpa_gn_silu_fwd_fp8(const void* x, int x_dtype, const float* gamma, const float* beta,
                         const float* film_scale, const float* film_shift, const void* film_wb,
@@ -477,8 +490,8 @@ int dpa_grouped_linear_dgrad_fp8(const void* dyq, const float* dy_scale, const v
 
 /* ------------------------------------------------------------------------------------------
  * LayerNorm over the channel axis of bf16 token rows [rows][C], fp32 statistics (biased
- * variance), bf16 out: the attention block's nn.LayerNorm (diffusion/unet.py:182, applied at
- * :186 to the [B, H*W, C] view of the channels-last activation; autocast runs it in fp32 and
+ * variance), bf16 out: the attention block's nn.LayerNorm (diffusion/unet.py:174, applied at
+ * :187 to the [B, H*W, C] view of the channels-last activation; autocast runs it in fp32 and
  * the qkv projection rounds its output to bf16, which is what `out` stores).
  *   out = bf16((x - mean) * rstd * gamma + beta);  mean/rstd [rows] saved for the backward.
  * Backward: dx (bf16), dgamma/dbeta (fp32, summed over rows in a fixed order).
@@ -495,7 +508,7 @@ int dpa_layernorm_bwd_bf16(const void* x, const void* dout, const float* gamma,
 
 /* The LayerNorm entries with x (and dx) in bf16 or fp32 (DPA_DTYPE_*), the output y bf16:
  * an fp32 token row (the fp32 residual stream) is normalised as it is, as autocast's float32
- * nn.LayerNorm does (diffusion/unet.py:182), and its gradient returned in fp32. */
+ * nn.LayerNorm does (diffusion/unet.py:174, :187), and its gradient returned in fp32. */
 int dpa_layernorm_fwd_ex(const void* x, int x_dtype, const float* gamma, const float* beta,
                          void* out, float* mean, float* rstd, int64_t rows, int C, float eps,
                          void* stream);
@@ -572,7 +585,7 @@ int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, void* gbq,
                                uint32_t* gb_count, int64_t n, float inv, void* stream);
 
 /* Decoder input of the U-Net: y = cat([up(a), h], dim=1) in NHWC, fp32, where up is the 2x
- * nearest upsampling (up = 1) or the identity (up = 0) -- diffusion/unet.py:389-392,
+ * nearest upsampling (up = 1) or the identity (up = 0) -- diffusion/unet.py:379-382,
  * torch.concat([self.upsample(act), h]) under autocast (F.interpolate runs in fp32 and the
  * concatenation promotes). a: [N][H >> up][W >> up][C1], h: [N][H][W][C2], each bf16 or fp32
  * (DPA_DTYPE_*); y: [N][H][W][C1 + C2] fp32. C1, C2 multiples of 4. One pass, no upsampled

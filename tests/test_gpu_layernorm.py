@@ -1,5 +1,5 @@
 """GPU parity of the fused bf16 LayerNorm (dpa_layernorm_*, layer_norm.LayerNormBF16) against a
-float64 torch reference: the attention block's nn.LayerNorm (diffusion/unet.py:182, :186) run
+float64 torch reference: the attention block's nn.LayerNorm (diffusion/unet.py:174, :187) run
 in fp32 by autocast and rounded to bf16 by the qkv projection. Forward within one bf16 ulp
 (almost all bit-identical), statistics to 1e-5, dx to the conv tolerance, dgamma/dbeta 1e-4.
 """

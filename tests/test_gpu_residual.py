@@ -71,7 +71,7 @@ def test_residual_join_fp32_stream_bit_exact(shape, cl, swap):
 ])
 def test_upsample_concat_bit_exact(n, c1, c2, h, w, up, a32, h32):
     """cat([F.interpolate(a, 2x nearest), h], 1) as the U-Net evaluates it under autocast
-    (diffusion/unet.py:389-392): the fp32 output and both gradients (the upsampling's summed
+    (diffusion/unet.py:379-382): the fp32 output and both gradients (the upsampling's summed
     in torch's order, each cast to its operand's dtype) bit for bit."""
     g = torch.Generator().manual_seed(n * 100 + c1 + h)
     hl, wl = (h // 2, w // 2) if up else (h, w)

@@ -258,3 +258,14 @@ def test_checkpoint_round_trip_in_reference_format(tmp_path):
     torch.save({"step": 1}, tmp_path / "n.pt")
     with pytest.raises(KeyError):
         T.load_checkpoint(tmp_path / "n.pt")
+
+
+def test_mse_loss_hip_refuses_mismatched_operands():
+    """The HIP loss reads pred.numel() elements of each operand: a target of another shape
+    (which F.mse_loss would broadcast) or on another device is refused before any launch."""
+    D = dpa_mod("ddpm")
+    pred = torch.zeros((2, 3, 4, 4))
+    with pytest.raises(ValueError):
+        D.mse_loss_hip(pred, torch.zeros((1, 3, 4, 4)))
+    with pytest.raises(ValueError):
+        D.mse_loss_hip(pred, torch.zeros((2, 3, 4, 4), device="meta"))
