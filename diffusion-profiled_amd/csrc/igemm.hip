@@ -66,7 +66,14 @@ struct IgemmArgs {
   int kc_per_tap, nk;  // K-steps per tap (C / 128) and per work item (a tile's K range)
   int splits;          // K ranges per tile: work item = (tile, split), item / splits = tile
   float* partial;      // splits > 1: fp32 partial sums per work item, in accumulator order
-  FastDiv divQ, divP, divKC, divNX, divNK, divTN, divSP;
+  // Output parity classes of a strided data gradient in one launch. Tiles are class-major,
+  // tiles_pc per class; class c offsets its output pixels by (cls_oy[c], cls_ox[c]) and its
+  // taps by input (cls_dy0[c], cls_dx0[c]) and weight tap cls_w0[c], and only cls_ny[c] x
+  // cls_nx[c] of the launch's ny x nx taps are real (the others read zero rows, so their
+  // MFMAs add zeros). nclass = 1: the scalar fields above, as class 0.
+  int nclass, tiles_pc;
+  int cls_oy[4], cls_ox[4], cls_dy0[4], cls_dx0[4], cls_w0[4], cls_ny[4], cls_nx[4];
+  FastDiv divQ, divP, divKC, divNX, divNK, divTN, divSP, divPC;
 };
 
 // 16 zero bytes: the DMA source for padding taps and rows past M.
@@ -91,10 +98,17 @@ __device__ __forceinline__ void decode_pixel(const IgemmArgs& p, int m, int& n, 
   n = (int)nn;
 }
 
-__device__ __forceinline__ int out_offset(const IgemmArgs& p, int m) {
+__device__ __forceinline__ int out_offset(const IgemmArgs& p, int m, int oy_off, int ox_off) {
   int n, ii, jj;
   decode_pixel(p, m, n, ii, jj);
-  return ((n * p.Ho + ii * p.oy_step + p.oy_off) * p.Wo + jj * p.ox_step + p.ox_off) * p.Cout;
+  return ((n * p.Ho + ii * p.oy_step + oy_off) * p.Wo + jj * p.ox_step + ox_off) * p.Cout;
+}
+
+// output tile -> (class, tile within the class)
+__device__ __forceinline__ int tile_class(const IgemmArgs& p, int tile, int& tic) {
+  const int c = p.nclass > 1 ? (int)fdiv((uint32_t)tile, p.divPC) : 0;
+  tic = tile - c * p.tiles_pc;
+  return c;
 }
 
 __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
@@ -129,12 +143,20 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   int a_off[kALoads], a_mask[kALoads], b_off[kBLoads];
   int dma_tile = -1;
   int dma_k0 = 0;  // first global K-step of the item being loaded
+  int dma_dy0 = 0, dma_dx0 = 0, dma_w0 = 0, dma_ny = 0, dma_nx = 0;  // its class's taps
   auto set_dma_tile = [&](int j) __attribute__((always_inline)) {
     const int item = t_begin + j * p.wg_per_xcd;
     const int tile = (int)fdiv((uint32_t)item, p.divSP);
     dma_k0 = (item - tile * p.splits) * nk;
-    const int tm = (int)fdiv((uint32_t)tile, p.divTN);
-    const int tn = tile - tm * p.tiles_n;
+    int tic;
+    const int cls = tile_class(p, tile, tic);
+    dma_dy0 = p.cls_dy0[cls];
+    dma_dx0 = p.cls_dx0[cls];
+    dma_w0 = p.cls_w0[cls];
+    dma_ny = p.cls_ny[cls];
+    dma_nx = p.cls_nx[cls];
+    const int tm = (int)fdiv((uint32_t)tic, p.divTN);
+    const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
 #pragma unroll
     for (int r = 0; r < kALoads; ++r) {
@@ -151,8 +173,8 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
         for (int ty = 0; ty < kMaxTapDim; ++ty) {
 #pragma unroll
           for (int tx = 0; tx < kMaxTapDim; ++tx) {
-            const int iy = iy0 + p.dy0 + ty * p.dys, ix = ix0 + p.dx0 + tx * p.dxs;
-            const bool in = (ty < p.ny) & (tx < p.nx) & ((unsigned)iy < (unsigned)p.Hi) &
+            const int iy = iy0 + dma_dy0 + ty * p.dys, ix = ix0 + dma_dx0 + tx * p.dxs;
+            const bool in = (ty < dma_ny) & (tx < dma_nx) & ((unsigned)iy < (unsigned)p.Hi) &
                             ((unsigned)ix < (unsigned)p.Wi);
             mask |= (int)in << (ty * p.nx + tx);
           }
@@ -183,8 +205,11 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int c0 = (k - t * p.kc_per_tap) * kBK;
     const int ty = (int)fdiv((uint32_t)t, p.divNX);
     const int tx = t - ty * p.nx;
-    const int ad = ((p.dy0 + ty * p.dys) * p.Wi + p.dx0 + tx * p.dxs) * p.C + c0;
-    const int wd = (p.w0 + ty * p.wys + tx * p.wxs) * p.C + c0;
+    const int ad = ((dma_dy0 + ty * p.dys) * p.Wi + dma_dx0 + tx * p.dxs) * p.C + c0;
+    // a tap past the class's own grid has only zero A rows; its B rows come from the class's
+    // first tap (a valid address; the products are zero)
+    const bool tap_ok = (ty < dma_ny) & (tx < dma_nx);
+    const int wd = (tap_ok ? dma_w0 + ty * p.wys + tx * p.wxs : dma_w0) * p.C + c0;
 #pragma unroll
     for (int r = 0; r < kALoads; ++r) {
       const bool ok = live & ((a_mask[r] >> t) & 1);
@@ -215,8 +240,11 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   auto epilogue = [&](int j) __attribute__((always_inline)) {
     const int item = t_begin + j * p.wg_per_xcd;
     const int tile = (int)fdiv((uint32_t)item, p.divSP);
-    const int tm = (int)fdiv((uint32_t)tile, p.divTN);
-    const int tn = tile - tm * p.tiles_n;
+    int tic;
+    const int cls = tile_class(p, tile, tic);
+    const int oy_off = p.cls_oy[cls], ox_off = p.cls_ox[cls];
+    const int tm = (int)fdiv((uint32_t)tic, p.divTN);
+    const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int c0 = n0 + wn * kWTN;
     if (p.splits > 1) {
@@ -255,7 +283,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
         const int r = c >> 3, g = c & 7;
         const uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((g ^ (r & 7)) * 16));
         const int m = m0 + wm * kWTM + pj * 16 + r;
-        if (m < p.M) st_nt16(p.out + out_offset(p, m) + c0 + g * 8, v);
+        if (m < p.M) st_nt16(p.out + out_offset(p, m, oy_off, ox_off) + c0 + g * 8, v);
       }
     }
 #pragma unroll
@@ -353,7 +381,7 @@ __global__ __launch_bounds__(256) void igemm_split_reduce_kernel(const IgemmArgs
   uint2 o;
   o.x = pack_bf16x2(v[0], v[1]);
   o.y = pack_bf16x2(v[2], v[3]);
-  st_nt8(p.out + out_offset(p, m) + c, o);
+  st_nt8(p.out + out_offset(p, m, p.oy_off, p.ox_off) + c, o);
 }
 
 static int g_num_cus = 0;
@@ -415,11 +443,20 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   if (act_bytes > kMaxOperandBytes || wgt_bytes > kMaxOperandBytes || out_elems > kMaxOperandBytes)
     return DPA_ERR_SIZE;
   finish_geometry(a);
+  if (a.nclass <= 1) {  // one class: the scalar tap grid
+    a.nclass = 1;
+    a.cls_oy[0] = a.oy_off; a.cls_ox[0] = a.ox_off;
+    a.cls_dy0[0] = a.dy0; a.cls_dx0[0] = a.dx0; a.cls_w0[0] = a.w0;
+    a.cls_ny[0] = a.ny; a.cls_nx[0] = a.nx;
+  }
   const int tiles_m = (int)ceil_div(a.M, kBM);
-  const int tiles = tiles_m * a.tiles_n;
+  a.tiles_pc = tiles_m * a.tiles_n;
+  const int tiles = a.tiles_pc * a.nclass;
   int64_t need = 0;
   int splits = plan_splits(tiles, a.nk, num_cus(), &need);
-  if (splits > 1 && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+  // the split reduce writes class 0's pixels only: several classes run unsplit
+  if (splits > 1 && (a.nclass > 1 || !workspace || workspace_bytes < need ||
+                     !aligned(workspace, 16)))
     splits = 1;
   a.splits = splits;
   a.partial = (float*)workspace;
@@ -440,6 +477,7 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   a.divNK = make_fastdiv((uint32_t)a.nk);
   a.divTN = make_fastdiv((uint32_t)a.tiles_n);
   a.divSP = make_fastdiv((uint32_t)a.splits);
+  a.divPC = make_fastdiv((uint32_t)a.tiles_pc);
   igemm_fp8_kernel<<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK || splits == 1) return st;
@@ -541,6 +579,43 @@ static int dgrad_geometry(IgemmArgs& a, int N, int H, int W, int Cin, int Cout, 
   return DPA_OK;
 }
 
+// A strided data gradient whose parity classes all have the same output grid (H and W
+// multiples of the stride) runs as one launch of all classes: every class has its own tap
+// grid inside the largest one, padded with zero taps, so the classes share K-step counts.
+static bool dgrad_classes_merge(int H, int W, int stride) {
+  return stride > 1 && stride * stride <= 4 && H % stride == 0 && W % stride == 0;
+}
+
+static int dgrad_merged_geometry(IgemmArgs& a, int N, int H, int W, int Cin, int Cout, int R,
+                                 int S, int stride, int pad) {
+  int c = 0, ny = 0, nx = 0;
+  for (int ay = 0; ay < stride; ++ay)
+    for (int ax = 0; ax < stride; ++ax, ++c) {
+      IgemmArgs g{};
+      const int st = dgrad_geometry(g, N, H, W, Cin, Cout, R, S, stride, pad, ay, ax);
+      if (st != DPA_OK) return st;
+      if (c == 0) {
+        a.Hi = g.Hi; a.Wi = g.Wi; a.C = g.C; a.Cout = g.Cout; a.T = g.T;
+        a.Pg = g.Pg; a.Qg = g.Qg; a.Ho = g.Ho; a.Wo = g.Wo;
+        a.oy_step = g.oy_step; a.ox_step = g.ox_step; a.iy_step = g.iy_step;
+        a.ix_step = g.ix_step; a.M = g.M;
+        a.dys = g.dys; a.dxs = g.dxs; a.wys = g.wys; a.wxs = g.wxs;
+        a.oy_off = g.oy_off; a.ox_off = g.ox_off; a.dy0 = g.dy0; a.dx0 = g.dx0; a.w0 = g.w0;
+      } else if (g.Pg != a.Pg || g.Qg != a.Qg) {
+        return DPA_ERR_SHAPE;
+      }
+      a.cls_oy[c] = g.oy_off; a.cls_ox[c] = g.ox_off;
+      a.cls_dy0[c] = g.dy0; a.cls_dx0[c] = g.dx0; a.cls_w0[c] = g.w0;
+      a.cls_ny[c] = g.ny; a.cls_nx[c] = g.nx;
+      ny = g.ny > ny ? g.ny : ny;
+      nx = g.nx > nx ? g.nx : nx;
+    }
+  a.nclass = c;
+  a.ny = ny;
+  a.nx = nx;
+  return DPA_OK;
+}
+
 static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const float* ws,
                       void* dx, int N, int H, int W, int Cin, int Cout, int R, int S,
                       int stride, int pad, hipStream_t s, void* workspace = nullptr,
@@ -548,6 +623,13 @@ static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const f
   // the 3x3 / s1 / p1 data gradient is a conv of dy with the mirrored, transposed weight
   if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad) && aligned(dx, 16))
     return hconv_run(dyq, wt, dys, ws, nullptr, dx, N, H, W, Cout, Cin, 1, 0, num_cus(), s);
+  if (dgrad_classes_merge(H, W, stride)) {
+    IgemmArgs a{};
+    fill_common(a, dyq, wt, dx, dys, ws, nullptr);
+    const int st = dgrad_merged_geometry(a, N, H, W, Cin, Cout, R, S, stride, pad);
+    if (st != DPA_OK) return st;
+    return launch_igemm(a, N, s, nullptr, 0);
+  }
   for (int ay = 0; ay < stride; ++ay)
     for (int ax = 0; ax < stride; ++ax) {
       IgemmArgs a{};
@@ -563,6 +645,7 @@ static int conv_dgrad(const void* dyq, const void* wt, const float* dys, const f
 static int64_t conv_dgrad_workspace(int N, int H, int W, int Cin, int Cout, int R, int S,
                                     int stride, int pad) {
   if (use_hconv(N, H, W, Cout, Cin, R, S, stride, pad)) return 0;
+  if (dgrad_classes_merge(H, W, stride)) return 0;  // one launch, never split
   int64_t most = 0;
   for (int ay = 0; ay < stride; ++ay)
     for (int ax = 0; ax < stride; ++ax) {
