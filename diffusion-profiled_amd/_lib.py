@@ -164,6 +164,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int] + [c_void_p] * 8 + [c_int] + [c_void_p] * 4 + [c_int64] + [c_int] * 4
         + [c_float, c_void_p, c_float, c_void_p, c_void_p],
     ),
+    "dpa_gn_silu_fwd_ex_amax": (
+        c_int,
+        [c_void_p, c_int] + [c_void_p] * 9 + [c_int64] + [c_int] * 4
+        + [c_float, c_void_p, c_float, c_void_p, c_void_p, c_int, c_void_p],
+    ),
+    "dpa_gn_silu_fwd_fp8_amax": (
+        c_int,
+        [c_void_p, c_int] + [c_void_p] * 8 + [c_int] + [c_void_p] * 4 + [c_int64] + [c_int] * 4
+        + [c_float, c_void_p, c_float, c_void_p, c_void_p, c_int, c_void_p],
+    ),
     "dpa_gn_silu_bwd_fp8": (
         c_int,
         [c_void_p] * 12 + [c_int] + [c_void_p] * 7 + [c_int64] + [c_int] * 4
@@ -179,6 +189,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_residual_scale_fp8_partials": (c_int, [c_int64]),
     "dpa_residual_scale_bwd_fp8": (
         c_int, [c_void_p, c_int] + [c_void_p] * 4 + [c_int, c_void_p, c_int64, c_float, c_void_p],
+    ),
+    "dpa_residual_scale_bwd_amax": (
+        c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_float, c_void_p],
     ),
 }
 

@@ -207,7 +207,7 @@ __device__ __forceinline__ void store_amax_partial(us2 acc, uint32_t* red, uint3
     uint32_t r = red[0];
     for (int i = 1; i < nw; ++i) r = r > red[i] ? r : red[i];
     partials[blk] = r;
-    if (blk == 0) *count = nblk;
+    if (blk == 0 && count) *count = nblk;
   }
 }
 

@@ -381,6 +381,44 @@ extern "C" int dpa_residual_scale_bf16(const void* a, const void* b, void* y, in
   return launch_status();
 }
 
+// The join's backward for a gradient an FP8 GEMM quantizes next with current scaling (the
+// attention out-projection's dy, a 1x1 skip conv's or a current-scaling conv's dy): the bf16
+// gradient bf16(g * inv) is stored (kF32: ga = g * inv in fp32 and gb = its bf16 rounding;
+// otherwise the one bf16 tensor both operands receive, written to gb) with one amax partial of
+// those bf16 values per workgroup, so the GEMM's cast runs without its amax pass. Grid-strided
+// over groups of 8 elements, as residual_bwd_q_kernel.
+template <bool kF32>
+__global__ __launch_bounds__(kEwThreads) void residual_bwd_amax_kernel(
+    const void* __restrict__ g, float* __restrict__ ga, uint4* __restrict__ gb,
+    uint32_t* __restrict__ part, int64_t n8, float inv) {
+  __shared__ uint32_t red[kEwThreads / 64];
+  us2 acc = {0, 0};
+  for (int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * kEwThreads) {
+    uint4 o;
+    if constexpr (kF32) {
+      const float4* gp = static_cast<const float4*>(g) + 2 * i;
+      const float4 v0 = gp[0], v1 = gp[1];
+      const float4 s0 = float4{v0.x * inv, v0.y * inv, v0.z * inv, v0.w * inv};
+      const float4 s1 = float4{v1.x * inv, v1.y * inv, v1.z * inv, v1.w * inv};
+      float4* ap = reinterpret_cast<float4*>(ga) + 2 * i;
+      ap[0] = s0;
+      ap[1] = s1;
+      o = uint4{pack_bf16x2(s0.x, s0.y), pack_bf16x2(s0.z, s0.w), pack_bf16x2(s1.x, s1.y),
+                pack_bf16x2(s1.z, s1.w)};
+    } else {
+      const uint4 v = static_cast<const uint4*>(g)[i];
+      o = uint4{pack_bf16x2(bf16_lo(v.x) * inv, bf16_hi(v.x) * inv),
+                pack_bf16x2(bf16_lo(v.y) * inv, bf16_hi(v.y) * inv),
+                pack_bf16x2(bf16_lo(v.z) * inv, bf16_hi(v.z) * inv),
+                pack_bf16x2(bf16_lo(v.w) * inv, bf16_hi(v.w) * inv)};
+    }
+    gb[i] = o;
+    acc = absmax8(acc, o);
+  }
+  store_amax_partial(acc, red, part, nullptr, blockIdx.x, gridDim.x);
+}
+
 static int64_t residual_q_blocks(int64_t n) {
   const int64_t b = ceil_div(n / 8, (int64_t)kEwThreads);
   return b < kResQBlocks ? b : kResQBlocks;
@@ -388,6 +426,27 @@ static int64_t residual_q_blocks(int64_t n) {
 
 extern "C" int dpa_residual_scale_fp8_partials(int64_t n) {
   return n > 0 && n % 8 == 0 ? (int)residual_q_blocks(n) : 0;
+}
+
+extern "C" int dpa_residual_scale_bwd_amax(const void* g, int g_dtype, float* ga, void* gb,
+                                           uint32_t* gb_partials, int gb_partials_cap,
+                                           int64_t n, float inv, void* stream) {
+  if (!g || !gb || !gb_partials) return DPA_ERR_NULL;
+  if (g_dtype != DPA_DTYPE_BF16 && g_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if ((g_dtype == DPA_DTYPE_F32) != (ga != nullptr)) return DPA_ERR_NULL;
+  if (n <= 0 || n % 8 != 0) return DPA_ERR_SIZE;
+  const int64_t nb = residual_q_blocks(n);
+  if (gb_partials_cap < nb) return DPA_ERR_WORKSPACE;
+  if (!aligned(g, 16) || !aligned(ga, 16) || !aligned(gb, 16) || !aligned(gb_partials, 4))
+    return DPA_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  if (g_dtype == DPA_DTYPE_F32)
+    residual_bwd_amax_kernel<true><<<(unsigned)nb, kEwThreads, 0, s>>>(
+        g, ga, (uint4*)gb, gb_partials, n / 8, inv);
+  else
+    residual_bwd_amax_kernel<false><<<(unsigned)nb, kEwThreads, 0, s>>>(
+        g, nullptr, (uint4*)gb, gb_partials, n / 8, inv);
+  return launch_status();
 }
 
 extern "C" int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, void* gbq,

@@ -51,6 +51,7 @@ struct GnArgs {
   const void* dx_add;  // bwd: a gradient added to dx (chunked and small forms), or null
   int dx_add_bf16;     // bwd: dx_add is bf16 while x and dx are fp32
   uint16_t* x_bf16;    // fwd: fp32 x also written as bf16 here (chunked and small forms), or null
+  uint32_t* xb_part;   // fwd: with x_bf16, one amax partial of its bf16 values per workgroup
   // Producer-fused cast for a delayed-scaling consumer (chunked and small forms): instead of
   // the bf16 output (fwd) or bf16 dx (bwd), e4m3(bf16 value / *q_scale) goes to q, and each
   // workgroup leaves the amax of its bf16 values in q_part[workgroup] (count in *q_count)
@@ -639,11 +640,20 @@ __device__ __forceinline__ void store_dx(const GnArgs& p, int64_t off, F dx, GnQ
 
 // fp32 x also stored rounded to bf16 (RNE), for a consumer that rounds it anyway (the residual
 // block's 1x1 skip conv), so no separate cast pass reads x again
-__device__ __forceinline__ void store_x_bf16(const GnArgs& p, int64_t off, const float (&f)[8]) {
+__device__ __forceinline__ uint4 store_x_bf16(const GnArgs& p, int64_t off, const float (&f)[8]) {
   uint32_t o[4];
 #pragma unroll
   for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(f[e], f[e + 1]);
-  st_nt16(p.x_bf16 + off, uint4{o[0], o[1], o[2], o[3]});
+  const uint4 w = uint4{o[0], o[1], o[2], o[3]};
+  st_nt16(p.x_bf16 + off, w);
+  return w;
+}
+
+// The workgroup's amax partial of the bf16 copy of x (every thread; red: one u32 per wave), for
+// the current-scaling FP8 conv that quantizes that copy next
+__device__ __forceinline__ void finish_xb_amax(const GnArgs& p, us2 acc, uint32_t* red) {
+  const uint32_t blk = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  store_amax_partial(acc, red, p.xb_part, nullptr, blk, gridDim.x * gridDim.y * gridDim.z);
 }
 
 // The forward's per-channel affine of this thread's 8 channels: out = silu(x A + B) with
@@ -813,13 +823,14 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
   uint16_t* ob = static_cast<uint16_t*>(p.out) + (int64_t)n * p.HW * p.C + ch;
   const uint64_t seed = kDrop ? *p.drop_seed : 0;
   GnQ qo(p);
+  us2 xacc = {0, 0};
 #pragma unroll
   for (int u = 0; u < kChU; ++u) {
     float f[8];
     unpack_x<kF32>(v, u, f);
     const int64_t off = ((int64_t)n * p.HW + pxs[u]) * p.C + ch;
     if constexpr (kF32) {
-      if (p.x_bf16 && ok[u]) store_x_bf16(p, off, f);
+      if (p.x_bf16 && ok[u]) xacc = absmax8(xacc, store_x_bf16(p, off, f));
     }
     const uint32_t kb = kDrop ? drop_keep8(seed, off, p.drop_keep) : 0u;
     const uint4 o = fwd_out8<kDrop>(f, A, B, kb, p.drop_scale);
@@ -831,6 +842,12 @@ __global__ __launch_bounds__(8 * kChPLN) void gn_chunk_apply_kernel(const GnArgs
     }
   }
   if (p.q) qo.finish(p, qred);
+  if constexpr (kF32) {
+    if (p.x_bf16 && p.xb_part) {
+      __syncthreads();  // qred is reused
+      finish_xb_amax(p, xacc, qred);
+    }
+  }
 }
 
 struct GnBwdSetup {
@@ -1107,13 +1124,15 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
   res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
   if constexpr (kF32) {
     if (p.x_bf16) {
+      us2 xacc = {0, 0};
 #pragma unroll
       for (int u = 0; u < U; ++u)
         if (ok[u]) {
           float f[8];
           unpack_x<kF32>(v, u, f);
-          store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f);
+          xacc = absmax8(xacc, store_x_bf16(p, ((int64_t)n * p.HW + pxs[u]) * p.C + ch, f));
         }
+      if (p.xb_part) finish_xb_amax(p, xacc, qred);
     }
   }
   float sm[2] = {0.f, 0.f};
@@ -1433,7 +1452,8 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
                   float* rstd, int N, int HW, int C, int G, float eps, void* stream,
                   void* workspace = nullptr, int64_t workspace_bytes = 0, bool x_f32 = false,
                   const void* drop_seed = nullptr, float drop_p = 0.0f, void* x_bf16 = nullptr,
-                  const GnQOut* qo = nullptr) {
+                  const GnQOut* qo = nullptr, uint32_t* xb_part = nullptr,
+                  int xb_part_cap = 0) {
   if (!x || !gamma || !beta || (!out && !qo) || !mean || !rstd) return DPA_ERR_NULL;
   if (qo && out) return DPA_ERR_SHAPE;  // one output: bf16 or e4m3
   if ((film_scale == nullptr) != (film_shift == nullptr)) return DPA_ERR_NULL;
@@ -1461,6 +1481,15 @@ static int gn_fwd(const void* x, const float* gamma, const float* beta, const fl
   if (x_bf16 && !x_f32) return DPA_ERR_SHAPE;  // the bf16 copy is of an fp32 x
   if (!aligned(x_bf16, 16)) return DPA_ERR_ALIGN;
   a.x_bf16 = (uint16_t*)x_bf16;
+  if (xb_part) {
+    // one partial per workgroup of the launch that writes the copy (the resident form, or
+    // the chunked form's apply launch)
+    if (!x_bf16) return DPA_ERR_NULL;
+    if (!chunked && !resident) return nchunk > 0 ? DPA_ERR_WORKSPACE : DPA_ERR_SHAPE;
+    if (xb_part_cap < gn_q_blocks(N, HW, C)) return DPA_ERR_WORKSPACE;
+    if (!aligned(xb_part, 4)) return DPA_ERR_ALIGN;
+    a.xb_part = xb_part;
+  }
   const int dst = gn_set_dropout(a, drop_seed, drop_p);
   if (dst != DPA_OK) return dst;
   if (qo) {
@@ -1560,6 +1589,26 @@ extern "C" int dpa_gn_silu_fwd_ex(const void* x, int x_dtype, const float* gamma
   return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
                 eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
                 drop_p, x_bf16);
+}
+
+extern "C" int dpa_gn_silu_fwd_ex_amax(const void* x, int x_dtype, const float* gamma,
+                                       const float* beta, const float* film_scale,
+                                       const float* film_shift, const void* film_wb, void* out,
+                                       float* mean, float* rstd, void* workspace,
+                                       int64_t workspace_bytes, int N, int HW, int C, int G,
+                                       float eps, const void* drop_seed, float drop_p,
+                                       void* x_bf16, uint32_t* xb_partials, int xb_partials_cap,
+                                       void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  if (!xb_partials) return DPA_ERR_NULL;
+  if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
+    return DPA_ERR_WORKSPACE;
+  if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, out, mean, rstd, N, HW, C, G,
+                eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
+                drop_p, x_bf16, nullptr, xb_partials, xb_partials_cap);
 }
 
 // per-image channel partials of dgamma/dbeta, then (chunked form) the chunk sums
@@ -1743,6 +1792,29 @@ extern "C" int dpa_gn_silu_fwd_fp8(const void* x, int x_dtype, const float* gamm
   return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, nullptr, mean, rstd, N, HW, C,
                 G, eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
                 drop_p, x_bf16, &qo);
+}
+
+extern "C" int dpa_gn_silu_fwd_fp8_amax(const void* x, int x_dtype, const float* gamma,
+                                        const float* beta, const float* film_scale,
+                                        const float* film_shift, const void* film_wb, void* q,
+                                        const float* q_scale, uint32_t* q_partials,
+                                        int q_partials_cap, uint32_t* q_count, float* mean,
+                                        float* rstd, void* workspace, int64_t workspace_bytes,
+                                        int N, int HW, int C, int G, float eps,
+                                        const void* drop_seed, float drop_p, void* x_bf16,
+                                        uint32_t* xb_partials, int xb_partials_cap,
+                                        void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (film_wb && film_scale) return DPA_ERR_SHAPE;
+  if (!q || !xb_partials) return DPA_ERR_NULL;
+  if (gn_shape_ok(N, HW, C, G) && workspace_bytes < gn_fwd_workspace(N, HW, G))
+    return DPA_ERR_WORKSPACE;
+  if (workspace_bytes > 0 && !workspace) return DPA_ERR_WORKSPACE;
+  if (!aligned(workspace, 8)) return DPA_ERR_ALIGN;
+  const GnQOut qo{q, q_scale, q_partials, q_partials_cap, q_count};
+  return gn_fwd(x, gamma, beta, film_scale, film_shift, film_wb, nullptr, mean, rstd, N, HW, C,
+                G, eps, stream, workspace, workspace_bytes, x_dtype == DPA_DTYPE_F32, drop_seed,
+                drop_p, x_bf16, &qo, xb_partials, xb_partials_cap);
 }
 
 extern "C" int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float* gamma,

@@ -177,8 +177,9 @@ PRODUCER_AMAX = True
 
 
 def mark_amax_partials(t: torch.Tensor, partials: torch.Tensor, count: int) -> torch.Tensor:
-    """Record on t (bf16, contiguous, just written) the int32 buffer holding ``count``
-    per-workgroup maxima of |t| (bf16 magnitude bits) that its producer left."""
+    """Record on t (bf16, dense -- contiguous or channels-last -- and just written) the int32
+    buffer holding ``count`` per-workgroup maxima of |t| (bf16 magnitude bits) that its
+    producer left."""
     t._dpa_amax = (partials, int(count), t.data_ptr(), t._version, t.numel())
     return t
 
@@ -187,13 +188,15 @@ def quantize_fp8_from_producer(x2: torch.Tensor, src: torch.Tensor):
     """``quantize_fp8_tensor(x2)`` from the maxima recorded on ``src`` when x2 is src's data
     unchanged (same address, element count and version), else None."""
     rec = getattr(src, "_dpa_amax", None)
+    if rec is None and src._base is not None:   # a view autograd made of the recorded tensor
+        rec = getattr(src._base, "_dpa_amax", None)
     if rec is None or not PRODUCER_AMAX:
         return None
     partials, count, ptr, version, numel = rec
-    if (x2.dtype != torch.bfloat16 or not x2.is_contiguous() or x2.data_ptr() != ptr
+    if (x2.dtype != torch.bfloat16 or not _dense(x2) or x2.data_ptr() != ptr
             or x2._version != version or x2.numel() != numel):
         return None
-    q = torch.empty_like(x2, dtype=FP8_DTYPE)
+    q = torch.empty_like(x2, dtype=FP8_DTYPE, memory_format=torch.preserve_format)
     scale = torch.empty((), device=x2.device, dtype=torch.float32)
     _lib.call("dpa_quantize_fp8_bf16_from_partials", x2.data_ptr(), x2.numel(),
               partials.data_ptr(), count, q.data_ptr(), scale.data_ptr(), _stream(x2))
@@ -992,8 +995,9 @@ class Conv2dFP8GeneralPrepared(torch.autograd.Function):
     def forward(ctx: Any, x: torch.Tensor, weight: torch.Tensor, wq: torch.Tensor,
                 wq_t: torch.Tensor, w_scale: torch.Tensor, stride: int,
                 padding: int) -> torch.Tensor:
+        src = x
         x = x.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
-        x_fp8, x_scale = quantize_fp8(x)
+        x_fp8, x_scale = quantize_fp8_from_producer(x, src) or quantize_fp8(x)
         ctx.save_for_backward(x_fp8, wq, wq_t, x_scale, w_scale)
         ctx.stride, ctx.padding = stride, padding
         ctx.input_hw = (x.shape[2], x.shape[3])
@@ -1007,8 +1011,9 @@ class Conv2dFP8GeneralPrepared(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     def backward(ctx: Any, dy: torch.Tensor) -> Any:
         x_fp8, wq, wq_t, x_scale, w_scale = ctx.saved_tensors
+        src = dy
         dy = dy.to(torch.bfloat16).contiguous(memory_format=torch.channels_last)
-        dy_fp8, dy_scale = quantize_fp8(dy)
+        dy_fp8, dy_scale = quantize_fp8_from_producer(dy, src) or quantize_fp8(dy)
         k = ctx.k
         dx = None
         if ctx.needs_input_grad[0]:

@@ -16,6 +16,7 @@ from typing import Any
 import torch
 
 from . import _lib
+from . import fp8_kernels as _fp8
 from .fp8_kernels import FP8_DTYPE, Fp8Handoff, placeholder
 
 
@@ -106,21 +107,37 @@ class DropoutSeeds:
 DROPOUT_SEEDS = DropoutSeeds()
 
 
+def _xb_partials(x_bf16, groups):
+    """Room for the amax partials of the bf16 copy of x (one per workgroup of the launch that
+    writes it), or None when that copy is not written or no form records them."""
+    if x_bf16 is None or not _fp8.PRODUCER_AMAX:
+        return None
+    n, c, h, w = x_bf16.shape
+    count = _lib.query("dpa_gn_silu_fp8_partials", n, h * w, c, groups)
+    if count <= 0:
+        return None
+    return torch.empty(count, device=x_bf16.device, dtype=torch.int32)
+
+
 def _fwd_call(x, gamma, beta, fs, fb, wb, out, mean, rstd, groups, eps, seed=None, p_drop=0.0,
               x_bf16=None):
     """The workspace form of the forward (chunked for images of 1025+ pixels); x bf16 or fp32;
-    seed: dropout seed tensor (int64 [1]) or None."""
+    seed: dropout seed tensor (int64 [1]) or None. A bf16 copy x_bf16 of an fp32 x carries the
+    amax partials its writer left (for the current-scaling 1x1 skip conv that reads it)."""
     n, c, h, w = x.shape
     ws_bytes = _lib.query("dpa_gn_silu_fwd_workspace_bytes", n, h * w, c, groups)
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     dt = DTYPE_F32 if x.dtype == torch.float32 else DTYPE_BF16
-    _lib.call(
-        "dpa_gn_silu_fwd_ex",
-        x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb), out.data_ptr(),
-        mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c, groups, float(eps),
-        p(seed), float(p_drop), p(x_bf16), _stream(x),
-    )
+    xbp = _xb_partials(x_bf16, groups)
+    args = (x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), p(fs), p(fb), p(wb),
+            out.data_ptr(), mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c,
+            groups, float(eps), p(seed), float(p_drop), p(x_bf16))
+    if xbp is None:
+        _lib.call("dpa_gn_silu_fwd_ex", *args, _stream(x))
+    else:
+        _lib.call("dpa_gn_silu_fwd_ex_amax", *args, xbp.data_ptr(), xbp.numel(), _stream(x))
+        _fp8.mark_amax_partials(x_bf16, xbp, xbp.numel())
 
 
 def fp8_ok(shape, groups: int, hand: Fp8Handoff) -> bool:
@@ -142,13 +159,16 @@ def _fwd_fp8_call(x, gamma, beta, wb, hand: Fp8Handoff, mean, rstd, groups, eps,
     ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8) if ws_bytes else None
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     dt = DTYPE_F32 if x.dtype == torch.float32 else DTYPE_BF16
-    _lib.call(
-        "dpa_gn_silu_fwd_fp8",
-        x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), None, None, p(wb), q.data_ptr(),
-        hand.scale.data_ptr(), hand.partials.data_ptr(), hand.partials.numel(),
-        hand.count.data_ptr(), mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w, c,
-        groups, float(eps), p(seed), float(p_drop), p(x_bf16), _stream(x),
-    )
+    xbp = _xb_partials(x_bf16, groups)
+    args = (x.data_ptr(), dt, gamma.data_ptr(), beta.data_ptr(), None, None, p(wb), q.data_ptr(),
+            hand.scale.data_ptr(), hand.partials.data_ptr(), hand.partials.numel(),
+            hand.count.data_ptr(), mean.data_ptr(), rstd.data_ptr(), p(ws), ws_bytes, n, h * w,
+            c, groups, float(eps), p(seed), float(p_drop), p(x_bf16))
+    if xbp is None:
+        _lib.call("dpa_gn_silu_fwd_fp8", *args, _stream(x))
+    else:
+        _lib.call("dpa_gn_silu_fwd_fp8_amax", *args, xbp.data_ptr(), xbp.numel(), _stream(x))
+        _fp8.mark_amax_partials(x_bf16, xbp, xbp.numel())
     hand.q = q
 
 

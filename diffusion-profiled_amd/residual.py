@@ -11,7 +11,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .fp8_kernels import FP8_DTYPE, Fp8Handoff, placeholder
+from . import fp8_kernels as _fp8
+from .fp8_kernels import FP8_DTYPE, Fp8Handoff, mark_amax_partials, placeholder
 
 # torch divides by a CPU scalar as a product with the fp32 reciprocal of the scalar
 INV_SQRT2 = float(np.float32(1.0) / np.float32(math.sqrt(2.0)))
@@ -38,14 +39,37 @@ def _scale(a: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
 
 def _bwd_fp8(g: torch.Tensor, hand: Fp8Handoff) -> torch.Tensor:
     """The join's backward writing b's gradient as the e4m3 dy of the conv that produced b
-    (to hand.q); returns a's gradient (g's dtype)."""
+    (to hand.q); returns a's gradient (g's dtype). For a bf16 g, a's gradient holds the very
+    bf16 values b's cast saw, so the cast's amax partials are recorded on it too (a 1x1 skip
+    conv quantizing it next skips its amax pass; the partials stay in the conv's buffer until
+    the next step's window records)."""
     ga = torch.empty_like(g)
     gbq = torch.empty_like(g, dtype=FP8_DTYPE)
     _lib.call("dpa_residual_scale_bwd_fp8", g.data_ptr(), _DT[g.dtype], ga.data_ptr(),
               gbq.data_ptr(), hand.scale.data_ptr(), hand.partials.data_ptr(),
               hand.partials.numel(), hand.count.data_ptr(), g.numel(), INV_SQRT2, _stream(g))
     hand.q = gbq
+    if g.dtype == torch.bfloat16 and _fp8.PRODUCER_AMAX:
+        mark_amax_partials(ga, hand.partials, _lib.query("dpa_residual_scale_fp8_partials",
+                                                         g.numel()))
     return ga
+
+
+def _bwd_amax(g: torch.Tensor) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """The plain join backward (bf16 g: the one bf16 gradient of both operands; fp32 g: the
+    fp32 and the bf16 gradient) with amax partials of the bf16 gradient recorded on it, for a
+    current-scaling FP8 GEMM that quantizes it next. Returns (fp32 gradient or None, bf16
+    gradient)."""
+    n = g.numel()
+    count = _lib.query("dpa_residual_scale_fp8_partials", n)
+    part = torch.empty(count, device=g.device, dtype=torch.int32)
+    f32 = g.dtype == torch.float32
+    ga = torch.empty_like(g) if f32 else None
+    gb = torch.empty_like(g, dtype=torch.bfloat16)
+    _lib.call("dpa_residual_scale_bwd_amax", g.data_ptr(), _DT[g.dtype],
+              None if ga is None else ga.data_ptr(), gb.data_ptr(), part.data_ptr(), count, n,
+              INV_SQRT2, _stream(g))
+    return ga, mark_amax_partials(gb, part, count)
 
 
 def _fp8_grad_ok(g: torch.Tensor, dtype: torch.dtype, hand: Fp8Handoff) -> bool:
@@ -69,6 +93,8 @@ class ResidualScale(torch.autograd.Function):
             return _bwd_fp8(g, hand), placeholder(g.shape, torch.bfloat16, g.device), None
         if g.dtype != torch.bfloat16 or g.numel() % 8 != 0:
             gs = g / math.sqrt(2.0)
+        elif _fp8.PRODUCER_AMAX and hand is None:
+            gs = _bwd_amax(g)[1]
         else:
             gs = _scale(g, None)
         if hand is not None:             # unfused: cast b's gradient in a pass of its own
@@ -99,6 +125,8 @@ class ResidualScaleF32(torch.autograd.Function):
         if g.dtype != torch.float32:
             gs = g.float() / math.sqrt(2.0)
             ga, gb = gs, gs.to(torch.bfloat16)
+        elif _fp8.PRODUCER_AMAX and hand is None and g.numel() % 8 == 0:
+            ga, gb = _bwd_amax(g)
         else:
             ga = torch.empty_like(g)
             gb = torch.empty_like(g, dtype=torch.bfloat16)

@@ -363,6 +363,29 @@ int dpa_gn_silu_fwd_fp8(const void* x, int x_dtype, const float* gamma, const fl
                         uint32_t* q_count, float* mean, float* rstd, void* workspace,
                         int64_t workspace_bytes, int N, int HW, int C, int G, float eps,
                         const void* drop_seed, float drop_p, void* x_bf16, void* stream);
+
+/* dpa_gn_silu_fwd_ex / dpa_gn_silu_fwd_fp8 that also leave, with x_bf16 (fp32 x), one amax
+ * partial of the bf16 copy of x per workgroup of the launch that writes it (u32 bf16
+ * magnitude bits; count dpa_gn_silu_fp8_partials(N, HW, C, G)): the copy is the input of the
+ * residual block's 1x1 skip conv (diffusion/unet.py:137-139, :161), which quantizes it with
+ * current scaling, and dpa_quantize_fp8_bf16_from_partials takes these partials in place of
+ * its amax pass (partial_amax_kernel, diffusion/fp8_kernels.py:54-64). Resident and chunked
+ * forms; xb_partials_cap below the count returns DPA_ERR_WORKSPACE. */
+int dpa_gn_silu_fwd_ex_amax(const void* x, int x_dtype, const float* gamma, const float* beta,
+                            const float* film_scale, const float* film_shift,
+                            const void* film_wb, void* out, float* mean, float* rstd,
+                            void* workspace, int64_t workspace_bytes, int N, int HW, int C,
+                            int G, float eps, const void* drop_seed, float drop_p,
+                            void* x_bf16, uint32_t* xb_partials, int xb_partials_cap,
+                            void* stream);
+int dpa_gn_silu_fwd_fp8_amax(const void* x, int x_dtype, const float* gamma, const float* beta,
+                             const float* film_scale, const float* film_shift,
+                             const void* film_wb, void* q, const float* q_scale,
+                             uint32_t* q_partials, int q_partials_cap, uint32_t* q_count,
+                             float* mean, float* rstd, void* workspace, int64_t workspace_bytes,
+                             int N, int HW, int C, int G, float eps, const void* drop_seed,
+                             float drop_p, void* x_bf16, uint32_t* xb_partials,
+                             int xb_partials_cap, void* stream);
 int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float* gamma, const float* beta,
                         const float* film_scale, const float* film_shift, const void* film_wb,
                         const float* mean, const float* rstd, void* dxq, const float* dx_scale,
@@ -583,6 +606,19 @@ int dpa_residual_scale_fp8_partials(int64_t n);
 int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, void* gbq,
                                const float* gb_scale, uint32_t* gb_partials, int gb_partials_cap,
                                uint32_t* gb_count, int64_t n, float inv, void* stream);
+
+/* The join's backward when the bf16 gradient it writes is quantized next by a current-scaling
+ * FP8 GEMM (the attention out-projection of diffusion/unet.py:199-203, a 1x1 skip conv or a
+ * current-scaling conv feeding the join): the plain backward (g_dtype DPA_DTYPE_F32: ga = g * inv
+ * in fp32 and gb = bf16(g * inv), as dpa_residual_scale_bwd_f32; DPA_DTYPE_BF16: ga NULL and
+ * gb = bf16(g * inv), the one gradient both operands receive, as dpa_residual_scale_bf16 with
+ * b NULL) plus one amax partial of gb per workgroup (u32 bf16 magnitude bits; count
+ * dpa_residual_scale_fp8_partials(n)), which dpa_quantize_fp8_bf16_from_partials takes in place
+ * of the quantization's amax pass (partial_amax_kernel, diffusion/fp8_kernels.py:54-64).
+ * n % 8 == 0, g, ga, gb 16-B aligned. */
+int dpa_residual_scale_bwd_amax(const void* g, int g_dtype, float* ga, void* gb,
+                                uint32_t* gb_partials, int gb_partials_cap, int64_t n,
+                                float inv, void* stream);
 
 /* Decoder input of the U-Net: y = cat([up(a), h], dim=1) in NHWC, fp32, where up is the 2x
  * nearest upsampling (up = 1) or the identity (up = 0) -- diffusion/unet.py:379-382,
