@@ -67,12 +67,12 @@ struct IgemmArgs {
   int splits;          // K ranges per tile: work item = (tile, split), item / splits = tile
   float* partial;      // splits > 1: fp32 partial sums per work item, in accumulator order
   // Output parity classes of a strided data gradient in one launch. Tiles are class-major,
-  // tiles_pc per class; class c offsets its output pixels by (cls_oy[c], cls_ox[c]) and its
-  // taps by input (cls_dy0[c], cls_dx0[c]) and weight tap cls_w0[c], and only cls_ny[c] x
-  // cls_nx[c] of the launch's ny x nx taps are real (the others read zero rows, so their
-  // MFMAs add zeros). nclass = 1: the scalar fields above, as class 0.
+  // tiles_pc per class; class c offsets its output pixels by (oy, ox) and its taps by input
+  // (dy0, dx0) and weight tap w0, and only ny x nx of the launch's ny x nx taps are real (the
+  // others read zero rows, so their MFMAs add zeros). cls[c] packs them as 4-bit fields
+  // (cls_field). nclass = 1: the scalar fields above.
   int nclass, tiles_pc;
-  int cls_oy[4], cls_ox[4], cls_dy0[4], cls_dx0[4], cls_w0[4], cls_ny[4], cls_nx[4];
+  uint32_t cls[4];
   FastDiv divQ, divP, divKC, divNX, divNK, divTN, divSP, divPC;
 };
 
@@ -111,6 +111,23 @@ __device__ __forceinline__ int tile_class(const IgemmArgs& p, int tile, int& tic
   return c;
 }
 
+// fields of a packed class word, 4 bits each
+enum ClsField { kClsOy = 0, kClsOx = 4, kClsDy0 = 8, kClsDx0 = 12, kClsW0 = 16, kClsNy = 20,
+                kClsNx = 24 };
+__host__ __device__ __forceinline__ int cls_field(uint32_t w, ClsField f) {
+  return (int)((w >> f) & 15u);
+}
+
+// p.cls[c] by constant indices: the kernel arguments are then all read at the start, in one
+// batch, instead of by a load whose address waits for c
+__device__ __forceinline__ uint32_t cls_word(const IgemmArgs& p, int c) {
+  uint32_t v = p.cls[0];
+  v = c == 1 ? p.cls[1] : v;
+  v = c == 2 ? p.cls[2] : v;
+  v = c == 3 ? p.cls[3] : v;
+  return v;
+}
+
 __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
   const int s = swz(row);
   const uint4 lo = *reinterpret_cast<const uint4*>(base + row * kBK + (((2 * q) ^ s) * 16));
@@ -118,6 +135,10 @@ __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
+// kClasses: the launch holds several output parity classes (p.nclass > 1). The one-class
+// instance reads the scalar tap grid only: the class tables would take SGPRs the main loop
+// needs (with them it reloads kernel arguments inside the loop, ~1 us per launch).
+template <bool kClasses>
 __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -148,13 +169,21 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int item = t_begin + j * p.wg_per_xcd;
     const int tile = (int)fdiv((uint32_t)item, p.divSP);
     dma_k0 = (item - tile * p.splits) * nk;
-    int tic;
-    const int cls = tile_class(p, tile, tic);
-    dma_dy0 = p.cls_dy0[cls];
-    dma_dx0 = p.cls_dx0[cls];
-    dma_w0 = p.cls_w0[cls];
-    dma_ny = p.cls_ny[cls];
-    dma_nx = p.cls_nx[cls];
+    int tic = tile;
+    if constexpr (kClasses) {
+      const uint32_t cw = cls_word(p, tile_class(p, tile, tic));
+      dma_dy0 = cls_field(cw, kClsDy0);
+      dma_dx0 = cls_field(cw, kClsDx0);
+      dma_w0 = cls_field(cw, kClsW0);
+      dma_ny = cls_field(cw, kClsNy);
+      dma_nx = cls_field(cw, kClsNx);
+    } else {
+      dma_dy0 = p.dy0;
+      dma_dx0 = p.dx0;
+      dma_w0 = p.w0;
+      dma_ny = p.ny;
+      dma_nx = p.nx;
+    }
     const int tm = (int)fdiv((uint32_t)tic, p.divTN);
     const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
@@ -208,7 +237,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int ad = ((dma_dy0 + ty * p.dys) * p.Wi + dma_dx0 + tx * p.dxs) * p.C + c0;
     // a tap past the class's own grid has only zero A rows; its B rows come from the class's
     // first tap (a valid address; the products are zero)
-    const bool tap_ok = (ty < dma_ny) & (tx < dma_nx);
+    const bool tap_ok = !kClasses || ((ty < dma_ny) & (tx < dma_nx));
     const int wd = (tap_ok ? dma_w0 + ty * p.wys + tx * p.wxs : dma_w0) * p.C + c0;
 #pragma unroll
     for (int r = 0; r < kALoads; ++r) {
@@ -240,9 +269,12 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   auto epilogue = [&](int j) __attribute__((always_inline)) {
     const int item = t_begin + j * p.wg_per_xcd;
     const int tile = (int)fdiv((uint32_t)item, p.divSP);
-    int tic;
-    const int cls = tile_class(p, tile, tic);
-    const int oy_off = p.cls_oy[cls], ox_off = p.cls_ox[cls];
+    int tic = tile, oy_off = p.oy_off, ox_off = p.ox_off;
+    if constexpr (kClasses) {
+      const uint32_t cw = cls_word(p, tile_class(p, tile, tic));
+      oy_off = cls_field(cw, kClsOy);
+      ox_off = cls_field(cw, kClsOx);
+    }
     const int tm = (int)fdiv((uint32_t)tic, p.divTN);
     const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
@@ -443,12 +475,7 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   if (act_bytes > kMaxOperandBytes || wgt_bytes > kMaxOperandBytes || out_elems > kMaxOperandBytes)
     return DPA_ERR_SIZE;
   finish_geometry(a);
-  if (a.nclass <= 1) {  // one class: the scalar tap grid
-    a.nclass = 1;
-    a.cls_oy[0] = a.oy_off; a.cls_ox[0] = a.ox_off;
-    a.cls_dy0[0] = a.dy0; a.cls_dx0[0] = a.dx0; a.cls_w0[0] = a.w0;
-    a.cls_ny[0] = a.ny; a.cls_nx[0] = a.nx;
-  }
+  if (a.nclass <= 1) a.nclass = 1;  // one class: the scalar tap grid
   const int tiles_m = (int)ceil_div(a.M, kBM);
   a.tiles_pc = tiles_m * a.tiles_n;
   const int tiles = a.tiles_pc * a.nclass;
@@ -478,7 +505,10 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   a.divTN = make_fastdiv((uint32_t)a.tiles_n);
   a.divSP = make_fastdiv((uint32_t)a.splits);
   a.divPC = make_fastdiv((uint32_t)a.tiles_pc);
-  igemm_fp8_kernel<<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  if (a.nclass > 1)
+    igemm_fp8_kernel<true><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  else
+    igemm_fp8_kernel<false><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   int st = launch_status();
   if (st != DPA_OK || splits == 1) return st;
   igemm_split_reduce_kernel<<<(unsigned)(tiles * (kRedThreadsPerTile / 256)), 256, 0, s>>>(a);
@@ -604,9 +634,13 @@ static int dgrad_merged_geometry(IgemmArgs& a, int N, int H, int W, int Cin, int
       } else if (g.Pg != a.Pg || g.Qg != a.Qg) {
         return DPA_ERR_SHAPE;
       }
-      a.cls_oy[c] = g.oy_off; a.cls_ox[c] = g.ox_off;
-      a.cls_dy0[c] = g.dy0; a.cls_dx0[c] = g.dx0; a.cls_w0[c] = g.w0;
-      a.cls_ny[c] = g.ny; a.cls_nx[c] = g.nx;
+      const int f[7] = {g.oy_off, g.ox_off, g.dy0, g.dx0, g.w0, g.ny, g.nx};
+      uint32_t w = 0;
+      for (int i = 0; i < 7; ++i) {
+        if (f[i] < 0 || f[i] > 15) return DPA_ERR_SHAPE;
+        w |= (uint32_t)f[i] << (4 * i);
+      }
+      a.cls[c] = w;
       ny = g.ny > ny ? g.ny : ny;
       nx = g.nx > nx ? g.nx : nx;
     }
