@@ -193,6 +193,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_residual_scale_bwd_amax": (
         c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_float, c_void_p],
     ),
+    "dpa_conv3x3_thin_fwd": (
+        c_int, [c_void_p, c_int, c_void_p, c_int] + [c_int] * 4 + [c_void_p] + [c_int] * 5 + [c_void_p],
+    ),
+    "dpa_conv3x3_thin_dgrad": (
+        c_int, [c_void_p, c_void_p, c_int] + [c_int] * 4 + [c_void_p] + [c_int] * 5 + [c_void_p],
+    ),
+    "dpa_conv3x3_thin_wgrad_workspace_bytes": (c_int64, [c_int] * 5),
+    "dpa_conv3x3_thin_wgrad": (
+        c_int, [c_void_p, c_int, c_void_p, c_void_p] + [c_int] * 5 + [c_void_p, c_int64, c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -44,6 +44,7 @@ from .layer_norm import supported as ln_supported
 from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok, fp8_ok as gn_fp8_ok
 from .gn_silu import group_norm_silu, group_norm_silu_film, group_norm_silu_tee
 from .gn_silu import supported as gn_supported
+from .thinconv import ImageConv2d
 
 
 @dataclass
@@ -479,12 +480,13 @@ class Stage(nn.Module):
 
 
 class _OutHead(nn.Sequential):
-    """GroupNorm(32) + SiLU + 3x3 conv to image channels (diffusion/unet.py:306-310); the
+    """GroupNorm(32) + SiLU + 3x3 conv to image channels (diffusion/unet.py:325-329); the
     first two run as the fused kernel. Indices 0/1/2 keep the reference's state_dict keys."""
 
     def __init__(self, channs: int, out_channels: int, fused: bool):
         super().__init__(nn.GroupNorm(32, channs), nn.SiLU(),
-                         nn.Conv2d(channs, out_channels, kernel_size=(3, 3), padding=1, bias=False))
+                         ImageConv2d(channs, out_channels, kernel_size=(3, 3), padding=1,
+                                     bias=False))
         self.fused = fused
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -499,7 +501,8 @@ class UNet(nn.Module):
         self.config = config
         self.base_channs = config.base_hidden
         channs_1 = config.scales[0] * self.base_channs
-        self.conv_in = nn.Conv2d(config.in_channels, channs_1, kernel_size=(3, 3), padding=1, bias=False)
+        self.conv_in = ImageConv2d(config.in_channels, channs_1, kernel_size=(3, 3), padding=1,
+                                   bias=False)
 
         down_stages: deque = deque()
         up_stages: deque = deque()

@@ -677,6 +677,32 @@ int dpa_adamw_ema_step(const DpaOptTensor* tensors, int count, float* step, floa
                        float beta1, float beta2, float eps, float weight_decay, float max_norm,
                        float ema_beta, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * bf16 3x3 / stride-1 / pad-1 convolutions with an image-channel side: the U-Net's input conv
+ * (diffusion/unet.py:255-257, nn.Conv2d(3, C, 3, padding=1, bias=False)) and its output head's
+ * conv (:325-329, nn.Conv2d(C, 3, ...)), which the reference runs in bf16 under autocast
+ * (train.py:120, :136): bf16 operands, fp32 accumulation, bf16 output. One side has 1-3
+ * channels, the other 128 or 256; NHWC activations, W in {16, 32, 64}, H a multiple of
+ * 64 / W; the weight [Cout][Cin][3][3] fp32 or bf16 (w_dtype) at element strides ws0..ws3,
+ * rounded to bf16 on load. Other shapes return DPA_ERR_SHAPE. No counterpart entry in the
+ * reference (cuDNN through nn.Conv2d there).
+ * fwd: x bf16, or for a thin input fp32 (rounded to bf16 on load, as autocast's cast);
+ * y bf16 [N][H][W][Cout], 16-B aligned.
+ * dgrad: Cout <= 3 only (dy thin, bf16): dx bf16 [N][H][W][Cin].
+ * wgrad: dw fp32 [Cout][3][3][Cin] = fp32(bf16(sum over pixels)) -- the bf16 weight gradient
+ * cast back to the fp32 weight, as autocast's; partial sums per workgroup in the workspace
+ * (dpa_conv3x3_thin_wgrad_workspace_bytes), added in a fixed order: deterministic. */
+int dpa_conv3x3_thin_fwd(const void* x, int x_dtype, const void* w, int w_dtype, int ws0,
+                         int ws1, int ws2, int ws3, void* y, int N, int H, int W, int Cin,
+                         int Cout, void* stream);
+int dpa_conv3x3_thin_dgrad(const void* dy, const void* w, int w_dtype, int ws0, int ws1,
+                           int ws2, int ws3, void* dx, int N, int H, int W, int Cin, int Cout,
+                           void* stream);
+int64_t dpa_conv3x3_thin_wgrad_workspace_bytes(int N, int H, int W, int Cin, int Cout);
+int dpa_conv3x3_thin_wgrad(const void* x, int x_dtype, const void* dy, float* dw, int N, int H,
+                           int W, int Cin, int Cout, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif
