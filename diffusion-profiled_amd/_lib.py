@@ -109,6 +109,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "dpa_layernorm_fwd_ex": (c_int, [c_void_p, c_int] + [c_void_p] * 5 + [c_int64, c_int, c_float, c_void_p]),
     "dpa_layernorm_bwd_ex": (c_int, [c_void_p, c_int] + [c_void_p] * 8 + [c_int64, c_int64, c_int, c_void_p]),
+    "dpa_layernorm_bwd_ex_add": (
+        c_int, [c_void_p, c_int] + [c_void_p] * 9 + [c_int64, c_int64, c_int, c_void_p],
+    ),
     "dpa_attention_fwd_bf16": (c_int, [c_void_p] * 3 + [c_int] * 4 + [c_void_p]),
     "dpa_attention_bwd_bf16": (c_int, [c_void_p] * 5 + [c_int] * 4 + [c_void_p]),
     "dpa_attention_fwd_amax": (c_int, [c_void_p] * 3 + [c_int] * 4 + [c_void_p, c_void_p]),

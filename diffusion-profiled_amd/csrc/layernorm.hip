@@ -41,6 +41,7 @@ struct LnArgs {
   float* rstd;
   float* part;  // bwd: [blocks][2][C]
   uint32_t* amax_part;  // fwd, optional: per-workgroup max of |y| (bf16 magnitude bits)
+  const void* dx_add;   // bwd, optional: added to dx as it is stored (x's type)
   int64_t rows;
   int C;
   float eps;
@@ -232,14 +233,16 @@ __global__ __launch_bounds__(kLnThreads) void ln_bwd_kernel(const LnArgs p) {
   __shared__ float red[kLnWaves][2][64 * V];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = (int64_t)blockIdx.x * ln_rows_per_block<V>() + wave * R;
-  LnXRaw<V, kF32> rx[R];
+  LnXRaw<V, kF32> rx[R], ra[R];
   LnRaw<V> rd[R];
   float mus[R], rss[R];
+  const XT* padd = static_cast<const XT*>(p.dx_add);
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i < p.rows ? r0 + i : p.rows - 1;
     ln_load<V>(px + r * p.C, lane, rx[i]);
     ln_load<V>(p.dout + r * p.C, lane, rd[i]);
+    if (padd) ln_load<V>(padd + r * p.C, lane, ra[i]);
     mus[i] = p.mean[r];
     rss[i] = p.rstd[r];
   }
@@ -276,6 +279,17 @@ __global__ __launch_bounds__(kLnThreads) void ln_bwd_kernel(const LnArgs p) {
     const float m1 = wave_sum_f32(s1) * inv_c, m2 = wave_sum_f32(s2) * inv_c;
 #pragma unroll
     for (int k = 0; k < V; ++k) f[k] = rs * (d[k] - m1 - f[k] * m2);
+    if (padd) {
+      // the skip path's gradient of the same tensor, added as autograd adds two gradients in
+      // x's type: fp32 + fp32, or bf16(dx) + bf16 computed in fp32 and rounded once more
+      float ad[V];
+      ln_unpack<V>(ra[i], ad);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (!kF32) f[k] = bf16_bits_to_f32(f32_to_bf16_bits(f[k]));
+        f[k] = f[k] + ad[k];
+      }
+    }
     if (live) {
       us2 unused = {0, 0};
       ln_store<V>(static_cast<XT*>(p.out) + r * p.C, lane, f, unused);
@@ -443,14 +457,17 @@ extern "C" int64_t dpa_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
 
 static int ln_bwd(const void* x, bool f32, const void* dout, const float* gamma,
                   const float* mean, const float* rstd, void* dx, float* dgamma, float* dbeta,
-                  void* workspace, int64_t workspace_bytes, int64_t rows, int C, void* stream) {
+                  void* workspace, int64_t workspace_bytes, int64_t rows, int C, void* stream,
+                  const void* dx_add = nullptr) {
   if (!x || !dout || !gamma || !mean || !rstd || !dx || !dgamma || !dbeta) return DPA_ERR_NULL;
   if (!ln_shape_ok(rows, C)) return DPA_ERR_SHAPE;
   if (!workspace || workspace_bytes < dpa_layernorm_bwd_workspace_bytes(rows, C))
     return DPA_ERR_WORKSPACE;
-  if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4))
+  if (!aligned(x, 16) || !aligned(dout, 16) || !aligned(dx, 16) || !aligned(workspace, 4) ||
+      !aligned(dx_add, 16))
     return DPA_ERR_ALIGN;
   LnArgs a{};
+  a.dx_add = dx_add;
   a.x = x;
   a.dout = (const uint16_t*)dout;
   a.gamma = gamma;
@@ -485,4 +502,16 @@ extern "C" int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout
   if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
   return ln_bwd(x, x_dtype == DPA_DTYPE_F32, dout, gamma, mean, rstd, dx, dgamma, dbeta,
                 workspace, workspace_bytes, rows, C, stream);
+}
+
+extern "C" int dpa_layernorm_bwd_ex_add(const void* x, int x_dtype, const void* dout,
+                                        const float* gamma, const float* mean,
+                                        const float* rstd, const void* dx_add, void* dx,
+                                        float* dgamma, float* dbeta, void* workspace,
+                                        int64_t workspace_bytes, int64_t rows, int C,
+                                        void* stream) {
+  if (x_dtype != DPA_DTYPE_BF16 && x_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  if (!dx_add) return DPA_ERR_NULL;
+  return ln_bwd(x, x_dtype == DPA_DTYPE_F32, dout, gamma, mean, rstd, dx, dgamma, dbeta,
+                workspace, workspace_bytes, rows, C, stream, dx_add);
 }

@@ -78,5 +78,48 @@ class LayerNormBF16(torch.autograd.Function):
                 dbeta.to(ctx.param_dtypes[1]), None)
 
 
+class LayerNormTee(torch.autograd.Function):
+    """(bf16(LayerNorm(x)), x): the attention block's norm and its skip input
+    (diffusion/unet.py:182-187, :201: the block input feeds the LayerNorm and the residual
+    join). The backward adds the skip path's gradient of x into dx inside the LayerNorm kernel
+    (dpa_layernorm_bwd_ex_add) instead of autograd's separate accumulation kernel: the same
+    sum with the same roundings (fp32 + fp32, or bf16(dx) + bf16 rounded again)."""
+
+    @staticmethod
+    def forward(ctx: Any, x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float):
+        out = LayerNormBF16.forward(ctx, x, gamma, beta, eps)
+        return out, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx: Any, dout: torch.Tensor, dskip: torch.Tensor | None):
+        xb, g32, mean, rstd = ctx.saved_tensors
+        if dskip is None or dskip.dtype != xb.dtype or xb.dtype != ctx.x_dtype:
+            dx, dgamma, dbeta, _ = LayerNormBF16.backward(ctx, dout)
+            if dskip is not None:
+                dx = dx + dskip.to(dx.dtype)
+            return dx, dgamma, dbeta, None
+        c = xb.shape[-1]
+        rows = xb.numel() // c
+        dout = dout.to(torch.bfloat16).contiguous()
+        add = dskip.contiguous()
+        dx = torch.empty_like(xb)
+        dgamma = torch.empty(c, device=xb.device, dtype=torch.float32)
+        dbeta = torch.empty(c, device=xb.device, dtype=torch.float32)
+        ws_bytes = _lib.query("dpa_layernorm_bwd_workspace_bytes", rows, c)
+        ws = torch.empty(ws_bytes, device=xb.device, dtype=torch.uint8)
+        dt = DTYPE_F32 if xb.dtype == torch.float32 else DTYPE_BF16
+        _lib.call("dpa_layernorm_bwd_ex_add", xb.data_ptr(), dt, dout.data_ptr(),
+                  g32.data_ptr(), mean.data_ptr(), rstd.data_ptr(), add.data_ptr(),
+                  dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws_bytes,
+                  rows, c, _stream(xb))
+        return (dx, dgamma.to(ctx.param_dtypes[0]), dbeta.to(ctx.param_dtypes[1]), None)
+
+
 def layer_norm_bf16(x: torch.Tensor, norm: torch.nn.LayerNorm) -> torch.Tensor:
     return LayerNormBF16.apply(x, norm.weight, norm.bias, norm.eps)
+
+
+def layer_norm_tee(x: torch.Tensor, norm: torch.nn.LayerNorm):
+    """(bf16(norm(x)), x) with the skip gradient added inside the LayerNorm backward; x a
+    contiguous bf16 or fp32 token view."""
+    return LayerNormTee.apply(x, norm.weight, norm.bias, norm.eps)

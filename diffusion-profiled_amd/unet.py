@@ -38,7 +38,7 @@ from . import fp8_kernels as K
 from . import grouped as GR
 from .attention import self_attention_qkv
 from .attention import supported as attn_supported
-from .layer_norm import layer_norm_bf16
+from .layer_norm import layer_norm_bf16, layer_norm_tee
 from .residual import downsample2, join_fp8_ok, residual_join, upsample_concat
 from .layer_norm import supported as ln_supported
 from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok, fp8_ok as gn_fp8_ok
@@ -417,13 +417,21 @@ class CHWAttention(nn.Module):
     def reset_parameters(self):
         torch.nn.init.zeros_(self.out.weight)
 
+    # the skip path's gradient added inside the LayerNorm backward (LayerNormTee)
+    ln_tee = True
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         resid = x
         b, c, h, w = x.shape
         seq = x.permute(0, 2, 3, 1).reshape(b, h * w, c)           # b (h w) c
         if _on_gpu(x) and ln_supported(c):
             # the bf16 tokens in, the bf16 the qkv projection would round to out (fp32 stats)
-            seq = layer_norm_bf16(seq, self.norm)
+            if (self.ln_tee and seq.is_contiguous() and x.dtype in (torch.bfloat16, torch.float32)
+                    and seq.data_ptr() % 16 == 0):
+                seq, tokens = layer_norm_tee(seq, self.norm)
+                resid = tokens.reshape(b, h, w, c).permute(0, 3, 1, 2)
+            else:
+                seq = layer_norm_bf16(seq, self.norm)
         else:
             seq = self.norm(seq)
         qkv = self.qkv(seq)

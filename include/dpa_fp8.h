@@ -539,6 +539,14 @@ int dpa_layernorm_bwd_ex(const void* x, int x_dtype, const void* dout, const flo
                          const float* mean, const float* rstd, void* dx, float* dgamma,
                          float* dbeta, void* workspace, int64_t workspace_bytes, int64_t rows,
                          int C, void* stream);
+/* The backward with the gradient the attention block's skip path gives the same tokens
+ * (dx_add, x's dtype, 16-B aligned) added to dx as it is stored, as autograd adds the two
+ * gradients of the block input (diffusion/unet.py:182-187, :201: x feeds the LayerNorm and
+ * the residual join): fp32 + fp32, or bf16(dx) + dx_add in fp32 rounded to bf16. */
+int dpa_layernorm_bwd_ex_add(const void* x, int x_dtype, const void* dout, const float* gamma,
+                             const float* mean, const float* rstd, const void* dx_add, void* dx,
+                             float* dgamma, float* dbeta, void* workspace,
+                             int64_t workspace_bytes, int64_t rows, int C, void* stream);
 
 /* The forward also writing the per-workgroup maxima of |y| (bf16 magnitude bits) to
  * amax_partials (dpa_layernorm_fwd_partials(rows, C) entries; 0 for an unsupported shape),

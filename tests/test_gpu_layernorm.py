@@ -106,3 +106,54 @@ def test_layernorm_fp32_tokens_vs_float64(rows, c):
     assert rel(xd.grad.cpu().numpy(), xr.grad.numpy()) < 2e-5
     assert rel(gd.grad.cpu().numpy(), gr.grad.numpy()) < 1e-4
     assert rel(bd.grad.cpu().numpy(), br.grad.numpy()) < 1e-4
+
+
+@pytest.mark.parametrize("dtype,c,hw", [(torch.bfloat16, 256, 16), (torch.float32, 256, 8),
+                                        (torch.float32, 256, 4), (torch.bfloat16, 128, 16)])
+def test_attention_block_skip_gradient_add_in_layernorm(dtype, c, hw):
+    """The attention block with its input's skip gradient added inside the LayerNorm backward
+    (LayerNormTee, dpa_layernorm_bwd_ex_add) against the same block with autograd's separate
+    add: output, input gradient and every parameter gradient bit for bit, bf16 and fp32
+    block inputs (the fp32 residual stream of the lower levels)."""
+    U = dpa_mod("unet")
+    cfg = U.cfg5_config(p_drop=0.0)
+    torch.manual_seed(0)
+    blk = U.CHWAttention(cfg, c).cuda()
+    with torch.no_grad():                      # a non-zero out projection
+        blk.out.weight.normal_(0, 0.05)
+    g = torch.Generator().manual_seed(1)
+    x0 = torch.randn((8, c, hw, hw), generator=g).cuda().to(dtype)
+    x0 = x0.contiguous(memory_format=torch.channels_last)
+    gy = torch.randn((8, c, hw, hw), generator=g).cuda().to(dtype)
+    gy = gy.contiguous(memory_format=torch.channels_last)
+    L = dpa_mod("_lib")
+    real_call, calls = L.call, []
+
+    def counting(name, *args):
+        calls.append(name)
+        return real_call(name, *args)
+
+    res = {}
+    for tee in (True, False):
+        blk.ln_tee = tee
+        calls.clear()
+        for p in blk.parameters():
+            p.grad = None
+        x = x0.clone().requires_grad_()
+        L.call = counting
+        try:
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = blk(x)
+            y.backward(gy)
+            torch.cuda.synchronize()
+        finally:
+            L.call = real_call
+        assert calls.count("dpa_layernorm_bwd_ex_add") == (1 if tee else 0), calls
+        res[tee] = (y.detach(), x.grad, [p.grad.clone() for p in blk.parameters()])
+    blk.ln_tee = True
+    (ya, gxa, pa), (yb, gxb, pb) = res[True], res[False]
+    assert torch.equal(ya, yb)
+    assert gxa.dtype == gxb.dtype == dtype
+    assert torch.equal(gxa, gxb)
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b)
