@@ -142,6 +142,51 @@ __global__ __launch_bounds__(kOptThreads) void opt_update_kernel(
   const float coef = scalars[0], step_size = scalars[2], bc2_sqrt = scalars[3];
   const float decay = 1.0f - lr * weight_decay;
   const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2, ome = 1.0f - ema_beta;
+  if (i0 + kOptElems <= n) {
+    // a full block: every load first (nontemporal: each byte is touched once per step), then
+    // the updates, then the stores
+    constexpr int kIt = kOptElems / (kOptThreads * 4);
+    v4f P[kIt], G[kIt], M[kIt], V[kIt], E[kIt];
+    const int64_t b = i0 + threadIdx.x * 4;
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+      const int64_t i = b + k * kOptThreads * 4;
+      P[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p + i));
+      if (has_g) {
+        G[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g + i));
+        M[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(m + i));
+        V[k] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(v + i));
+      } else {
+        G[k] = M[k] = V[k] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      E[k] = e ? __builtin_nontemporal_load(reinterpret_cast<const v4f*>(e + i))
+               : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float pv = P[k][j], mv = M[k][j], vv = V[k][j], ev = E[k][j];
+        opt_elem(pv, G[k][j], mv, vv, e ? &ev : nullptr, has_g, coef, decay, beta1, omb1, beta2,
+                 omb2, step_size, bc2_sqrt, eps, ema_beta, ome);
+        P[k][j] = pv;
+        M[k][j] = mv;
+        V[k][j] = vv;
+        E[k][j] = ev;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+      const int64_t i = b + k * kOptThreads * 4;
+      if (has_g) {
+        __builtin_nontemporal_store(P[k], reinterpret_cast<v4f*>(p + i));
+        __builtin_nontemporal_store(M[k], reinterpret_cast<v4f*>(m + i));
+        __builtin_nontemporal_store(V[k], reinterpret_cast<v4f*>(v + i));
+      }
+      if (e) __builtin_nontemporal_store(E[k], reinterpret_cast<v4f*>(e + i));
+    }
+    return;
+  }
   for (int64_t i = i0 + threadIdx.x * 4; i < i0 + kOptElems && i < n; i += kOptThreads * 4) {
     if (i + 4 <= n) {
       float4 pv = *reinterpret_cast<float4*>(p + i);
