@@ -256,7 +256,11 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t 
 // 16-B-per-lane global -> LDS DMA (lane i lands at lds + 16 i). Issued through inline asm so
 // the compiler does not guard later LDS reads with conservative vmcnt(0) waits: all waits for
 // these DMAs are explicit in-order vmcnt counts in the kernels that issue them (in-order counting
-// keeps every compiler-inserted wait conservative, hence correct).
+// keeps every compiler-inserted wait conservative, hence correct). The asm sets m0 itself and
+// lists it as clobbered; clang warns that m0 is a reserved register whose value it may not
+// preserve around the statement. In the kernels built here nothing else uses m0 (in the
+// compiled igemm / hwgrad / wgrad code every m0 access is one of these s_mov / DMA pairs), so
+// no compiler-held value is live across it.
 __device__ __forceinline__ void dma16(const void* src, const void* lds) {
   const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(lds));
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "m0");
