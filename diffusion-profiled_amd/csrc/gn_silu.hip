@@ -1348,10 +1348,12 @@ static GnRes gn_res_shape(int HW) {
   if (HW <= kResMaxHW) return {64, 16};
   return {0, 0};
 }
-// The backward with an fp32 x holds 3 x 16 B per pixel: at 16 pixels per lane that exceeds the
-// register file, so images above 256 pixels take the chunked form.
-static bool gn_res_bwd_ok(int HW, bool x_f32) {
-  return HW <= kResMaxHW && (!x_f32 || HW <= 256);
+// The backward with an fp32 x holds 2 x 16 B of x per pixel in registers (dout goes to LDS at
+// 16 pixels per lane): that fits at 16 pixels per lane without FiLM and dropout (their
+// per-channel terms and keep bits are the registers that do not fit); with them, images
+// above 256 pixels take the chunked form.
+static bool gn_res_bwd_ok(int HW, bool x_f32, bool film, bool drop) {
+  return HW <= kResMaxHW && (!x_f32 || HW <= 256 || (!film && !drop));
 }
 
 static int gn_chunks(int HW) {
@@ -1660,7 +1662,8 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   hipStream_t s = (hipStream_t)stream;
   const int nchunk = gn_chunks(HW);
   const GnRes rs = gn_res_shape(HW);
-  const bool resident = gn_res_bwd_ok(HW, x_f32);
+  const bool resident =
+      gn_res_bwd_ok(HW, x_f32, film_scale || film_wb, drop_seed != nullptr);
   const bool chunked = !resident && nchunk > 0 && workspace_bytes >= gn_bwd_workspace(N, HW, C) &&
                        aligned(workspace, 16);
   if ((x_f32 || drop_seed || dx_add) && !chunked && !resident)
@@ -1702,7 +1705,7 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
         gn_res_bwd_kernel<32, 4, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
       else if (rs.u == 8)
         gn_res_bwd_kernel<32, 8, kF, k3, kD><<<grid, 8 * 32, 0, s>>>(a);
-      else if constexpr (!k3)  // an fp32 x above 256 pixels takes the chunked form
+      else if constexpr (!k3 || (!kF && !kD))  // (gn_res_bwd_ok)
         gn_res_bwd_kernel<64, 16, kF, k3, kD><<<grid, 8 * 64, 0, s>>>(a);
     });
   } else {

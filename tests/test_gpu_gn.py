@@ -236,8 +236,11 @@ def test_one_launch_and_chunked_forms_agree(G, n, c, h, w, film):
 
 
 F32_CASES = [
-    # fp32 inputs (the fp32 residual stream / decoder concatenations): chunked and small forms
+    # fp32 inputs (the fp32 residual stream / decoder concatenations): resident, chunked and
+    # small forms; 1024 pixels without FiLM (the decoder's first GroupNorm) is resident
     (2, 128, 32, 32, False),
+    (2, 512, 32, 32, False),
+    (2, 128, 32, 32, True),  # 1024 pixels with FiLM: chunked
     (2, 256, 16, 16, True),
     (2, 512, 8, 8, False),
     (3, 256, 4, 4, True),
