@@ -266,10 +266,10 @@ int dpa_gn_silu_fwd_ws_bf16(const void* x, const float* gamma, const float* beta
 
 /* Bytes of workspace dpa_gn_silu_bwd_bf16 needs: per-image channel partial sums (2*N*C fp32)
  * and, from 256 pixels, room for the chunk sums of the chunked backward (two launches like
- * the forward). The backward runs the resident form up to 1024 pixels (fp32 x: up to 256
- * pixels, since its 3 x 16 B per pixel exceed the register file at 16 pixels per lane), the
- * chunked form above that up to 8192 pixels with the full workspace, and the one-launch form
- * with a workspace of only 2*N*C floats. */
+ * the forward). The backward runs the resident form up to 1024 pixels (fp32 x with FiLM or
+ * dropout: up to 256 pixels, since x, the FiLM terms and the keep bits exceed the register
+ * file at 16 pixels per lane), the chunked form above that up to 8192 pixels with the full
+ * workspace, and the one-launch form with a workspace of only 2*N*C floats. */
 int64_t dpa_gn_silu_bwd_workspace_bytes(int N, int HW, int C, int G);
 
 /* Backward of dpa_gn_silu_fwd_bf16 given dout (bf16, same layout as out). Writes dx (bf16)
@@ -306,9 +306,9 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * in fp32 (nn.GroupNorm runs in float32, diffusion/unet.py:151, :157) and returns an fp32
  * input gradient; with DPA_DTYPE_F32 the kernels read the fp32 x as it is and write dx in
  * fp32 (the output y stays bf16). fp32 x takes the resident form (images of up to 1024
- * pixels; the backward up to 256) or the chunked form (above that, up to 8192 pixels, with a
- * workspace of the *_workspace_bytes size); larger images return DPA_ERR_SHAPE, a missing
- * workspace DPA_ERR_WORKSPACE.
+ * pixels; the backward with FiLM or dropout up to 256) or the chunked form (above that, up to
+ * 8192 pixels, with a workspace of the *_workspace_bytes size); larger images return
+ * DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE.
  * Optional dropout of the output (diffusion/unet.py:160, nn.Dropout(p) before conv_2):
  * drop_seed = a uint64 in device memory, NULL for none; an element is kept when its 32-bit
  * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
