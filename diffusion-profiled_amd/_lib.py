@@ -126,6 +126,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_upsample_concat_bwd_f32": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int] + [c_int] * 6 + [c_void_p]),
     "dpa_downsample2_f32": (c_int, [c_void_p, c_int, c_void_p] + [c_int] * 4 + [c_void_p]),
     "dpa_downsample2_bwd_f32": (c_int, [c_void_p, c_void_p, c_int] + [c_int] * 4 + [c_void_p]),
+    "dpa_downsample2_bwd_add_f32": (c_int, [c_void_p] * 3 + [c_int] * 5 + [c_void_p]),
     "dpa_mse_loss_workspace_bytes": (c_int64, []),
     "dpa_mse_loss_f32": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]),
     "dpa_adamw_ema_workspace_bytes": (c_int64, [c_void_p, c_int]),

@@ -251,6 +251,38 @@ __global__ __launch_bounds__(kEwThreads) void down2_bwd_kernel(const float* __re
   store4<TA>(ga + p * C + c, v);
 }
 
+// The same backward with the gradient that a's other reader (the decoder's concatenation)
+// sent added in: ga = a_dtype(gy or 0) + gskip, rounded as autograd's sum of the two
+// gradients (the downsampling's in a's dtype, then one add in a's dtype; every pixel gets the
+// add, so a -0 skip gradient beside a 0 becomes +0 as there). ga may alias gskip.
+template <typename TA>
+__global__ __launch_bounds__(kEwThreads) void down2_bwd_add_kernel(
+    const float* __restrict__ gy, const TA* gskip, TA* ga, int H, int W, int C, int64_t total4) {
+  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= total4) return;
+  const int c4 = C >> 2;
+  const int64_t p = i / c4;
+  const int c = (int)(i - p * c4) * 4;
+  const int64_t hw = (int64_t)H * W;
+  const int64_t n = p / hw;
+  const int r = (int)(p - n * hw);
+  const int yy = r / W, xx = r - yy * W;
+  float4 v = float4{0.f, 0.f, 0.f, 0.f};
+  if (((yy | xx) & 1) == 0) {
+    const int64_t q = (n * (H >> 1) + (yy >> 1)) * (W >> 1) + (xx >> 1);
+    v = *reinterpret_cast<const float4*>(gy + q * C + c);
+  }
+  const float4 s = load4f<TA>(gskip + p * C + c);
+  float4 o;
+  if constexpr (sizeof(TA) == 2) {  // bf16(bf16(v) + s)
+    o = float4{bf16_round(v.x) + s.x, bf16_round(v.y) + s.y, bf16_round(v.z) + s.z,
+               bf16_round(v.w) + s.w};
+  } else {
+    o = float4{v.x + s.x, v.y + s.y, v.z + s.z, v.w + s.w};
+  }
+  store4<TA>(ga + p * C + c, o);
+}
+
 }  // namespace dpa
 
 using namespace dpa;
@@ -468,5 +500,26 @@ extern "C" int dpa_residual_scale_bwd_fp8(const void* g, int g_dtype, void* ga, 
   else
     residual_bwd_q_kernel<false><<<(unsigned)nb, kEwThreads, 0, s>>>(
         g, ga, (uint8_t*)gbq, gb_scale, gb_partials, gb_count, n / 8, inv);
+  return launch_status();
+}
+
+extern "C" int dpa_downsample2_bwd_add_f32(const float* gy, const void* gskip, void* ga,
+                                           int a_dtype, int N, int H, int W, int C,
+                                           void* stream) {
+  const int af = a_dtype == DPA_DTYPE_F32;
+  if (!af && a_dtype != DPA_DTYPE_BF16) return DPA_ERR_SHAPE;
+  if (!gy || !gskip || !ga) return DPA_ERR_NULL;
+  if (N <= 0 || H <= 0 || W <= 0 || C <= 0 || C % 4) return DPA_ERR_SIZE;
+  if (H % 2 || W % 2) return DPA_ERR_SHAPE;
+  if (!aligned(ga, af ? 16 : 8) || !aligned(gskip, af ? 16 : 8) || !aligned(gy, 16))
+    return DPA_ERR_ALIGN;
+  const int64_t total4 = (int64_t)N * H * W * (C / 4);
+  const unsigned grid = (unsigned)ceil_div(total4, (int64_t)kEwThreads);
+  if (af)
+    down2_bwd_add_kernel<float><<<grid, kEwThreads, 0, (hipStream_t)stream>>>(
+        gy, (const float*)gskip, (float*)ga, H, W, C, total4);
+  else
+    down2_bwd_add_kernel<uint16_t><<<grid, kEwThreads, 0, (hipStream_t)stream>>>(
+        gy, (const uint16_t*)gskip, (uint16_t*)ga, H, W, C, total4);
   return launch_status();
 }

@@ -247,12 +247,54 @@ class Downsample2(torch.autograd.Function):
         return ga
 
 
-def downsample2(a: torch.Tensor) -> torch.Tensor:
-    """F.interpolate(a, scale_factor=0.5, mode="nearest") (fp32 under autocast)."""
-    if ((torch.is_autocast_enabled("cuda") or a.dtype == torch.float32) and a.is_cuda
+class Downsample2Tee(torch.autograd.Function):
+    """(downsample2(a), a): the encoder activation that feeds both the next level (through the
+    2x downsampling) and the decoder's concatenation (diffusion/unet.py:368-376). The backward
+    adds the concatenation's gradient of a inside the downsampling's backward
+    (dpa_downsample2_bwd_add_f32) instead of autograd's separate accumulation kernel: the same
+    sum with the same roundings."""
+
+    @staticmethod
+    def forward(ctx: Any, a: torch.Tensor):
+        y = Downsample2.forward(ctx, a)
+        return y, a.view_as(a)
+
+    @staticmethod
+    def backward(ctx: Any, gy: torch.Tensor | None, gskip: torch.Tensor | None):
+        shape, dtype = ctx.meta
+        if gy is None:
+            return gskip
+        if (gskip is None or gskip.dtype != dtype
+                or not gskip.is_contiguous(memory_format=torch.channels_last)
+                or gskip.data_ptr() % 16 != 0):
+            ga = Downsample2.backward(ctx, gy)
+            return ga if gskip is None else ga + gskip
+        gy = gy.float().contiguous(memory_format=torch.channels_last)
+        ga = torch.empty(shape, device=gy.device, dtype=dtype, memory_format=torch.channels_last)
+        n, c, h, w = shape
+        _lib.call("dpa_downsample2_bwd_add_f32", gy.data_ptr(), gskip.data_ptr(), ga.data_ptr(),
+                  _DT[dtype], n, h, w, c, _stream(gy))
+        return ga
+
+
+def _down_ok(a: torch.Tensor) -> bool:
+    return ((torch.is_autocast_enabled("cuda") or a.dtype == torch.float32) and a.is_cuda
             and a.dtype in _DT and a.ndim == 4 and a.shape[1] % 4 == 0
             and a.shape[2] % 2 == 0 and a.shape[3] % 2 == 0
-            and a.is_contiguous(memory_format=torch.channels_last) and a.data_ptr() % 16 == 0):
+            and a.is_contiguous(memory_format=torch.channels_last) and a.data_ptr() % 16 == 0)
+
+
+def downsample2(a: torch.Tensor) -> torch.Tensor:
+    """F.interpolate(a, scale_factor=0.5, mode="nearest") (fp32 under autocast)."""
+    if _down_ok(a):
         return Downsample2.apply(a)
     import torch.nn.functional as F
     return F.interpolate(a, scale_factor=0.5, mode="nearest")
+
+
+def downsample2_tee(a: torch.Tensor):
+    """(downsample2(a), a) with the second output's gradient added inside the downsampling's
+    backward (Downsample2Tee); elsewhere (a, the plain downsampling)."""
+    if _down_ok(a):
+        return Downsample2Tee.apply(a)
+    return downsample2(a), a

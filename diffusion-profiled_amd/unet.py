@@ -39,7 +39,8 @@ from . import grouped as GR
 from .attention import self_attention_qkv
 from .attention import supported as attn_supported
 from .layer_norm import layer_norm_bf16, layer_norm_tee
-from .residual import downsample2, join_fp8_ok, residual_join, upsample_concat
+from .residual import (downsample2, downsample2_tee, join_fp8_ok, residual_join,
+                       upsample_concat)
 from .layer_norm import supported as ln_supported
 from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok, fp8_ok as gn_fp8_ok
 from .gn_silu import group_norm_silu, group_norm_silu_film, group_norm_silu_tee
@@ -504,6 +505,9 @@ class _OutHead(nn.Sequential):
 class UNet(nn.Module):
     """diffusion/unet.py:245-388."""
 
+    # the encoder activations' two gradients summed inside the downsampling's backward
+    down_tee = True
+
     def __init__(self, config: UNetConfig):
         super().__init__()
         self.config = config
@@ -639,8 +643,15 @@ class UNet(nn.Module):
         act = self.conv_in(x)
         hs = []
         for i, stage in enumerate(self.down_stages):
-            # self.downsample(act): F.interpolate(scale 0.5, nearest), one pass on the GPU
-            act = stage(downsample2(act) if i > 0 else act, t_emb)
+            if i > 0:
+                # self.downsample(act): F.interpolate(scale 0.5, nearest), one pass on the GPU;
+                # the skip copy's gradient (from the decoder's concatenation) is added inside
+                # the downsampling's backward
+                if self.down_tee:
+                    act, hs[-1] = downsample2_tee(act)
+                else:
+                    act = downsample2(act)
+            act = stage(act, t_emb)
             hs.append(act)
         act = self.mid(act, t_emb)
         for i, stage in enumerate(self.up_stages):

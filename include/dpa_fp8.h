@@ -650,6 +650,13 @@ int dpa_downsample2_f32(const void* a, int a_dtype, float* y, int N, int H, int 
                         void* stream);
 int dpa_downsample2_bwd_f32(const float* gy, void* ga, int a_dtype, int N, int H, int W, int C,
                             void* stream);
+/* The backward when a has a second reader whose gradient gskip (a's dtype and shape) is
+ * ready (the encoder activation that the decoder's concatenation also reads,
+ * diffusion/unet.py:363-376): ga = a_dtype(gy at the sampled pixels, 0 elsewhere) + gskip, one
+ * add in a's dtype as autograd accumulates the two gradients; one pass instead of the
+ * backward plus autograd's add. ga may alias gskip. */
+int dpa_downsample2_bwd_add_f32(const float* gy, const void* gskip, void* ga, int a_dtype, int N,
+                                int H, int W, int C, void* stream);
 
 /* The training loss mean((pred - target)^2) of the DDPM step (diffusion/ddpm.py:209-215,
  * F.mse_loss with both operands in fp32 under autocast): pred bf16 or fp32 (DPA_DTYPE_*),

@@ -116,3 +116,45 @@ def test_downsample2_bit_exact(n, c, h, w, a32):
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     assert a1.grad.dtype == a.dtype and torch.equal(a1.grad, a2.grad)
+
+
+@pytest.mark.parametrize("n,c,h,w,a32", [(4, 128, 32, 32, False), (4, 256, 16, 16, True),
+                                         (3, 256, 8, 8, True), (2, 64, 6, 10, False)])
+def test_downsample2_tee_equals_autograd_sum(n, c, h, w, a32):
+    """An activation read by the downsampling and by a second consumer (the decoder's
+    concatenation, diffusion/unet.py:368-376): the tee's input gradient, summed inside the
+    downsampling's backward, equals interpolate + autograd's accumulation bit for bit,
+    including the sign of zero where the second gradient is -0."""
+    g = torch.Generator().manual_seed(3 * n + c + h + w)
+    a = (torch.randn((n, c, h, w), generator=g) * 2).cuda()
+    a = a.to(torch.float32 if a32 else torch.bfloat16).contiguous(memory_format=torch.channels_last)
+    gy = (torch.randn((n, c, h // 2, w // 2), generator=g) * 1e-2).cuda().contiguous(
+        memory_format=torch.channels_last)
+    gs = (torch.randn((n, c, h, w), generator=g) * 1e-2).cuda().to(a.dtype)
+    gs[0, 0] = -0.0  # -0 beside the downsampling's +0 off the sampled pixels
+    gs = gs.contiguous(memory_format=torch.channels_last)
+    a1, a2 = a.clone().requires_grad_(), a.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y1, s1 = R.downsample2_tee(a1)
+        y2 = torch.nn.functional.interpolate(a2, scale_factor=0.5, mode="nearest")
+        s2 = a2
+    assert y1.dtype == y2.dtype == torch.float32 and torch.equal(y1, y2)
+    assert torch.equal(s1, a)
+    torch.autograd.backward([y1, s1], [gy, gs])
+    torch.autograd.backward([y2, s2], [gy, gs])
+    torch.cuda.synchronize()
+    assert a1.grad.dtype == a.dtype
+    b1 = a1.grad.view(torch.int16 if a.dtype == torch.bfloat16 else torch.int32)
+    b2 = a2.grad.view(torch.int16 if a.dtype == torch.bfloat16 else torch.int32)
+    assert torch.equal(b1, b2)
+    # only the downsampling's gradient (the skip copy unused): the plain backward
+    a3 = a.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y3, _ = R.downsample2_tee(a3)
+    y3.backward(gy)
+    a4 = a.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y4 = R.downsample2(a4)
+    y4.backward(gy)
+    torch.cuda.synchronize()
+    assert torch.equal(a3.grad, a4.grad)

@@ -271,6 +271,37 @@ def _fp8_site_active(m, x) -> bool:
     return m.fp8 and K.linear_fp8_supported(m.in_features, m.out_features)
 
 
+def test_unet_fused_gradient_sums_equal_autograd():
+    """The skip-gradient sums fused into kernels (the encoder activations' two gradients
+    inside the downsampling's backward, the attention block input's inside the LayerNorm
+    backward) change no bit of the U-Net's gradients: cfg5's model at batch 2 (current
+    scaling, dropout off), forward + backward under autocast with the fused sums and with
+    autograd's own accumulation."""
+    torch.manual_seed(5)
+    model = _nonzero_init(U.UNet(_cfg())).to(memory_format=torch.channels_last).cuda()
+    g = torch.Generator().manual_seed(6)
+    x = (torch.rand((2, 3, 32, 32), generator=g) * 2 - 1).cuda().contiguous(
+        memory_format=torch.channels_last)
+    t = torch.randint(0, 1000, (2,), generator=g).cuda()
+    gy = torch.randn((2, 3, 32, 32), generator=g).cuda().contiguous(
+        memory_format=torch.channels_last)
+    grads = []
+    for fused in (True, False):
+        model.down_tee = fused
+        for m in model.modules():
+            if isinstance(m, U.CHWAttention):
+                m.ln_tee = fused
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = model(x, t)
+        y.float().backward(gy)
+        grads.append({n: p.grad.clone() for n, p in model.named_parameters() if p.grad is not None})
+    torch.cuda.synchronize()
+    assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 100
+    for n in grads[0]:
+        assert torch.equal(grads[0][n], grads[1][n]), n
+
+
 def test_unet_forward_backward_vs_fakequant_emulation():
     """cfg5's U-Net (current scaling, dropout off) at batch 2, one forward+backward under
     autocast: every FP8 site (registry and general 3x3 convs, 1x1 skips, linears) is checked
