@@ -8,8 +8,11 @@ Conv2dFP8Specialized does per layer in the reference (diffusion/fp8_kernels.py:8
     python bench.py [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3|cfg3s2|cfg3k1|cfg4|cfg5]
 
 Prints ONE JSON line. `value` is TFLOP/s of algorithmic conv work (3 x 2*M*N*K per step)
-with inputs resident in HBM; the step is captured once as a HIP graph and replayed K times
-(wall clock around the replays, synchronised on both sides). `roofline` is for the dominant
+with inputs resident in HBM; ten steps are captured back to back as one HIP graph
+(--steps-per-graph) and exactly K steps are replayed (whole graphs, then a one-step graph for
+any remainder; wall clock around the replays, synchronised on both sides). A replay boundary
+costs ~4-7 µs that a conv inside a captured training step does not pay; the time with one
+step per replay is reported beside it (`ms_per_step_one_step_graphs`). `roofline` is for the dominant
 kernel: HIP events around a graph replay of many calls, recorded on the replay stream (the
 stream every kernel of the library is launched on). `cpu_baseline` times the
 oracle's CPU path (the reference recipe on torch CPU: e4m3 round trip + fp32 conv) on a
@@ -45,6 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps-per-graph", type=int, default=10,
+                    help="cfg1-cfg3: steps captured back to back in one HIP graph (the timed "
+                         "steps are exactly --steps: whole graphs, then single-step replays)")
     ap.add_argument("--workload", default="cfg2",
                     choices=["cfg2", "cfg1", "cfg3", "cfg3s2", "cfg3k1", "cfg4", "cfg5", "gn32",
                              "attn256"],
@@ -714,16 +720,30 @@ def main():
     for name, fn in wl.parts().items():
         parts[name] = time_part(fn, args.kernel_reps)
 
-    # the step as one HIP graph (one replay = one step), timed over K replays
-    g = capture(wl.step, 1)
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        g.replay()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
+    # the step as HIP graphs: g holds `per` steps back to back (one replay launches them with
+    # no host work and no graph boundary in between, as the conv runs inside a captured
+    # training step), g1 one step; exactly args.steps steps are timed (whole g replays, then g1
+    # replays for the remainder). The one-step-per-replay time is reported beside it.
+    per = max(1, min(args.steps_per_graph, args.steps))
+    g = capture(wl.step, per)
+    g1 = capture(wl.step, 1)
+
+    def run_steps(k):
+        for _ in range(k // per):
+            g.replay()
+        for _ in range(k % per):
+            g1.replay()
+
+    def timed(fn, k):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn(k)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / k
+
+    run_steps(args.warmup)
+    dt = timed(run_steps, args.steps)
+    dt1 = timed(lambda k: [g1.replay() for _ in range(k)], args.steps)
 
     tflops = wl.step_flop() / dt / 1e12
     # dominant kernel = the MFMA kernel with the most device time per step: the conv kernel
@@ -771,17 +791,18 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 4),
+        "ms_per_step_one_step_graphs": round(dt1 * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8e4m3 (fp32 accumulate, bf16 out)",
         "data": "synthetic (seeded N(0,1) activations, Kaiming-uniform weights, N(0,1e-2) grad_out)",
-        "config": wl.config(),
+        "config": dict(wl.config(), steps_per_graph=per),
         "roofline": roofline,
         "kernels": kernels,
     }
     if args.workload == "cfg2" and not args.no_unet:
-        del g
+        del g, g1
         _, _, out["unet_train_step"] = unet_step_summary(20, 3)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
