@@ -46,6 +46,28 @@ constexpr int kBRowsPerWave = kBN / kWaves;           // 16
 constexpr int kSlotBytes = 16 * kWTN * 2;             // 16 pixels x 64 channels of bf16
 constexpr int kMaxTapDim = 3;
 
+// Tile shape of an igemm_fp8_kernel instance: BM output pixels x kBN channels, the 8 waves as
+// (BM / 64) x (8 / (BM / 64)) wave tiles of 64 pixels x kWTN channels. BM = 256 is the default;
+// BM = 128 (64 x 32 wave tiles, 32 KB stages) gives launches with few output pixels twice the
+// tiles, so they fill the CUs without splitting K.
+template <int BM>
+struct IgCfg {
+  static constexpr int kBM = BM;
+  static constexpr int kWavesM = BM / kWTM;
+  static constexpr int kWTN = kBN / (kWaves / kWavesM);
+  static constexpr int kCB = kWTN / 16;  // 16-channel MFMA blocks per wave
+  static constexpr int kStageBytes = (BM + kBN) * kBK;
+  static constexpr int kALoads = BM * kBK / 16 / kIgThreads;
+  static constexpr int kBLoads = kBN * kBK / 16 / kIgThreads;
+  static constexpr int kLoadsPerStage = kALoads + kBLoads;
+  static constexpr int kARowsPerWave = BM / kWaves;
+  static constexpr int kBRowsPerWave = kBN / kWaves;
+  static constexpr int kSlotG = kWTN / 8;                 // 16-B granules per slot row
+  static constexpr int kSlotBytes = 16 * kSlotG * 16;      // 16 pixels x kWTN channels, bf16
+};
+static_assert(IgCfg<256>::kWTN == kWTN && IgCfg<256>::kLoadsPerStage == kLoadsPerStage &&
+                  IgCfg<256>::kSlotBytes == kSlotBytes, "the default tile");
+
 struct IgemmArgs {
   const uint8_t* act;  // [N][Hi][Wi][C]
   const uint8_t* wgt;  // [Cout][T][C]
@@ -80,9 +102,6 @@ struct IgemmArgs {
 __device__ __attribute__((aligned(64))) uint8_t g_zero16[64];
 constexpr int64_t kMaxOperandBytes = 0x7fffffff;  // 32-bit offsets
 
-// Three pipeline stages and the per-wave epilogue slots: 3 x 48 KB + 8 x 2 KB = 160 KB.
-__shared__ __attribute__((aligned(1024))) uint8_t ig_st[3][kStageBytes];
-__shared__ __attribute__((aligned(1024))) uint8_t ig_slot[kWaves][kSlotBytes];
 
 // LDS rows are 128 B = 8 granules of 16 B; granule g of row r lives at (g ^ swz(r)). Measured
 // on gfx950 (SQ_LDS_BANK_CONFLICT): this swizzle makes the 16-row, one-granule fragment
@@ -138,8 +157,19 @@ __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
 // kClasses: the launch holds several output parity classes (p.nclass > 1). The one-class
 // instance reads the scalar tap grid only: the class tables would take SGPRs the main loop
 // needs (with them it reloads kernel arguments inside the loop, ~1 us per launch).
-template <bool kClasses>
+template <bool kClasses, int BM = 256>
 __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArgs p) {
+  // this instance's tile (IgCfg); the names shadow the default tile's constants
+  using Cfg = IgCfg<BM>;
+  constexpr int kBM = Cfg::kBM, kWavesM = Cfg::kWavesM, kWTN = Cfg::kWTN, kCB = Cfg::kCB;
+  constexpr int kALoads = Cfg::kALoads, kBLoads = Cfg::kBLoads;
+  constexpr int kLoadsPerStage = Cfg::kLoadsPerStage;
+  constexpr int kARowsPerWave = Cfg::kARowsPerWave, kBRowsPerWave = Cfg::kBRowsPerWave;
+  constexpr int kSlotG = Cfg::kSlotG;
+  // three pipeline stages and the per-wave epilogue slots: 3 x 48 KB + 8 x 2 KB = 160 KB
+  // (BM = 256), 3 x 32 KB + 8 x 1 KB (BM = 128)
+  __shared__ __attribute__((aligned(1024))) uint8_t ig_st[3][Cfg::kStageBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t ig_slot[kWaves][Cfg::kSlotBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -255,12 +285,12 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   };
 
   // ---- compute side ----
-  v4f acc[4][4];
+  v4f acc[kCB][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kCB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  v8i fa[4], fb[4];
+  v8i fa[4], fb[kCB];
 
   // finished item j: scale, bias, bf16 -> wave slot -> 128-B runs per pixel; or, with
   // split K, the raw fp32 sums of its K range as the accumulators hold them: item i's
@@ -279,7 +309,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int c0 = n0 + wn * kWTN;
-    if (p.splits > 1) {
+    if (BM == 256 && p.splits > 1) {  // (launch_igemm splits the default tile only)
       float* part = p.partial + (int64_t)item * (kBM * kBN) + wave * (16 * 256) + lane * 4;
 #pragma unroll
       for (int pj = 0; pj < 4; ++pj) {
@@ -295,7 +325,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
 #pragma unroll
     for (int pj = 0; pj < 4; ++pj) {
 #pragma unroll
-      for (int ci = 0; ci < 4; ++ci) {
+      for (int ci = 0; ci < kCB; ++ci) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[ci][pj][e] * scale;
@@ -307,19 +337,21 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
         uint2 o;
         o.x = pack_bf16x2(v[0], v[1]);
         o.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(slot + frow * 128 + ((g ^ (frow & 7)) * 16) + (fq & 1) * 8) = o;
+        *reinterpret_cast<uint2*>(slot + frow * (16 * kSlotG) +
+                                  ((g ^ (frow & (kSlotG - 1))) * 16) + (fq & 1) * 8) = o;
       }
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < kSlotG / 4; ++rr) {
         const int c = lane + 64 * rr;
-        const int r = c >> 3, g = c & 7;
-        const uint4 v = *reinterpret_cast<const uint4*>(slot + r * 128 + ((g ^ (r & 7)) * 16));
+        const int r = c / kSlotG, g = c % kSlotG;
+        const uint4 v = *reinterpret_cast<const uint4*>(slot + r * (16 * kSlotG) +
+                                                        ((g ^ (r & (kSlotG - 1))) * 16));
         const int m = m0 + wm * kWTM + pj * 16 + r;
         if (m < p.M) st_nt16(p.out + out_offset(p, m, oy_off, ox_off) + c0 + g * 8, v);
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kCB; ++i)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
   };
@@ -330,7 +362,7 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   wait_vmcnt<2 * kLoadsPerStage>();
   lds_barrier();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fb[i] = ld_frag(ig_st[0] + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
+  for (int i = 0; i < kCB; ++i) fb[i] = ld_frag(ig_st[0] + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
 #pragma unroll
   for (int i = 0; i < 4; ++i) fa[i] = ld_frag(ig_st[0], wm * kWTM + i * 16 + frow, fq);
 
@@ -348,14 +380,14 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
 #pragma unroll
     for (int pj = 0; pj < 4; ++pj) {
 #pragma unroll
-      for (int ci = 0; ci < 4; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
+      for (int ci = 0; ci < kCB; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
       fa[pj] = ld_frag(nxt, wm * kWTM + pj * 16 + frow, fq);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x008, kCB, 0);  // kCB MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // then 2 DS reads
     }
     issue(ig_st[cur], s + 3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fb[i] = ld_frag(nxt + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
+    for (int i = 0; i < kCB; ++i) fb[i] = ld_frag(nxt + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
     if (++kstep == nk) {
       kstep = 0;
       epilogue((int)fdiv((uint32_t)s, p.divNK));
@@ -449,6 +481,8 @@ static int plan_splits(int tiles, int nk, int cus, int64_t* bytes) {
   return best;
 }
 
+constexpr int kHalfMaxSteps = 18;  // two 128-channel chunks of a 3x3 conv
+
 static void finish_geometry(IgemmArgs& a) {
   a.kc_per_tap = a.C / kBK;
   a.nk = a.ny * a.nx * a.kc_per_tap;
@@ -476,11 +510,15 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
     return DPA_ERR_SIZE;
   finish_geometry(a);
   if (a.nclass <= 1) a.nclass = 1;  // one class: the scalar tap grid
-  const int tiles_m = (int)ceil_div(a.M, kBM);
+  // Launches whose 256-pixel tiles would leave at least half the CUs idle take 128-pixel
+  // tiles (twice as many) unsplit, when a tile has at most kHalfMaxSteps K-steps.
+  const bool half = a.nclass == 1 && a.nk <= kHalfMaxSteps &&
+                    ceil_div(a.M, kBM) * a.tiles_n * 2 <= num_cus();
+  const int tiles_m = (int)ceil_div(a.M, half ? 128 : kBM);
   a.tiles_pc = tiles_m * a.tiles_n;
   const int tiles = a.tiles_pc * a.nclass;
   int64_t need = 0;
-  int splits = plan_splits(tiles, a.nk, num_cus(), &need);
+  int splits = half ? 1 : plan_splits(tiles, a.nk, num_cus(), &need);
   // the split reduce writes class 0's pixels only: several classes run unsplit
   if (splits > 1 && (a.nclass > 1 || !workspace || workspace_bytes < need ||
                      !aligned(workspace, 16)))
@@ -507,6 +545,8 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   a.divPC = make_fastdiv((uint32_t)a.tiles_pc);
   if (a.nclass > 1)
     igemm_fp8_kernel<true><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  else if (half)
+    igemm_fp8_kernel<false, 128><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   else
     igemm_fp8_kernel<false><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   int st = launch_status();
