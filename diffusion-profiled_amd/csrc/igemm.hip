@@ -13,7 +13,8 @@
 // class touches; the linear is the 1x1 case with H = W = 1.
 //
 // Schedule: persistent. One workgroup of 8 waves (4 x 2, two per SIMD) per CU walks its
-// output tiles of 256 pixels x 128 channels (a contiguous run per XCD, so neighbouring
+// output tiles of 256 pixels x 128 channels (128 or 64 pixels for launches with few output
+// pixels, IgCfg; a contiguous run per XCD, so neighbouring
 // tiles share halo rows in that XCD's L2) as one continuous stream of K-steps (128 input
 // channels of one tap per step). Operands reach LDS by DMA (global_load_lds, 16 B per lane)
 // through a 3-stage ring, issued three steps ahead, also across tile boundaries. Each wave
@@ -48,8 +49,9 @@ constexpr int kMaxTapDim = 3;
 
 // Tile shape of an igemm_fp8_kernel instance: BM output pixels x kBN channels, the 8 waves as
 // (BM / 64) x (8 / (BM / 64)) wave tiles of 64 pixels x kWTN channels. BM = 256 is the default;
-// BM = 128 (64 x 32 wave tiles, 32 KB stages) gives launches with few output pixels twice the
-// tiles, so they fill the CUs without splitting K.
+// BM = 128 (64 x 32 wave tiles, 32 KB stages) and BM = 64 (64 x 16, 24 KB stages) give
+// launches with few output pixels two or four times the tiles, so they fill the CUs without
+// splitting K.
 template <int BM>
 struct IgCfg {
   static constexpr int kBM = BM;
@@ -340,14 +342,17 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
         *reinterpret_cast<uint2*>(slot + frow * (16 * kSlotG) +
                                   ((g ^ (frow & (kSlotG - 1))) * 16) + (fq & 1) * 8) = o;
       }
+      // the slot's 16 x kSlotG 16-B chunks, one per lane and pass
 #pragma unroll
-      for (int rr = 0; rr < kSlotG / 4; ++rr) {
+      for (int rr = 0; rr < (16 * kSlotG + 63) / 64; ++rr) {
         const int c = lane + 64 * rr;
         const int r = c / kSlotG, g = c % kSlotG;
-        const uint4 v = *reinterpret_cast<const uint4*>(slot + r * (16 * kSlotG) +
-                                                        ((g ^ (r & (kSlotG - 1))) * 16));
-        const int m = m0 + wm * kWTM + pj * 16 + r;
-        if (m < p.M) st_nt16(p.out + out_offset(p, m, oy_off, ox_off) + c0 + g * 8, v);
+        if (16 * kSlotG >= 64 || c < 16 * kSlotG) {
+          const uint4 v = *reinterpret_cast<const uint4*>(slot + r * (16 * kSlotG) +
+                                                          ((g ^ (r & (kSlotG - 1))) * 16));
+          const int m = m0 + wm * kWTM + pj * 16 + r;
+          if (m < p.M) st_nt16(p.out + out_offset(p, m, oy_off, ox_off) + c0 + g * 8, v);
+        }
       }
     }
 #pragma unroll
@@ -481,7 +486,11 @@ static int plan_splits(int tiles, int nk, int cus, int64_t* bytes) {
   return best;
 }
 
+// Small-tile choice (launch_igemm), measured on the U-Net's 8x8 / 4x4 convs and the stride-2
+// conv: 64-pixel tiles win wherever 128-pixel ones would fill at most half the CUs; allowing
+// 36 K-steps per unsplit tile (the 512-channel 4x4 convs) instead of 18 changed nothing.
 constexpr int kHalfMaxSteps = 18;  // two 128-channel chunks of a 3x3 conv
+constexpr int kQuarterFill = 2;
 
 static void finish_geometry(IgemmArgs& a) {
   a.kc_per_tap = a.C / kBK;
@@ -511,10 +520,16 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   finish_geometry(a);
   if (a.nclass <= 1) a.nclass = 1;  // one class: the scalar tap grid
   // Launches whose 256-pixel tiles would leave at least half the CUs idle take 128-pixel
-  // tiles (twice as many) unsplit, when a tile has at most kHalfMaxSteps K-steps.
-  const bool half = a.nclass == 1 && a.nk <= kHalfMaxSteps &&
-                    ceil_div(a.M, kBM) * a.tiles_n * 2 <= num_cus();
-  const int tiles_m = (int)ceil_div(a.M, half ? 128 : kBM);
+  // tiles (twice as many) unsplit, when a tile has at most kHalfMaxSteps K-steps, and
+  // 64-pixel tiles when the 128-pixel ones would still leave half the CUs idle.
+  int bm = kBM;
+  if (a.nclass == 1 && a.nk <= kHalfMaxSteps) {
+    const int cus = num_cus();
+    if (ceil_div(a.M, 256) * a.tiles_n * 2 <= cus) bm = 128;
+    if (bm == 128 && ceil_div(a.M, 128) * a.tiles_n * kQuarterFill <= cus) bm = 64;
+  }
+  const bool half = bm < kBM;
+  const int tiles_m = (int)ceil_div(a.M, bm);
   a.tiles_pc = tiles_m * a.tiles_n;
   const int tiles = a.tiles_pc * a.nclass;
   int64_t need = 0;
@@ -545,8 +560,10 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   a.divPC = make_fastdiv((uint32_t)a.tiles_pc);
   if (a.nclass > 1)
     igemm_fp8_kernel<true><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
-  else if (half)
+  else if (bm == 128)
     igemm_fp8_kernel<false, 128><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  else if (bm == 64)
+    igemm_fp8_kernel<false, 64><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   else
     igemm_fp8_kernel<false><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   int st = launch_status();
