@@ -46,7 +46,7 @@ struct GnArgs {
   const uint16_t* wb;  // or FiLM from the bf16 time projection [N][2C]: scale bf16(w + 1), shift b
   uint16_t* dwb;       // bwd: its gradient [N][2C] bf16, or null
   const uint64_t* drop_seed;  // dropout after the SiLU: seed in device memory, or null
-  uint32_t drop_keep;         // keep an element when its hash is >= this (p * 2^32)
+  uint32_t drop_keep;         // keep an element when its 16-bit hash is >= this (p * 2^16)
   float drop_scale;           // RN32(1 / (1 - p))
   const void* dx_add;  // bwd: a gradient added to dx (chunked and small forms), or null
   int dx_add_bf16;     // bwd: dx_add is bf16 while x and dx are fp32
@@ -67,21 +67,27 @@ struct GnArgs {
 // keep decision of element idx (NHWC index) is a counter hash of (seed, idx), so the backward
 // recomputes the mask instead of storing it; kept values are scaled by 1 / (1 - p) in fp32
 // before the bf16 rounding, as the reference drops its fp32 SiLU output before the conv's
-// bf16 cast. The hash: splitmix64 of seed + (idx / 2) * golden ratio, one output per pair of
-// elements, its low 32 bits deciding the even element and its high 32 bits the odd one.
+// bf16 cast. The hash: splitmix64 of seed + (idx / 4) * golden ratio, one output per four
+// elements: element idx is kept when bits [16 (idx % 4), 16 (idx % 4) + 16) of its hash, as
+// a 16-bit number, are >= floor(p * 2^16). Four elements per 64-bit hash halve the hash's vector
+// instructions against one per pair (its multiplies are done in 32-bit halves); 16 bits
+// still give a drop rate within 2^-16 of p.
 // Returns the keep bits of the 8 elements idx0 .. idx0 + 7 (idx0 a multiple of 8).
 __device__ __forceinline__ uint32_t drop_keep8(uint64_t seed, int64_t idx0, uint32_t keep_from) {
   constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
-  const uint64_t z0 = seed + (uint64_t)(idx0 >> 1) * kGolden;
+  const uint64_t z0 = seed + (uint64_t)(idx0 >> 2) * kGolden;
   uint32_t bits = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     uint64_t z = z0 + (uint64_t)i * kGolden;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
     z ^= z >> 31;
-    bits |= (uint32_t)((uint32_t)z >= keep_from) << (2 * i);
-    bits |= (uint32_t)((uint32_t)(z >> 32) >= keep_from) << (2 * i + 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t r = (uint32_t)(z >> (16 * j)) & 0xffffu;
+      bits |= (uint32_t)(r >= keep_from) << (4 * i + j);
+    }
   }
   return bits;
 }
@@ -462,14 +468,15 @@ __global__ __launch_bounds__(8 * PLN) void gn_silu_bwd_kernel(const GnArgs p) {
   });
 }
 
-// dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c], summed in image order
-// within each of 4 interleaved slices, then over the slices (deterministic). One workgroup
-// per 64 channels: 64 channel lanes x 4 image slices.
-__global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __restrict__ part,
-                                                              float* __restrict__ dgamma,
-                                                              float* __restrict__ dbeta, int N,
-                                                              int C) {
-  __shared__ float red[2][4][64];
+// dgamma[c] = sum_n part[0][n][c], dbeta[c] = sum_n part[1][n][c]: 16 interleaved image
+// slices (slice s sums images s, s + 16, ... in order, all its loads in flight at once), then
+// a fixed pairwise tree over the slices (deterministic). One workgroup per 64 channels:
+// 64 channel lanes x 16 image slices.
+constexpr int kPrSlices = 16;
+__global__ __launch_bounds__(64 * kPrSlices) void gn_param_reduce_kernel(
+    const float* __restrict__ part, float* __restrict__ dgamma, float* __restrict__ dbeta, int N,
+    int C) {
+  __shared__ float red[2][kPrSlices][64];
   const int lane = threadIdx.x & 63;
   const int slice = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
@@ -477,7 +484,7 @@ __global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __res
   float sg = 0.f, sb = 0.f;
   if (c < C) {
 #pragma unroll 8
-    for (int n = slice; n < N; n += 4) {
+    for (int n = slice; n < N; n += kPrSlices) {
       sg += part[(int64_t)n * C + c];
       sb += part[nc + (int64_t)n * C + c];
     }
@@ -485,9 +492,15 @@ __global__ __launch_bounds__(256) void gn_param_reduce_kernel(const float* __res
   red[0][slice][lane] = sg;
   red[1][slice][lane] = sb;
   __syncthreads();
-  if (slice == 0 && c < C) {
-    dgamma[c] = (red[0][0][lane] + red[0][1][lane]) + (red[0][2][lane] + red[0][3][lane]);
-    dbeta[c] = (red[1][0][lane] + red[1][1][lane]) + (red[1][2][lane] + red[1][3][lane]);
+  if (slice < 2 && c < C) {
+    float v[kPrSlices];
+#pragma unroll
+    for (int i = 0; i < kPrSlices; ++i) v[i] = red[slice][i][lane];
+#pragma unroll
+    for (int w = kPrSlices / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int i = 0; i < w; ++i) v[i] = v[i] + v[i + w];
+    (slice == 0 ? dgamma : dbeta)[c] = v[0];
   }
 }
 
@@ -1435,15 +1448,15 @@ static int64_t gn_fwd_workspace(int N, int HW, int G) {
   return (int64_t)N * gn_chunks(HW) * G * (int64_t)sizeof(float2);
 }
 
-// Dropout arguments: keep when the hash is >= p * 2^32; scale 1 / (1 - p) rounded as torch's
-// dropout forms it (1 - p in double, rounded to fp32, its reciprocal rounded to fp32).
+// Dropout arguments: keep when the 16-bit hash is >= floor(p * 2^16) (p < 1: at most 65535);
+// scale 1 / (1 - p) rounded as torch's dropout forms it (1 - p in double, rounded to fp32, its
+// reciprocal rounded to fp32).
 static int gn_set_dropout(GnArgs& a, const void* seed, float p) {
   if (!seed) return DPA_OK;
   if (!(p >= 0.0f && p < 1.0f)) return DPA_ERR_SIZE;
   if (!aligned(seed, 8)) return DPA_ERR_ALIGN;
   a.drop_seed = (const uint64_t*)seed;
-  const double t = (double)p * 4294967296.0;
-  a.drop_keep = t >= 4294967295.0 ? 0xffffffffu : (uint32_t)t;
+  a.drop_keep = (uint32_t)((double)p * 65536.0);
   const float pa = (float)(1.0 - (double)p);
   a.drop_scale = (float)(1.0 / (double)pa);
   return DPA_OK;
@@ -1720,8 +1733,8 @@ static int gn_bwd(const void* x, const void* dout, const float* gamma, const flo
   }
   st = launch_status();
   if (st != DPA_OK) return st;
-  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 256, 0, s>>>((const float*)workspace,
-                                                                    dgamma, dbeta, N, C);
+  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 64 * kPrSlices, 0, s>>>(
+      (const float*)workspace, dgamma, dbeta, N, C);
   return launch_status();
 }
 

@@ -310,10 +310,10 @@ int dpa_gn_silu_film_bwd_bf16(const void* x, const void* dout, const float* gamm
  * 8192 pixels, with a workspace of the *_workspace_bytes size); larger images return
  * DPA_ERR_SHAPE, a missing workspace DPA_ERR_WORKSPACE.
  * Optional dropout of the output (diffusion/unet.py:160, nn.Dropout(p) before conv_2):
- * drop_seed = a uint64 in device memory, NULL for none; an element is kept when its 32-bit
- * half of splitmix64(seed + (idx / 2) * 0x9E3779B97F4A7C15) (idx its NHWC index; the low half
- * for even idx, the high half for odd idx) is >= floor(p * 2^32) with p the fp32 drop_p
- * argument (exact in double; 0xffffffff when that reaches 2^32 - 1), and kept values are
+ * drop_seed = a uint64 in device memory, NULL for none; an element is kept when bits
+ * [16 (idx % 4), 16 (idx % 4) + 16) of splitmix64(seed + (idx / 4) * 0x9E3779B97F4A7C15)
+ * (idx its NHWC index), as a 16-bit number, are >= floor(p * 2^16) with p the fp32 drop_p
+ * argument (exact in double), and kept values are
  * scaled in fp32 by RN32(1 / RN32(1 - p)) before the bf16 rounding (the
  * reference drops the fp32 SiLU output). The backward recomputes the mask from the same seed
  * and p. Dropout takes the resident or chunked form as fp32 x does; 0 <= p < 1.

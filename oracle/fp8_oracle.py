@@ -242,17 +242,17 @@ def splitmix64(seed: int, idx: np.ndarray) -> np.ndarray:
 
 def dropout_keep(seed: int, n: int, p: float) -> np.ndarray:
     """Keep mask of the fused dropout over n elements (NHWC index order): element idx is kept
-    when its 32-bit half of splitmix64(seed, idx // 2) (the low half for even idx, the high
-    half for odd idx) is >= p * 2^32. The reference draws its mask from torch's Philox
-    generator (diffusion/unet.py:160 nn.Dropout), which no restatement reproduces; this mask
-    has the same keep probability 1 - p. p is taken as the fp32 value the C ABI receives
-    (``float drop_p``): the threshold is floor(fp32(p) * 2^32), computed exactly in double."""
-    t = float(np.float32(p)) * 4294967296.0
-    keep_from = 0xFFFFFFFF if t >= 4294967295.0 else int(t)
+    when the 16-bit quarter idx % 4 of splitmix64(seed, idx // 4) (bits 16 (idx % 4) up to
+    16 (idx % 4) + 15) is >= floor(p * 2^16). The reference draws its mask from torch's
+    Philox generator (diffusion/unet.py:160 nn.Dropout), which no restatement reproduces;
+    this mask has the keep probability 1 - floor(p * 2^16) / 2^16, within 2^-16 of 1 - p. p
+    is taken as the fp32 value the C ABI receives (``float drop_p``): the threshold is
+    floor(fp32(p) * 2^16), computed exactly in double."""
+    keep_from = int(float(np.float32(p)) * 65536.0)
     idx = np.arange(n, dtype=np.uint64)
-    z = splitmix64(seed, idx >> np.uint64(1))
-    half = np.where((idx & np.uint64(1)) == 1, z >> np.uint64(32), z & np.uint64(0xFFFFFFFF))
-    return half >= np.uint64(keep_from)
+    z = splitmix64(seed, idx >> np.uint64(2))
+    quarter = (z >> (np.uint64(16) * (idx & np.uint64(3)))) & np.uint64(0xFFFF)
+    return quarter >= np.uint64(keep_from)
 
 
 def dropout_scale(p: float) -> np.float32:

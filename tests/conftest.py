@@ -93,16 +93,16 @@ def _splitmix64_state_for(z: int) -> int:
     return z
 
 
-def dropout_band_seed(p: float = 0.2) -> tuple[int, int]:
-    """A seed whose element-0 hash lies in [floor(p * 2^32), floor(fp32(p) * 2^32)): kept under
-    a double-precision threshold, dropped under the fp32 one the C ABI takes. Returns
-    (seed, element-0 hash)."""
-    lo_d = int(p * 4294967296.0)
-    lo_f = int(float(np.float32(p)) * 4294967296.0)
-    assert lo_d < lo_f
-    h0 = (lo_d + lo_f) // 2
-    for hi in range(0xFFFFFFFF, 0xFFFFFF00, -1):  # element 1 kept; the seed fits an int64
-        seed = _splitmix64_state_for((hi << 32) | h0)
+def dropout_band(k: int = 13107) -> tuple[float, int, int]:
+    """A drop probability p whose fp32 value is k / 2^16 while floor(p * 2^16) = k - 1, and a
+    seed whose element-0 hash quarter is k - 1: element 0 is kept under the double-precision
+    threshold and dropped under the fp32 one the C ABI takes; elements 1-3 (quarters 0xFFFF)
+    are kept. Returns (p, seed, element-0 quarter)."""
+    p = k / 65536.0 - 2.0**-40
+    assert float(np.float32(p)) == k / 65536.0 and int(p * 65536.0) == k - 1
+    h0 = k - 1
+    for hi in range(0xFFFF, 0xFF00, -1):  # quarter 3 stays near the top; the seed fits an int64
+        seed = _splitmix64_state_for((hi << 48) | (0xFFFF << 32) | (0xFFFF << 16) | h0)
         if seed < 2**62:
-            return seed, h0
+            return p, seed, h0
     raise AssertionError("no seed below 2^62")

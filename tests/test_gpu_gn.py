@@ -14,7 +14,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from conftest import assert_bf16_close, dpa_mod, dropout_band_seed, nhwc_bits, randn_bf16
+from conftest import assert_bf16_close, dpa_mod, dropout_band, nhwc_bits, randn_bf16
 from oracle import fp8_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -397,12 +397,11 @@ def test_gn_silu_film_dropout_vs_oracle(G, n, c, h, w, x32):
 @pytest.mark.parametrize("n,c,h,w,x32", [(1, 256, 16, 16, False), (1, 256, 8, 8, True)],
                          ids=lambda v: str(v))
 def test_gn_silu_film_dropout_threshold_band(G, n, c, h, w, x32):
-    """The keep threshold is floor(fp32(p) * 2^32). With p = 0.2 a hash in
-    [floor(0.2 * 2^32), floor(fp32(0.2) * 2^32)) must be dropped: the seed is built (by
-    inverting splitmix64) so that element 0's hash lies in that 13-value band. The kernel's
-    whole mask, forward and backward, equals the oracle's."""
-    p = 0.2
-    seed, _ = dropout_band_seed(p)
+    """The keep threshold is floor(fp32(p) * 2^16). With p = 13107 / 2^16 - 2^-40 (fp32 value
+    13107 / 2^16) a hash quarter of 13106 = floor(p * 2^16) must be dropped: the seed is built
+    (by inverting splitmix64) so that element 0's quarter is that value. The kernel's whole
+    mask, forward and backward, equals the oracle's."""
+    p, seed, _ = dropout_band()
     g = torch.Generator().manual_seed(9)
     x = torch.randn((n, c, h, w), generator=g) + 0.5
     if not x32:

@@ -240,11 +240,26 @@ def test_bf16_rounding_matches_torch():
 
 
 def test_dropout_threshold_uses_fp32_p():
-    """The keep threshold is floor(fp32(p) * 2^32): for p = 0.2 that is 858993472, 13 above
-    floor(0.2 * 2^32). A hash inside that band (built by inverting splitmix64) is dropped."""
-    seed, h0 = conftest.dropout_band_seed(0.2)
+    """The keep threshold is floor(fp32(p) * 2^16): for p = 13107 / 2^16 - 2^-40 that is 13107,
+    one above floor(p * 2^16). A hash quarter of 13106 (built by inverting splitmix64) is
+    dropped; the other three quarters of the same hash decide elements 1-3."""
+    p, seed, h0 = conftest.dropout_band()
     z = int(O.splitmix64(seed, np.zeros(1, dtype=np.uint64))[0])
-    assert z & 0xFFFFFFFF == h0 and z >> 32 > 0xFFFFFF00
-    keep = O.dropout_keep(seed, 2, 0.2)
-    assert not keep[0] and keep[1]
-    assert O.dropout_keep(seed, 2, np.float32(0.2))[0] == keep[0]
+    assert z & 0xFFFF == h0 == 13106 and (z >> 16) & 0xFFFF == 0xFFFF and z >> 48 > 0xFF00
+    keep = O.dropout_keep(seed, 5, p)
+    assert not keep[0] and keep[1:4].all()
+    assert O.dropout_keep(seed, 1, np.float32(p))[0] == keep[0]
+    assert O.dropout_keep(seed, 1, 13106 / 65536.0)[0]  # a threshold of 13106 keeps it
+
+
+def test_dropout_mask_layout():
+    """Element idx reads 16-bit quarter idx % 4 of splitmix64(seed, idx // 4), low quarter
+    first: the mask at p just above a quarter's value drops exactly the elements whose
+    quarter is below it, checked on hashes computed here quarter by quarter."""
+    seed, n = 0x1234_5678_9ABC_DEF0, 64
+    z = O.splitmix64(seed, np.arange(n // 4, dtype=np.uint64))
+    q = np.array([(int(z[i // 4]) >> (16 * (i % 4))) & 0xFFFF for i in range(n)])
+    for t in (1, int(q[5]), int(q[6]) + 1, 32768, 65535):
+        p = t / 65536.0
+        assert np.array_equal(O.dropout_keep(seed, n, p), q >= t), t
+    assert O.dropout_keep(seed, n, 0.0).all()
