@@ -47,28 +47,40 @@ constexpr int kBRowsPerWave = kBN / kWaves;           // 16
 constexpr int kSlotBytes = 16 * kWTN * 2;             // 16 pixels x 64 channels of bf16
 constexpr int kMaxTapDim = 3;
 
-// Tile shape of an igemm_fp8_kernel instance: BM output pixels x kBN channels, the 8 waves as
-// (BM / 64) x (8 / (BM / 64)) wave tiles of 64 pixels x kWTN channels. BM = 256 is the default;
-// BM = 128 (64 x 32 wave tiles, 32 KB stages) and BM = 64 (64 x 16, 24 KB stages) give
+// Tile shape of an igemm_fp8_kernel instance: BM output pixels x BN channels, the 8 waves as
+// kWavesM x kWavesN wave tiles of kWTM pixels x kWTN channels. 256 x 128 is the default;
+// 128 x 128 (64 x 32 wave tiles, 32 KB stages) and 64 x 128 (64 x 16, 24 KB stages) give
 // launches with few output pixels two or four times the tiles, so they fill the CUs without
-// splitting K.
-template <int BM>
+// splitting K; 64 x 32 (4 x 2 waves of 16 x 16, 12 KB stages) four times the 64 x 128 ones.
+// Its B tile is 256 DMAs of 16 B, so waves 0-3 load it (kBLoadWaves) and waves 4-7 wait for
+// their A loads only.
+template <int BM, int BN = kBN>
 struct IgCfg {
-  static constexpr int kBM = BM;
-  static constexpr int kWavesM = BM / kWTM;
-  static constexpr int kWTN = kBN / (kWaves / kWavesM);
+  static constexpr int kWavesM = BN == dpa::kBN ? BM / dpa::kWTM : BM / 16;
+  static constexpr int kBM = BM, kBN = BN;
+  static constexpr int kWavesN = kWaves / kWavesM;
+  static constexpr int kWTM = BM / kWavesM;
+  static constexpr int kWTN = BN / kWavesN;
+  static constexpr int kFA = kWTM / 16;  // 16-pixel MFMA blocks per wave
   static constexpr int kCB = kWTN / 16;  // 16-channel MFMA blocks per wave
-  static constexpr int kStageBytes = (BM + kBN) * kBK;
+  static constexpr int kStageBytes = (BM + BN) * kBK;
   static constexpr int kALoads = BM * kBK / 16 / kIgThreads;
-  static constexpr int kBLoads = kBN * kBK / 16 / kIgThreads;
-  static constexpr int kLoadsPerStage = kALoads + kBLoads;
+  static constexpr int kBLoadWaves = BN * kBK / 16 / 64 < kWaves ? BN * kBK / 16 / 64 : kWaves;
+  static constexpr int kBLoads = BN * kBK / 16 / (64 * kBLoadWaves);  // per B-loading wave
+  static constexpr int kLoadsPerStage = kALoads + kBLoads;          // of a B-loading wave
   static constexpr int kARowsPerWave = BM / kWaves;
-  static constexpr int kBRowsPerWave = kBN / kWaves;
+  static constexpr int kBRowsPerWave = BN / kBLoadWaves;
   static constexpr int kSlotG = kWTN / 8;                 // 16-B granules per slot row
   static constexpr int kSlotBytes = 16 * kSlotG * 16;      // 16 pixels x kWTN channels, bf16
+  static_assert(kWavesM * kWavesN == kWaves && kFA >= 1 && kCB >= 1 && kALoads >= 1 &&
+                    kBLoads >= 1 && kWTM % 16 == 0 && kWTN % 16 == 0,
+                "wave tiles of whole MFMA blocks, whole DMAs per wave");
 };
 static_assert(IgCfg<256>::kWTN == kWTN && IgCfg<256>::kLoadsPerStage == kLoadsPerStage &&
-                  IgCfg<256>::kSlotBytes == kSlotBytes, "the default tile");
+                  IgCfg<256>::kSlotBytes == kSlotBytes && IgCfg<256>::kFA == 4 &&
+                  IgCfg<256>::kBLoadWaves == kWaves && IgCfg<128>::kFA == 4 &&
+                  IgCfg<64>::kFA == 4 && IgCfg<64, 32>::kFA == 1 && IgCfg<64, 32>::kCB == 1,
+              "the tiles");
 
 struct IgemmArgs {
   const uint8_t* act;  // [N][Hi][Wi][C]
@@ -159,12 +171,13 @@ __device__ __forceinline__ v8i ld_frag(const uint8_t* base, int row, int q) {
 // kClasses: the launch holds several output parity classes (p.nclass > 1). The one-class
 // instance reads the scalar tap grid only: the class tables would take SGPRs the main loop
 // needs (with them it reloads kernel arguments inside the loop, ~1 us per launch).
-template <bool kClasses, int BM = 256>
+template <bool kClasses, int BM = 256, int BN = kBN>
 __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArgs p) {
   // this instance's tile (IgCfg); the names shadow the default tile's constants
-  using Cfg = IgCfg<BM>;
-  constexpr int kBM = Cfg::kBM, kWavesM = Cfg::kWavesM, kWTN = Cfg::kWTN, kCB = Cfg::kCB;
-  constexpr int kALoads = Cfg::kALoads, kBLoads = Cfg::kBLoads;
+  using Cfg = IgCfg<BM, BN>;
+  constexpr int kBM = Cfg::kBM, kBN = Cfg::kBN, kWavesM = Cfg::kWavesM, kWTM = Cfg::kWTM;
+  constexpr int kWTN = Cfg::kWTN, kFA = Cfg::kFA, kCB = Cfg::kCB;
+  constexpr int kALoads = Cfg::kALoads, kBLoads = Cfg::kBLoads, kBLoadWaves = Cfg::kBLoadWaves;
   constexpr int kLoadsPerStage = Cfg::kLoadsPerStage;
   constexpr int kARowsPerWave = Cfg::kARowsPerWave, kBRowsPerWave = Cfg::kBRowsPerWave;
   constexpr int kSlotG = Cfg::kSlotG;
@@ -175,9 +188,12 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave % kWavesM;  // pixel quarter (64 rows)
-  const int wn = wave / kWavesM;  // channel half (64 cols)
+  const int wm = wave % kWavesM;  // pixel block (kWTM rows)
+  const int wn = wave / kWavesM;  // channel block (kWTN cols)
   const int frow = lane & 15, fq = lane >> 4;
+  // this wave loads B rows (all waves but with the 64 x 32 tile); wave-uniform
+  const bool b_wave =
+      kBLoadWaves == kWaves || __builtin_amdgcn_readfirstlane(wave) < kBLoadWaves;
 
   // this workgroup's work items (tile, K range): XCD x owns items [x*tiles_per_xcd,
   // +tiles_per_xcd); its wg_per_xcd workgroups take them round-robin
@@ -278,21 +294,30 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
       // 8 rows of the A tile: 1 KB, lane i -> row +i/8, granule slot i%8
       dma16(ok ? real : (const uint8_t*)g_zero16, st + (wave * kARowsPerWave + 8 * r) * kBK);
     }
+    if (b_wave) {
 #pragma unroll
-    for (int r = 0; r < kBLoads; ++r) {
-      const uint8_t* real = p.wgt + (uint32_t)(b_off[r] + wd);
-      dma16(live ? real : (const uint8_t*)g_zero16,
-            st + kBM * kBK + (wave * kBRowsPerWave + 8 * r) * kBK);
+      for (int r = 0; r < kBLoads; ++r) {
+        const uint8_t* real = p.wgt + (uint32_t)(b_off[r] + wd);
+        dma16(live ? real : (const uint8_t*)g_zero16,
+              st + kBM * kBK + (wave * kBRowsPerWave + 8 * r) * kBK);
+      }
     }
+  };
+  // until at most n stages of this wave's DMAs are in flight
+  auto wait_stages = [&](auto n) __attribute__((always_inline)) {
+    if (b_wave)
+      wait_vmcnt<decltype(n)::value * kLoadsPerStage>();
+    else
+      wait_vmcnt<decltype(n)::value * kALoads>();
   };
 
   // ---- compute side ----
-  v4f acc[kCB][4];
+  v4f acc[kCB][kFA];
 #pragma unroll
   for (int i = 0; i < kCB; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  v8i fa[4], fb[kCB];
+    for (int j = 0; j < kFA; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8i fa[kFA], fb[kCB];
 
   // finished item j: scale, bias, bf16 -> wave slot -> 128-B runs per pixel; or, with
   // split K, the raw fp32 sums of its K range as the accumulators hold them: item i's
@@ -311,21 +336,24 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
     const int tn = tic - tm * p.tiles_n;
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int c0 = n0 + wn * kWTN;
-    if (BM == 256 && p.splits > 1) {  // (launch_igemm splits the default tile only)
-      float* part = p.partial + (int64_t)item * (kBM * kBN) + wave * (16 * 256) + lane * 4;
+    if constexpr (BM == 256 && BN == dpa::kBN) {  // (launch_igemm splits the default tile only)
+      if (p.splits > 1) {
+        float* part = p.partial + (int64_t)item * (kBM * kBN) + wave * (16 * 256) + lane * 4;
 #pragma unroll
-      for (int pj = 0; pj < 4; ++pj) {
+        for (int pj = 0; pj < 4; ++pj) {
 #pragma unroll
-        for (int ci = 0; ci < 4; ++ci) {
-          __builtin_nontemporal_store(acc[ci][pj], reinterpret_cast<v4f*>(part + (pj * 4 + ci) * 256));
-          acc[ci][pj] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int ci = 0; ci < 4; ++ci) {
+            __builtin_nontemporal_store(acc[ci][pj],
+                                        reinterpret_cast<v4f*>(part + (pj * 4 + ci) * 256));
+            acc[ci][pj] = v4f{0.f, 0.f, 0.f, 0.f};
+          }
         }
+        return;
       }
-      return;
     }
     uint8_t* slot = ig_slot[wave];
 #pragma unroll
-    for (int pj = 0; pj < 4; ++pj) {
+    for (int pj = 0; pj < kFA; ++pj) {
 #pragma unroll
       for (int ci = 0; ci < kCB; ++ci) {
         float v[4];
@@ -358,18 +386,18 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
 #pragma unroll
     for (int i = 0; i < kCB; ++i)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int jj = 0; jj < kFA; ++jj) acc[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
   };
 
   issue(ig_st[0], 0);
   issue(ig_st[1], 1);
   issue(ig_st[2], 2);
-  wait_vmcnt<2 * kLoadsPerStage>();
+  wait_stages(std::integral_constant<int, 2>{});
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < kCB; ++i) fb[i] = ld_frag(ig_st[0] + kBM * kBK, wn * kWTN + i * 16 + frow, fq);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fa[i] = ld_frag(ig_st[0], wm * kWTM + i * 16 + frow, fq);
+  for (int i = 0; i < kFA; ++i) fa[i] = ld_frag(ig_st[0], wm * kWTM + i * 16 + frow, fq);
 
   // Step s on stage buffer cur = s % 3: wait until stage s+1 has landed (its DMA was issued
   // two steps earlier), barrier (every wave finished reading stage s), then the 16 MFMAs on
@@ -378,12 +406,12 @@ __global__ __launch_bounds__(kIgThreads, 1) void igemm_fp8_kernel(const IgemmArg
   int cur = 0, kstep = 0;
   for (int s = 0; s < total; ++s) {
     const int nx = cur == 2 ? 0 : cur + 1;
-    wait_vmcnt<kLoadsPerStage>();
+    wait_stages(std::integral_constant<int, 1>{});
     wait_lgkmcnt0();
     lds_barrier();
     const uint8_t* nxt = ig_st[nx];
 #pragma unroll
-    for (int pj = 0; pj < 4; ++pj) {
+    for (int pj = 0; pj < kFA; ++pj) {
 #pragma unroll
       for (int ci = 0; ci < kCB; ++ci) acc[ci][pj] = mfma16x16x128_e4m3(fb[ci], fa[pj], acc[ci][pj]);
       fa[pj] = ld_frag(nxt, wm * kWTM + pj * 16 + frow, fq);
@@ -522,12 +550,15 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
   // Launches whose 256-pixel tiles would leave at least half the CUs idle take 128-pixel
   // tiles (twice as many) unsplit, when a tile has at most kHalfMaxSteps K-steps, and
   // 64-pixel tiles when the 128-pixel ones would still leave half the CUs idle.
-  int bm = kBM;
+  int bm = kBM, bn = kBN;
   if (a.nclass == 1 && a.nk <= kHalfMaxSteps) {
     const int cus = num_cus();
     if (ceil_div(a.M, 256) * a.tiles_n * 2 <= cus) bm = 128;
     if (bm == 128 && ceil_div(a.M, 128) * a.tiles_n * kQuarterFill <= cus) bm = 64;
+    // 64 x 32 tiles where the 64 x 128 ones fill at most a quarter of the CUs
+    if (bm == 64 && ceil_div(a.M, 64) * a.tiles_n * 4 <= cus) bn = 32;
   }
+  a.tiles_n = a.Cout / bn;
   const bool half = bm < kBM;
   const int tiles_m = (int)ceil_div(a.M, bm);
   a.tiles_pc = tiles_m * a.tiles_n;
@@ -562,6 +593,8 @@ static int launch_igemm(IgemmArgs& a, int N, hipStream_t s, void* workspace,
     igemm_fp8_kernel<true><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   else if (bm == 128)
     igemm_fp8_kernel<false, 128><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
+  else if (bm == 64 && bn == 32)
+    igemm_fp8_kernel<false, 64, 32><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   else if (bm == 64)
     igemm_fp8_kernel<false, 64><<<(unsigned)grid, kIgThreads, 0, s>>>(a);
   else
