@@ -52,6 +52,15 @@ struct GnArgs {
   int dx_add_bf16;     // bwd: dx_add is bf16 while x and dx are fp32
   uint16_t* x_bf16;    // fwd: fp32 x also written as bf16 here (chunked and small forms), or null
   uint32_t* xb_part;   // fwd: with x_bf16, one amax partial of its bf16 values per workgroup
+  // Two-source x (a decoder stage's first GroupNorm with the upsample-and-concatenate before
+  // it, diffusion/unet.py:379-382): channels [0, cat_ca) are the 2x nearest upsampling of
+  // cat_a ([N][H/2][W/2][cat_ca]), the others cat_h ([N][H][W][C - cat_ca]), both bf16 (the
+  // concatenation is fp32, but holds these bf16 values exactly); images of cat_w columns.
+  const uint16_t* cat_a;
+  const uint16_t* cat_h;
+  int cat_ca, cat_w;
+  uint16_t* cat_ga;  // bwd: gradient of cat_a (each 2x2 window of dx summed), bf16
+  uint16_t* cat_gh;  // bwd: gradient of cat_h, bf16
   // Producer-fused cast for a delayed-scaling consumer (chunked and small forms): instead of
   // the bf16 output (fwd) or bf16 dx (bwd), e4m3(bf16 value / *q_scale) goes to q, and each
   // workgroup leaves the amax of its bf16 values in q_part[workgroup] (count in *q_count)
@@ -1120,8 +1129,36 @@ __device__ __forceinline__ void res_load(const uint8_t* const (&src)[NL], const 
       v[l][u] = *reinterpret_cast<const uint4*>(src[l] + (int64_t)pxs[u] * stride[l]);
 }
 
-template <int PLN, int U, bool kFilm, bool kF32, bool kDrop>
+// Two-source x (GnArgs::cat_a / cat_h) of channels ch .. ch + 7 (all of them from one source:
+// cat_ca is a multiple of the slab), lane pl's pixels pl + PLN u as res_load's.
+template <int PLN, int U>
+__device__ __forceinline__ void cat_load(const GnArgs& p, int n, int ch, int pl, uint4 (&v)[1][U],
+                                         bool (&ok)[U], int (&pxs)[U]) {
+  const int W = p.cat_w, wl = W >> 1, ca = p.cat_ca;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int px = pl + PLN * u;
+    ok[u] = px < p.HW;
+    pxs[u] = ok[u] ? px : p.HW - 1;
+  }
+  if (ch < ca) {
+    const uint16_t* a = p.cat_a + (int64_t)n * (p.HW >> 2) * ca + ch;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int y = pxs[u] / W, x = pxs[u] - y * W;
+      v[0][u] = *reinterpret_cast<const uint4*>(a + ((y >> 1) * wl + (x >> 1)) * ca);
+    }
+  } else {
+    const int chh = p.C - ca;
+    const uint16_t* h = p.cat_h + (int64_t)n * p.HW * chh + (ch - ca);
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[0][u] = *reinterpret_cast<const uint4*>(h + (int64_t)pxs[u] * chh);
+  }
+}
+
+template <int PLN, int U, bool kFilm, bool kF32, bool kDrop, bool kCat = false>
 __global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
+  static_assert(!kCat || !kF32, "the two sources are bf16");
   __shared__ uint32_t qred[PLN / 8];
   __shared__ float red[(PLN / 8) * 8 * 2];
   __shared__ float hs[16];
@@ -1134,8 +1171,23 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
   uint4 v[in.kN][U];
   bool ok[U];
   int pxs[U];
-  res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
-  if constexpr (kF32) {
+  if constexpr (kCat)
+    cat_load<PLN, U>(p, n, ch, pl, v, ok, pxs);
+  else
+    res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
+  if constexpr (kCat) {
+    // the bf16 copy of the concatenation is the loaded values themselves
+    if (p.x_bf16) {
+      us2 xacc = {0, 0};
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) {
+          st_nt16(p.x_bf16 + ((int64_t)n * p.HW + pxs[u]) * p.C + ch, v[0][u]);
+          xacc = absmax8(xacc, v[0][u]);
+        }
+      if (p.xb_part) finish_xb_amax(p, xacc, qred);
+    }
+  } else if constexpr (kF32) {
     if (p.x_bf16) {
       us2 xacc = {0, 0};
 #pragma unroll
@@ -1229,8 +1281,9 @@ struct GnResDout {
   static constexpr int kBytes = kLds ? U * 8 * PLN * 16 : 16;
 };
 
-template <int PLN, int U, bool kFilm, bool kF32, bool kDrop>
+template <int PLN, int U, bool kFilm, bool kF32, bool kDrop, bool kCat = false>
 __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
+  static_assert(!kCat || (!kF32 && PLN == 64 && U == 16), "bf16 sources, 32x32 images");
   using DL = GnResDout<PLN, U>;
   __shared__ __attribute__((aligned(16))) uint8_t dls[DL::kBytes];
   __shared__ uint32_t qred[PLN / 8];
@@ -1248,7 +1301,12 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
   uint4 v[in.kN][U];
   bool ok[U];
   int pxs[U];
-  res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
+  if constexpr (kCat) {
+    static_assert(in.kN == 1, "dout in LDS");
+    cat_load<PLN, U>(p, n, ch, pl, v, ok, pxs);
+  } else {
+    res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
+  }
   if constexpr (DL::kLds) {
     const uint32_t lbase =
         __builtin_amdgcn_readfirstlane(LDS_ADDR(dls) + (uint32_t)(threadIdx.x & ~63) * 16);
@@ -1329,23 +1387,126 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
     m1[h] = group_sum(hs[0], 2 * gq + h, p.cpg) * inv_cnt;
     m2[h] = group_sum(hs[1], 2 * gq + h, p.cpg) * inv_cnt;
   }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    // the second pass forms the per-pixel terms again from the packed registers: hidden from
-    // the compiler, which would otherwise keep the first pass's unpacked terms of every
-    // pixel alive across the reduction (8-16 registers per pixel more)
+  // pixel u's dx (the fused concatenation's form; the loop below is the same per pixel)
+  auto pixel_dx = [&](int u, float (&t)[8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int l = 0; l < in.kN; ++l) opaque_u4(v[l][u]);
     float f[8], d[8], xh[8], g[8];
     unpack_x<kF32>(v, u, f);
     bwd_dout_kb<kDrop>(dout_u(u), keep[u], p.drop_scale, d);
     bwd_terms<kFilm>(f, d, st, xh, g);
-    auto dx = [&](int e) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
       const int h = e >> 2;
-      return st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
-    };
-    if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
-    __builtin_amdgcn_sched_barrier(0);
+      t[e] = st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
+    }
+  };
+  if constexpr (kCat) {
+    // The concatenation's fp32 gradient (plus the bf16 skip-path gradient, as autograd adds
+    // it), split as the upsample-and-concatenate's backward does: cat_h's channels rounded to
+    // bf16; cat_a's summed over each 2x2 window from zero in row-major order, then rounded
+    // (torch's upsample_nearest2d_backward). At 32x32, pixel pl + 64 u is row 2u + pl / 32,
+    // column pl % 32: window (u, j) holds lanes 2j, 2j + 1 (row 2u) and 2j + 32, 2j + 33 (row
+    // 2u + 1). The odd lane's value comes by a shuffle (8 threads on), the lower row's two
+    // through the dout slots of LDS already read, four pixels per exchange.
+    const bool in_a = ch < p.cat_ca;  // workgroup-uniform
+    const bool even = (pl & 1) == 0;
+    float* xs = reinterpret_cast<float*>(dls);
+#pragma unroll
+    for (int u0 = 0; u0 < U; u0 += 4) {
+      float t[4][8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = u0 + k;
+        pixel_dx(u, t[k]);
+        if (p.dx_add) {
+          float a[8];
+          unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.dx_add) +
+                                                  base + (int64_t)pxs[u] * p.C), a);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t[k][e] += a[e];
+        }
+        if (!in_a) {
+          const int chh = p.C - p.cat_ca;
+          uint32_t o[4];
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(t[k][e], t[k][e + 1]);
+          st_nt16(p.cat_gh + ((int64_t)n * p.HW + pxs[u]) * chh + (ch - p.cat_ca),
+                  uint4{o[0], o[1], o[2], o[3]});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (in_a) {
+        __syncthreads();  // every thread has read the dout slots u0 .. u0 + 3
+        float r[4][8];  // the odd neighbour's values (lane + 8: pixel lane pl + 1)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) r[k][e] = __shfl_down(t[k][e], 8, 64);
+        // slot u0 + k, entry (window column j, granule gq): row 2u + 1's pair, 16 floats
+        const int ent = (((pl & 31) >> 1) * 8 + gq) * 16;
+        if (pl >= 32 && even) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            float* e0 = xs + (u0 + k) * (8 * PLN * 4) + ent;
+#pragma unroll
+            for (int q4 = 0; q4 < 2; ++q4) {
+              *reinterpret_cast<v4f*>(e0 + 4 * q4) =
+                  v4f{t[k][4 * q4], t[k][4 * q4 + 1], t[k][4 * q4 + 2], t[k][4 * q4 + 3]};
+              *reinterpret_cast<v4f*>(e0 + 8 + 4 * q4) =
+                  v4f{r[k][4 * q4], r[k][4 * q4 + 1], r[k][4 * q4 + 2], r[k][4 * q4 + 3]};
+            }
+          }
+        }
+        __syncthreads();
+        if (pl < 32 && even) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float* e0 = xs + (u0 + k) * (8 * PLN * 4) + ent;
+            float acc[8];
+#pragma unroll
+            for (int q4 = 0; q4 < 2; ++q4) {
+              const v4f lo = *reinterpret_cast<const v4f*>(e0 + 4 * q4);
+              const v4f hi = *reinterpret_cast<const v4f*>(e0 + 8 + 4 * q4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int c = 4 * q4 + e;
+                acc[c] = 0.0f;
+                acc[c] += t[k][c];  // (2u, 2j)
+                acc[c] += r[k][c];  // (2u, 2j + 1)
+                acc[c] += lo[e];    // (2u + 1, 2j)
+                acc[c] += hi[e];    // (2u + 1, 2j + 1)
+              }
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(acc[e], acc[e + 1]);
+            const int wi = (u0 + k) * 16 + (pl >> 1);  // window row u0 + k, column pl / 2
+            st_nt16(p.cat_ga + ((int64_t)n * (p.HW >> 2) + wi) * p.cat_ca + ch,
+                    uint4{o[0], o[1], o[2], o[3]});
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // the second pass forms the per-pixel terms again from the packed registers: hidden
+      // from the compiler, which would otherwise keep the first pass's unpacked terms of
+      // every pixel alive across the reduction (8-16 registers per pixel more)
+#pragma unroll
+      for (int l = 0; l < in.kN; ++l) opaque_u4(v[l][u]);
+      float f[8], d[8], xh[8], g[8];
+      unpack_x<kF32>(v, u, f);
+      bwd_dout_kb<kDrop>(dout_u(u), keep[u], p.drop_scale, d);
+      bwd_terms<kFilm>(f, d, st, xh, g);
+      auto dx = [&](int e) __attribute__((always_inline)) {
+        const int h = e >> 2;
+        return st.rs[h] * __builtin_fmaf(-xh[e], m2[h], g[e] * st.gC[e] - m1[h]);
+      };
+      if (ok[u]) store_dx<kF32>(p, base + (int64_t)pxs[u] * p.C, dx, qo);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   if (p.q) qo.finish(p, qred);
 }
@@ -1849,4 +2010,106 @@ extern "C" int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float*
   return gn_bwd(x, dout, gamma, beta, film_scale, film_shift, film_wb, mean, rstd, dxq, dgamma,
                 dbeta, dfilm_scale, dfilm_shift, dfilm_wb, workspace, workspace_bytes, N, HW, C, G,
                 stream, false, drop_seed, drop_p, nullptr, false, &qo);
+}
+
+// ---- a decoder stage's first GroupNorm+SiLU fused with the upsample-and-concatenate before
+// it (diffusion/unet.py:379-382 and :151): x = cat([up2(a), h], channels), read from a and h
+// (both bf16, NHWC) instead of the fp32 concatenation; the backward writes the gradients of
+// a and h instead of the concatenation's. The resident form of 1024-pixel images only
+// (64 pixel lanes x 16 pixels, 2x2 windows per lane in the backward). ----
+
+static int upcat_gn_check(const void* a, const void* h, int N, int H, int W, int Ca, int Ch,
+                          int G) {
+  if (!a || !h) return DPA_ERR_NULL;
+  if (N <= 0 || H <= 0 || W <= 0 || Ca <= 0 || Ch <= 0) return DPA_ERR_SIZE;
+  if (H != 32 || W != 32 || Ca % kSlab != 0 || Ch % kSlab != 0 ||
+      !gn_shape_ok(N, H * W, Ca + Ch, G))
+    return DPA_ERR_SHAPE;
+  if ((int64_t)N * H * W * (Ca + Ch) > 0x7fffffffLL) return DPA_ERR_SIZE;
+  if (!aligned(a, 16) || !aligned(h, 16)) return DPA_ERR_ALIGN;
+  return DPA_OK;
+}
+
+extern "C" int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int N, int H, int W, int Ca,
+                                     int Ch, const float* gamma, const float* beta, void* out,
+                                     void* q, const float* q_scale, uint32_t* q_partials,
+                                     int q_partials_cap, uint32_t* q_count, float* mean,
+                                     float* rstd, void* x_bf16, uint32_t* xb_partials,
+                                     int xb_partials_cap, int G, float eps, void* stream) {
+  const int st0 = upcat_gn_check(a, h, N, H, W, Ca, Ch, G);
+  if (st0 != DPA_OK) return st0;
+  if (!gamma || !beta || !mean || !rstd || (!out && !q)) return DPA_ERR_NULL;
+  if (out && q) return DPA_ERR_SHAPE;  // one output: bf16 or e4m3
+  if (xb_partials && !x_bf16) return DPA_ERR_NULL;
+  if (!aligned(out, 16) || !aligned(x_bf16, 16) || !aligned(xb_partials, 4)) return DPA_ERR_ALIGN;
+  const int C = Ca + Ch, HW = H * W;
+  GnArgs g{};
+  g.x = h;  // (not read: the kernel reads cat_a and cat_h)
+  g.cat_a = (const uint16_t*)a;
+  g.cat_h = (const uint16_t*)h;
+  g.cat_ca = Ca;
+  g.cat_w = W;
+  g.gamma = gamma;
+  g.beta = beta;
+  g.out = out;
+  g.mean = mean;
+  g.rstd = rstd;
+  g.x_bf16 = (uint16_t*)x_bf16;
+  g.N = N; g.HW = HW; g.C = C; g.G = G; g.cpg = C / G; g.eps = eps;
+  const int64_t nblk = gn_q_blocks(N, HW, C);
+  if (xb_partials) {
+    if (xb_partials_cap < nblk) return DPA_ERR_WORKSPACE;
+    g.xb_part = xb_partials;
+  }
+  if (q) {
+    const GnQOut qo{q, q_scale, q_partials, q_partials_cap, q_count};
+    const int qst = gn_set_q(g, &qo, nblk);
+    if (qst != DPA_OK) return qst;
+    g.out = q;  // not written: the kernel stores through g.q
+  }
+  dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+  gn_res_fwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, (hipStream_t)stream>>>(g);
+  return launch_status();
+}
+
+extern "C" int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int N, int H, int W, int Ca,
+                                     int Ch, const void* dout, const float* gamma,
+                                     const float* beta, const float* mean, const float* rstd,
+                                     const void* dx_add, void* ga, void* gh, float* dgamma,
+                                     float* dbeta, void* workspace, int64_t workspace_bytes,
+                                     int G, void* stream) {
+  const int st0 = upcat_gn_check(a, h, N, H, W, Ca, Ch, G);
+  if (st0 != DPA_OK) return st0;
+  if (!dout || !gamma || !beta || !mean || !rstd || !ga || !gh || !dgamma || !dbeta)
+    return DPA_ERR_NULL;
+  const int C = Ca + Ch, HW = H * W;
+  if (!workspace || workspace_bytes < (int64_t)2 * N * C * 4) return DPA_ERR_WORKSPACE;
+  if (!aligned(dout, 16) || !aligned(dx_add, 16) || !aligned(ga, 16) || !aligned(gh, 16) ||
+      !aligned(workspace, 4))
+    return DPA_ERR_ALIGN;
+  GnArgs g{};
+  g.x = h;  // (not read: the kernel reads cat_a and cat_h)
+  g.cat_a = (const uint16_t*)a;
+  g.cat_h = (const uint16_t*)h;
+  g.cat_ca = Ca;
+  g.cat_w = W;
+  g.cat_ga = (uint16_t*)ga;
+  g.cat_gh = (uint16_t*)gh;
+  g.dout = (const uint16_t*)dout;
+  g.gamma = gamma;
+  g.beta = beta;
+  g.mean = const_cast<float*>(mean);
+  g.rstd = const_cast<float*>(rstd);
+  g.part = (float*)workspace;
+  g.dx_add = dx_add;
+  g.dx_add_bf16 = 1;
+  g.N = N; g.HW = HW; g.C = C; g.G = G; g.cpg = C / G; g.eps = 0.f;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(C / kSlab), (unsigned)N);
+  gn_res_bwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, s>>>(g);
+  int st = launch_status();
+  if (st != DPA_OK) return st;
+  gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 64 * kPrSlices, 0, s>>>(
+      (const float*)workspace, dgamma, dbeta, N, C);
+  return launch_status();
 }

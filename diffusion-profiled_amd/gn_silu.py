@@ -287,6 +287,100 @@ def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5, skip_bf1
     return GroupNormSiLUTee.apply(x, gamma, beta, groups, eps, skip_bf16, hand)
 
 
+def upcat_ok(a: torch.Tensor, h: torch.Tensor, up: bool) -> bool:
+    """Whether cat([up2(a), h], 1) can feed the fused upsample-and-concatenate GroupNorm
+    (dpa_upcat_gn_silu_fwd): both bf16 channels-last on the GPU, 1024-pixel images, channel
+    counts multiples of 64."""
+    cl = torch.channels_last
+    if not (up and a.is_cuda and h.is_cuda and a.dtype == torch.bfloat16
+            and h.dtype == torch.bfloat16 and a.ndim == 4 and h.ndim == 4):
+        return False
+    n, ca, ha, wa = a.shape
+    nh, ch, hh, wh = h.shape
+    return (n == nh and hh == 2 * ha and wh == 2 * wa and hh * wh == 1024 and ca % 64 == 0
+            and ch % 64 == 0 and a.is_contiguous(memory_format=cl)
+            and h.is_contiguous(memory_format=cl) and a.data_ptr() % 16 == 0
+            and h.data_ptr() % 16 == 0)
+
+
+class UpcatGroupNormSiLUTee(torch.autograd.Function):
+    """GroupNormSiLUTee on x = cat([up2(a), h], 1), the fp32 decoder-stage input of
+    diffusion/unet.py:379-382, with skip_bf16: (silu(GroupNorm(x)), x.to(bfloat16)). The
+    kernels read a and h (bf16) where x would be read, so the fp32 concatenation is never
+    formed; the backward returns the gradients of a and h that the upsample-and-concatenate's
+    backward would form from the GroupNorm's fp32 dx plus the bf16 skip-path gradient. Every
+    output and gradient is bit-identical to upsample_concat followed by GroupNormSiLUTee."""
+
+    @staticmethod
+    def forward(ctx: Any, a, h, gamma, beta, groups: int, eps: float,
+                hand: Fp8Handoff | None = None):
+        n, ca, _, _ = a.shape
+        _, ch, hh, wh = h.shape
+        c = ca + ch
+        cl = torch.channels_last
+        x16 = torch.empty((n, c, hh, wh), device=a.device, dtype=torch.bfloat16, memory_format=cl)
+        xbp = _xb_partials(x16, groups)
+        mean = torch.empty(n * groups, device=a.device, dtype=torch.float32)
+        rstd = torch.empty(n * groups, device=a.device, dtype=torch.float32)
+        g32, b32 = gamma.float().contiguous(), beta.float().contiguous()
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        if hand is None:
+            out = torch.empty((n, c, hh, wh), device=a.device, dtype=torch.bfloat16,
+                              memory_format=cl)
+            q = None
+            qargs = (None, None, 0, None)
+        else:
+            out = None
+            q = torch.empty((n, c, hh, wh), device=a.device, dtype=FP8_DTYPE, memory_format=cl)
+            qargs = (hand.scale.data_ptr(), hand.partials.data_ptr(), hand.partials.numel(),
+                     hand.count.data_ptr())
+        _lib.call("dpa_upcat_gn_silu_fwd", a.data_ptr(), h.data_ptr(), n, hh, wh, ca, ch,
+                  g32.data_ptr(), b32.data_ptr(), p(out), p(q), *qargs, mean.data_ptr(),
+                  rstd.data_ptr(), x16.data_ptr(), p(xbp), 0 if xbp is None else xbp.numel(),
+                  groups, float(eps), _stream(a))
+        if xbp is not None:
+            _fp8.mark_amax_partials(x16, xbp, xbp.numel())
+        if hand is not None:
+            hand.q = q
+            out = placeholder((n, c, hh, wh), torch.bfloat16, a.device)
+        ctx.groups = groups
+        ctx.save_for_backward(a, h, gamma, beta, mean, rstd)
+        return out, x16
+
+    @staticmethod
+    def backward(ctx: Any, dout, dskip):
+        a, h, gamma, beta, mean, rstd = ctx.saved_tensors
+        n, ca, _, _ = a.shape
+        _, ch, hh, wh = h.shape
+        c = ca + ch
+        cl = torch.channels_last
+        dout = dout.to(torch.bfloat16).contiguous(memory_format=cl)
+        add = None
+        if dskip is not None:
+            # the skip input is the bf16 copy, so its gradient is bf16
+            add = dskip.to(torch.bfloat16).contiguous(memory_format=cl)
+        ga = torch.empty_like(a, memory_format=cl)
+        gh = torch.empty_like(h, memory_format=cl)
+        dgamma = torch.empty(c, device=a.device, dtype=torch.float32)
+        dbeta = torch.empty(c, device=a.device, dtype=torch.float32)
+        ws_bytes = 2 * n * c * 4
+        ws = torch.empty(ws_bytes, device=a.device, dtype=torch.uint8)
+        _lib.call("dpa_upcat_gn_silu_bwd", a.data_ptr(), h.data_ptr(), n, hh, wh, ca, ch,
+                  dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+                  beta.float().contiguous().data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                  None if add is None else add.data_ptr(), ga.data_ptr(), gh.data_ptr(),
+                  dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws_bytes, ctx.groups,
+                  _stream(a))
+        return ga, gh, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None, None, None
+
+
+def upcat_group_norm_silu_tee(a, h, gamma, beta, groups: int, eps: float = 1e-5,
+                              hand: Fp8Handoff | None = None):
+    """group_norm_silu_tee(upsample_concat(a, h, True), ..., skip_bf16=True) without the fp32
+    concatenation (upcat_ok(a, h, True) must hold)."""
+    return UpcatGroupNormSiLUTee.apply(a, h, gamma, beta, groups, eps, hand)
+
+
 class GroupNormSiLUFilm(torch.autograd.Function):
     """silu(bf16(w + 1) * GroupNorm(x) + b) with (w, b) = chunk(film_wb, 2, dim=1), the time
     projection of diffusion/unet.py:157-159, read by the kernel in bf16; the backward returns

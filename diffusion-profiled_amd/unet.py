@@ -44,6 +44,7 @@ from .residual import (downsample2, downsample2_tee, join_fp8_ok, residual_join,
 from .layer_norm import supported as ln_supported
 from .gn_silu import DROPOUT_SEEDS, dropout_ok as gn_dropout_ok, fp8_ok as gn_fp8_ok
 from .gn_silu import group_norm_silu, group_norm_silu_film, group_norm_silu_tee
+from .gn_silu import upcat_group_norm_silu_tee, upcat_ok
 from .gn_silu import supported as gn_supported
 from .thinconv import ImageConv2d
 
@@ -282,6 +283,24 @@ def _conv_handoff(conv: Conv2dFP8, h: torch.Tensor, xh: K.Fp8Handoff | None,
     return conv(h, None if xh is None else xh.q, dyh)
 
 
+class CatInput:
+    """A decoder stage's input torch.concat([F.interpolate(a, scale_factor=2) if up else a, h],
+    dim=1) (diffusion/unet.py:379-382), not yet formed: the stage's first residual block reads
+    it through the fused upsample-and-concatenate GroupNorm where that applies, and forms it
+    (upsample_concat) otherwise."""
+
+    def __init__(self, a: torch.Tensor, h: torch.Tensor, up: bool):
+        self.a, self.h, self.up = a, h, up
+        n, ca, ha, wa = a.shape
+        s = 2 if up else 1
+        self.shape = torch.Size((n, ca + h.shape[1], ha * s, wa * s))
+        self.is_cuda = a.is_cuda
+        self.device = a.device
+
+    def materialize(self) -> torch.Tensor:
+        return upsample_concat(self.a, self.h, up=self.up)
+
+
 class ResidualBlock(nn.Module):
     """diffusion/unet.py:107-161.
 
@@ -313,7 +332,18 @@ class ResidualBlock(nn.Module):
     def reset_parameters(self):
         torch.nn.init.zeros_(self.conv_2.conv.weight)
 
-    def forward(self, x: torch.Tensor, t: torch.Tensor):
+    def forward(self, x: torch.Tensor | CatInput, t: torch.Tensor):
+        cat = None
+        if isinstance(x, CatInput):
+            # the fused upsample-and-concatenate GroupNorm: bf16 sources, a 1x1 skip conv
+            # (which reads the bf16 concatenation the kernel writes), the fused first norm
+            if (self.fused and upcat_ok(x.a, x.h, x.up)
+                    and gn_supported(x.shape[1], self.norm1.num_groups)
+                    and isinstance(self.skip_connection, Conv1x1FP8)
+                    and torch.is_autocast_enabled("cuda")):
+                cat = x
+            else:
+                x = x.materialize()
         n, _, hh, ww = x.shape
         y_shape = (n, self.conv_1.conv.out_channels, hh, ww)     # conv_1's and conv_2's output
         gpu = self.fused and _on_gpu(x)
@@ -334,9 +364,15 @@ class ResidualBlock(nn.Module):
             # writes that copy as it reads x
             skip16 = (isinstance(self.skip_connection, Conv1x1FP8)
                       and torch.is_autocast_enabled("cuda"))
-            h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias, g1,
-                                           self.norm1.eps, skip16, x1)
+            if cat is not None:
+                h, resid = upcat_group_norm_silu_tee(cat.a, cat.h, self.norm1.weight,
+                                                     self.norm1.bias, g1, self.norm1.eps, x1)
+            else:
+                h, resid = group_norm_silu_tee(x, self.norm1.weight, self.norm1.bias, g1,
+                                               self.norm1.eps, skip16, x1)
         else:
+            if cat is not None:
+                x = cat.materialize()
             resid, h = x, norm_silu(self.norm1, x, self.fused)
         x = _conv_handoff(self.conv_1, h, x1, dy1)
         if fused2:
@@ -507,6 +543,8 @@ class UNet(nn.Module):
 
     # the encoder activations' two gradients summed inside the downsampling's backward
     down_tee = True
+    # a decoder stage's upsample-and-concatenate read by its first GroupNorm (CatInput)
+    upcat_gn = True
 
     def __init__(self, config: UNetConfig):
         super().__init__()
@@ -656,8 +694,12 @@ class UNet(nn.Module):
         act = self.mid(act, t_emb)
         for i, stage in enumerate(self.up_stages):
             h = hs.pop()
-            # torch.concat([self.upsample(act) if i > 0 else act, h], dim=1), one pass on the GPU
-            act = stage(upsample_concat(act, h, up=i > 0), t_emb)
+            # torch.concat([self.upsample(act) if i > 0 else act, h], dim=1): one pass on the
+            # GPU, or none, read by the stage's first GroupNorm from act and h (CatInput)
+            if self.upcat_gn and i > 0:
+                act = stage(CatInput(act, h, True), t_emb)
+            else:
+                act = stage(upsample_concat(act, h, up=i > 0), t_emb)
         return self.out(act)
 
 

@@ -22,6 +22,7 @@ pytestmark = pytest.mark.gpu
 K = dpa_mod("fp8_kernels")
 U = dpa_mod("unet")
 T = dpa_mod("trainer")
+G = dpa_mod("gn_silu")
 
 
 def f32(t):
@@ -274,9 +275,10 @@ def _fp8_site_active(m, x) -> bool:
 def test_unet_fused_gradient_sums_equal_autograd():
     """The skip-gradient sums fused into kernels (the encoder activations' two gradients
     inside the downsampling's backward, the attention block input's inside the LayerNorm
-    backward) change no bit of the U-Net's gradients: cfg5's model at batch 2 (current
-    scaling, dropout off), forward + backward under autocast with the fused sums and with
-    autograd's own accumulation."""
+    backward) and the 32x32 decoder stage's upsample-and-concatenate read by its first
+    GroupNorm change no bit of the U-Net's gradients: cfg5's model at batch 2 (current
+    scaling, dropout off), forward + backward under autocast with the fused forms and with
+    autograd's own accumulation on the formed concatenation."""
     torch.manual_seed(5)
     model = _nonzero_init(U.UNet(_cfg())).to(memory_format=torch.channels_last).cuda()
     g = torch.Generator().manual_seed(6)
@@ -286,8 +288,28 @@ def test_unet_fused_gradient_sums_equal_autograd():
     gy = torch.randn((2, 3, 32, 32), generator=g).cuda().contiguous(
         memory_format=torch.channels_last)
     grads = []
+    calls = []
+    orig = G.UpcatGroupNormSiLUTee.apply
+
+    def counted(*args):
+        calls.append(1)
+        return orig(*args)
+
+    G.UpcatGroupNormSiLUTee.apply = counted  # counts the fused calls; removed again below
+    try:
+        _fused_vs_autograd_grads(model, x, t, gy, grads)
+    finally:
+        del G.UpcatGroupNormSiLUTee.apply
+    assert len(calls) == 1  # the fused pass took the fused concatenation once (32x32 stage)
+    assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 100
+    for n in grads[0]:
+        assert torch.equal(grads[0][n], grads[1][n]), n
+
+
+def _fused_vs_autograd_grads(model, x, t, gy, grads):
     for fused in (True, False):
         model.down_tee = fused
+        model.upcat_gn = fused
         for m in model.modules():
             if isinstance(m, U.CHWAttention):
                 m.ln_tee = fused
@@ -297,9 +319,6 @@ def test_unet_fused_gradient_sums_equal_autograd():
         y.float().backward(gy)
         grads.append({n: p.grad.clone() for n, p in model.named_parameters() if p.grad is not None})
     torch.cuda.synchronize()
-    assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 100
-    for n in grads[0]:
-        assert torch.equal(grads[0][n], grads[1][n]), n
 
 
 def test_unet_forward_backward_vs_fakequant_emulation():
