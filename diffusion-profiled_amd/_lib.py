@@ -124,10 +124,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dpa_residual_scale_bwd_f32": (c_int, [c_void_p] * 3 + [c_int64, c_float, c_void_p]),
     "dpa_upsample_concat_f32": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p] + [c_int] * 6 + [c_void_p]),
     "dpa_upsample_concat_bwd_f32": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int] + [c_int] * 6 + [c_void_p]),
-    "dpa_upcat_gn_silu_fwd": (c_int, [c_void_p, c_void_p] + [c_int] * 5
+    "dpa_upcat_gn_silu_fwd": (c_int, [c_void_p, c_void_p] + [c_int] * 6
                               + [c_void_p] * 6 + [c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                                   c_void_p, c_int, c_int, c_float, c_void_p]),
-    "dpa_upcat_gn_silu_bwd": (c_int, [c_void_p, c_void_p] + [c_int] * 5 + [c_void_p] * 11
+    "dpa_upcat_gn_silu_bwd": (c_int, [c_void_p, c_void_p] + [c_int] * 6 + [c_void_p] * 11
                               + [c_int64, c_int, c_void_p]),
     "dpa_downsample2_f32": (c_int, [c_void_p, c_int, c_void_p] + [c_int] * 4 + [c_void_p]),
     "dpa_downsample2_bwd_f32": (c_int, [c_void_p, c_void_p, c_int] + [c_int] * 4 + [c_void_p]),

@@ -54,13 +54,15 @@ struct GnArgs {
   uint32_t* xb_part;   // fwd: with x_bf16, one amax partial of its bf16 values per workgroup
   // Two-source x (a decoder stage's first GroupNorm with the upsample-and-concatenate before
   // it, diffusion/unet.py:379-382): channels [0, cat_ca) are the 2x nearest upsampling of
-  // cat_a ([N][H/2][W/2][cat_ca]), the others cat_h ([N][H][W][C - cat_ca]), both bf16 (the
-  // concatenation is fp32, but holds these bf16 values exactly); images of cat_w columns.
+  // cat_a ([N][H/2][W/2][cat_ca], bf16), the others cat_h ([N][H][W][C - cat_ca], bf16 or
+  // fp32); the concatenation they replace is fp32 and holds exactly these values. Images of
+  // cat_w columns.
   const uint16_t* cat_a;
   const uint16_t* cat_h;
   int cat_ca, cat_w;
+  int cat_hf;        // cat_h (and its gradient) fp32 instead of bf16 (forms with an fp32 x)
   uint16_t* cat_ga;  // bwd: gradient of cat_a (each 2x2 window of dx summed), bf16
-  uint16_t* cat_gh;  // bwd: gradient of cat_h, bf16
+  void* cat_gh;      // bwd: gradient of cat_h, in cat_h's type
   // Producer-fused cast for a delayed-scaling consumer (chunked and small forms): instead of
   // the bf16 output (fwd) or bf16 dx (bwd), e4m3(bf16 value / *q_scale) goes to q, and each
   // workgroup leaves the amax of its bf16 values in q_part[workgroup] (count in *q_count)
@@ -1130,10 +1132,13 @@ __device__ __forceinline__ void res_load(const uint8_t* const (&src)[NL], const 
 }
 
 // Two-source x (GnArgs::cat_a / cat_h) of channels ch .. ch + 7 (all of them from one source:
-// cat_ca is a multiple of the slab), lane pl's pixels pl + PLN u as res_load's.
-template <int PLN, int U>
-__device__ __forceinline__ void cat_load(const GnArgs& p, int n, int ch, int pl, uint4 (&v)[1][U],
+// cat_ca is a multiple of the slab), lane pl's pixels pl + PLN u as res_load's. kF32: x as
+// fp32 bits in v[0] (channels 0-3) and v[1] (4-7), bf16 sources widened; else bf16 in v[0]
+// (cat_h bf16). kDout: dout of the pixel in v[NL - 1].
+template <int NL, int PLN, int U, bool kF32, bool kDout>
+__device__ __forceinline__ void cat_load(const GnArgs& p, int n, int ch, int pl, uint4 (&v)[NL][U],
                                          bool (&ok)[U], int (&pxs)[U]) {
+  static_assert(NL == (kF32 ? 2 : 1) + (kDout ? 1 : 0), "x parts and dout");
   const int W = p.cat_w, wl = W >> 1, ca = p.cat_ca;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -1141,6 +1146,13 @@ __device__ __forceinline__ void cat_load(const GnArgs& p, int n, int ch, int pl,
     ok[u] = px < p.HW;
     pxs[u] = ok[u] ? px : p.HW - 1;
   }
+  auto widen = [&](int u) __attribute__((always_inline)) {
+    if constexpr (kF32) {
+      const uint4 b = v[0][u];
+      v[0][u] = uint4{b.x << 16, b.x & 0xffff0000u, b.y << 16, b.y & 0xffff0000u};
+      v[1][u] = uint4{b.z << 16, b.z & 0xffff0000u, b.w << 16, b.w & 0xffff0000u};
+    }
+  };
   if (ch < ca) {
     const uint16_t* a = p.cat_a + (int64_t)n * (p.HW >> 2) * ca + ch;
 #pragma unroll
@@ -1148,17 +1160,39 @@ __device__ __forceinline__ void cat_load(const GnArgs& p, int n, int ch, int pl,
       const int y = pxs[u] / W, x = pxs[u] - y * W;
       v[0][u] = *reinterpret_cast<const uint4*>(a + ((y >> 1) * wl + (x >> 1)) * ca);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) widen(u);
   } else {
     const int chh = p.C - ca;
-    const uint16_t* h = p.cat_h + (int64_t)n * p.HW * chh + (ch - ca);
+    const int64_t off = (int64_t)n * p.HW * chh + (ch - ca);
+    bool f32 = false;
+    if constexpr (kF32) f32 = p.cat_hf != 0;
+    if (f32) {
+      const float* h = static_cast<const float*>(static_cast<const void*>(p.cat_h)) + off;
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[0][u] = *reinterpret_cast<const uint4*>(h + (int64_t)pxs[u] * chh);
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < (kF32 ? 2 : 1); ++k)
+          v[k][u] = *reinterpret_cast<const uint4*>(h + (int64_t)pxs[u] * chh + 4 * k);
+    } else {
+      const uint16_t* h = p.cat_h + off;
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[0][u] = *reinterpret_cast<const uint4*>(h + (int64_t)pxs[u] * chh);
+#pragma unroll
+      for (int u = 0; u < U; ++u) widen(u);
+    }
+  }
+  if constexpr (kDout) {
+    const uint16_t* d = p.dout + (int64_t)n * p.HW * p.C + ch;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      v[NL - 1][u] = *reinterpret_cast<const uint4*>(d + (int64_t)pxs[u] * p.C);
   }
 }
 
 template <int PLN, int U, bool kFilm, bool kF32, bool kDrop, bool kCat = false>
 __global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
-  static_assert(!kCat || !kF32, "the two sources are bf16");
+  static_assert(!kCat || PLN * U == 1024 || (kF32 && PLN * U == 256), "32x32 or 16x16 images");
   __shared__ uint32_t qred[PLN / 8];
   __shared__ float red[(PLN / 8) * 8 * 2];
   __shared__ float hs[16];
@@ -1172,10 +1206,10 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_fwd_kernel(const GnArgs p) {
   bool ok[U];
   int pxs[U];
   if constexpr (kCat)
-    cat_load<PLN, U>(p, n, ch, pl, v, ok, pxs);
+    cat_load<in.kN, PLN, U, kF32, false>(p, n, ch, pl, v, ok, pxs);
   else
     res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
-  if constexpr (kCat) {
+  if constexpr (kCat && !kF32) {
     // the bf16 copy of the concatenation is the loaded values themselves
     if (p.x_bf16) {
       us2 xacc = {0, 0};
@@ -1283,12 +1317,15 @@ struct GnResDout {
 
 template <int PLN, int U, bool kFilm, bool kF32, bool kDrop, bool kCat = false>
 __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
-  static_assert(!kCat || (!kF32 && PLN == 64 && U == 16), "bf16 sources, 32x32 images");
+  static_assert(!kCat || (!kF32 && PLN == 64 && U == 16) || (kF32 && PLN == 32 && U == 8),
+                "32x32 images (bf16 sources) or 16x16 (cat_h bf16 or fp32)");
   using DL = GnResDout<PLN, U>;
   __shared__ __attribute__((aligned(16))) uint8_t dls[DL::kBytes];
   __shared__ uint32_t qred[PLN / 8];
   __shared__ float red[(PLN / 8) * 8 * 16];
   __shared__ float hs[2][16];
+  // kCat without the dout copy in LDS: four pixel rows of the 2x2 window exchange
+  __shared__ __attribute__((aligned(16))) float xch[kCat && !DL::kLds ? 4 * (PLN / 4) * 8 * 16 : 4];
   const int n = blockIdx.y;
   const int c0 = blockIdx.x * kSlab;
   const int gq = threadIdx.x & 7;
@@ -1302,8 +1339,7 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
   bool ok[U];
   int pxs[U];
   if constexpr (kCat) {
-    static_assert(in.kN == 1, "dout in LDS");
-    cat_load<PLN, U>(p, n, ch, pl, v, ok, pxs);
+    cat_load<in.kN, PLN, U, kF32, !DL::kLds>(p, n, ch, pl, v, ok, pxs);
   } else {
     res_load<in.kN, PLN, U>(in.src, in.stride, pl, p.HW, v, ok, pxs);
   }
@@ -1403,15 +1439,22 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
   };
   if constexpr (kCat) {
     // The concatenation's fp32 gradient (plus the bf16 skip-path gradient, as autograd adds
-    // it), split as the upsample-and-concatenate's backward does: cat_h's channels rounded to
-    // bf16; cat_a's summed over each 2x2 window from zero in row-major order, then rounded
-    // (torch's upsample_nearest2d_backward). At 32x32, pixel pl + 64 u is row 2u + pl / 32,
-    // column pl % 32: window (u, j) holds lanes 2j, 2j + 1 (row 2u) and 2j + 32, 2j + 33 (row
-    // 2u + 1). The odd lane's value comes by a shuffle (8 threads on), the lower row's two
-    // through the dout slots of LDS already read, four pixels per exchange.
+    // it), split as the upsample-and-concatenate's backward does: cat_h's channels in
+    // cat_h's type (bf16: rounded); cat_a's summed over each 2x2 window from zero in
+    // row-major order, then rounded to bf16 (torch's upsample_nearest2d_backward). The
+    // images are PLN / 2 wide, so pixel pl + PLN u is row 2u + pl / kW, column pl mod kW:
+    // window (u, j) holds lanes 2j, 2j + 1 (row 2u) and 2j + kW, 2j + kW + 1 (row 2u + 1). The
+    // odd lane's value comes by a shuffle (8 threads on), the lower row's two through LDS
+    // (the dout slots already read, or an exchange buffer), four pixels per exchange.
+    constexpr int kW = PLN / 2;
+    constexpr int kEnt = (kW / 2) * 8 * 16;  // floats per pixel row pair: (window, granule) x 16
     const bool in_a = ch < p.cat_ca;  // workgroup-uniform
     const bool even = (pl & 1) == 0;
-    float* xs = reinterpret_cast<float*>(dls);
+    float* xs = DL::kLds ? reinterpret_cast<float*>(dls) : xch;
+    constexpr int kSlot = DL::kLds ? 8 * PLN * 4 : kEnt;  // floats between pixel rows u
+    static_assert(kEnt <= kSlot, "an exchange fits a dout slot");
+    bool hf = false;
+    if constexpr (kF32) hf = p.cat_hf != 0;
 #pragma unroll
     for (int u0 = 0; u0 < U; u0 += 4) {
       float t[4][8];
@@ -1427,28 +1470,35 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
           for (int e = 0; e < 8; ++e) t[k][e] += a[e];
         }
         if (!in_a) {
-          const int chh = p.C - p.cat_ca;
-          uint32_t o[4];
+          const int64_t o = ((int64_t)n * p.HW + pxs[u]) * (p.C - p.cat_ca) + (ch - p.cat_ca);
+          if (hf) {
+            float* gh = static_cast<float*>(p.cat_gh) + o;
 #pragma unroll
-          for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(t[k][e], t[k][e + 1]);
-          st_nt16(p.cat_gh + ((int64_t)n * p.HW + pxs[u]) * chh + (ch - p.cat_ca),
-                  uint4{o[0], o[1], o[2], o[3]});
+            for (int q4 = 0; q4 < 2; ++q4)
+              st_nt16(gh + 4 * q4, uint4{__float_as_uint(t[k][4 * q4]), __float_as_uint(t[k][4 * q4 + 1]),
+                                         __float_as_uint(t[k][4 * q4 + 2]), __float_as_uint(t[k][4 * q4 + 3])});
+          } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) w[e >> 1] = pack_bf16x2(t[k][e], t[k][e + 1]);
+            st_nt16(static_cast<uint16_t*>(p.cat_gh) + o, uint4{w[0], w[1], w[2], w[3]});
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (in_a) {
-        __syncthreads();  // every thread has read the dout slots u0 .. u0 + 3
+        __syncthreads();  // every thread has read the dout slots u0 .. u0 + 3 (or the buffer)
         float r[4][8];  // the odd neighbour's values (lane + 8: pixel lane pl + 1)
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
           for (int e = 0; e < 8; ++e) r[k][e] = __shfl_down(t[k][e], 8, 64);
-        // slot u0 + k, entry (window column j, granule gq): row 2u + 1's pair, 16 floats
-        const int ent = (((pl & 31) >> 1) * 8 + gq) * 16;
-        if (pl >= 32 && even) {
+        // row u0 + k, entry (window column j, granule gq): row 2u + 1's pair, 16 floats
+        const int ent = (((pl % kW) >> 1) * 8 + gq) * 16;
+        if (pl >= kW && even) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            float* e0 = xs + (u0 + k) * (8 * PLN * 4) + ent;
+            float* e0 = xs + (DL::kLds ? u0 + k : k) * kSlot + ent;
 #pragma unroll
             for (int q4 = 0; q4 < 2; ++q4) {
               *reinterpret_cast<v4f*>(e0 + 4 * q4) =
@@ -1459,10 +1509,10 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
           }
         }
         __syncthreads();
-        if (pl < 32 && even) {
+        if (pl < kW && even) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const float* e0 = xs + (u0 + k) * (8 * PLN * 4) + ent;
+            const float* e0 = xs + (DL::kLds ? u0 + k : k) * kSlot + ent;
             float acc[8];
 #pragma unroll
             for (int q4 = 0; q4 < 2; ++q4) {
@@ -1478,14 +1528,15 @@ __global__ __launch_bounds__(8 * PLN) void gn_res_bwd_kernel(const GnArgs p) {
                 acc[c] += hi[e];    // (2u + 1, 2j + 1)
               }
             }
-            uint32_t o[4];
+            uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) o[e >> 1] = pack_bf16x2(acc[e], acc[e + 1]);
-            const int wi = (u0 + k) * 16 + (pl >> 1);  // window row u0 + k, column pl / 2
+            for (int e = 0; e < 8; e += 2) w[e >> 1] = pack_bf16x2(acc[e], acc[e + 1]);
+            const int wi = (u0 + k) * (kW / 2) + (pl >> 1);  // window row u0 + k, column pl / 2
             st_nt16(p.cat_ga + ((int64_t)n * (p.HW >> 2) + wi) * p.cat_ca + ch,
-                    uint4{o[0], o[1], o[2], o[3]});
+                    uint4{w[0], w[1], w[2], w[3]});
           }
         }
+        // (the buffer's next writes come after the next four pixels' first barrier)
       }
     }
   } else {
@@ -2013,16 +2064,19 @@ extern "C" int dpa_gn_silu_bwd_fp8(const void* x, const void* dout, const float*
 }
 
 // ---- a decoder stage's first GroupNorm+SiLU fused with the upsample-and-concatenate before
-// it (diffusion/unet.py:379-382 and :151): x = cat([up2(a), h], channels), read from a and h
-// (both bf16, NHWC) instead of the fp32 concatenation; the backward writes the gradients of
-// a and h instead of the concatenation's. The resident form of 1024-pixel images only
-// (64 pixel lanes x 16 pixels, 2x2 windows per lane in the backward). ----
+// it (diffusion/unet.py:379-382 and :151): x = cat([up2(a), h], channels), read from a (bf16)
+// and h (bf16, or fp32 at 16x16), NHWC, instead of the fp32 concatenation; the backward
+// writes the gradients of a and h instead of the concatenation's. The resident forms of
+// 32x32 images (64 pixel lanes x 16 pixels, h bf16) and 16x16 images (32 x 8). ----
 
-static int upcat_gn_check(const void* a, const void* h, int N, int H, int W, int Ca, int Ch,
-                          int G) {
+static int upcat_gn_check(const void* a, const void* h, int h_dtype, int N, int H, int W,
+                          int Ca, int Ch, int G) {
   if (!a || !h) return DPA_ERR_NULL;
   if (N <= 0 || H <= 0 || W <= 0 || Ca <= 0 || Ch <= 0) return DPA_ERR_SIZE;
-  if (H != 32 || W != 32 || Ca % kSlab != 0 || Ch % kSlab != 0 ||
+  if (h_dtype != DPA_DTYPE_BF16 && h_dtype != DPA_DTYPE_F32) return DPA_ERR_SHAPE;
+  const bool s32 = H == 32 && W == 32 && h_dtype == DPA_DTYPE_BF16;
+  const bool s16 = H == 16 && W == 16;
+  if (!(s32 || s16) || Ca % kSlab != 0 || Ch % kSlab != 0 ||
       !gn_shape_ok(N, H * W, Ca + Ch, G))
     return DPA_ERR_SHAPE;
   if ((int64_t)N * H * W * (Ca + Ch) > 0x7fffffffLL) return DPA_ERR_SIZE;
@@ -2030,13 +2084,14 @@ static int upcat_gn_check(const void* a, const void* h, int N, int H, int W, int
   return DPA_OK;
 }
 
-extern "C" int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int N, int H, int W, int Ca,
-                                     int Ch, const float* gamma, const float* beta, void* out,
-                                     void* q, const float* q_scale, uint32_t* q_partials,
+extern "C" int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int h_dtype, int N, int H,
+                                     int W, int Ca, int Ch, const float* gamma,
+                                     const float* beta, void* out, void* q,
+                                     const float* q_scale, uint32_t* q_partials,
                                      int q_partials_cap, uint32_t* q_count, float* mean,
                                      float* rstd, void* x_bf16, uint32_t* xb_partials,
                                      int xb_partials_cap, int G, float eps, void* stream) {
-  const int st0 = upcat_gn_check(a, h, N, H, W, Ca, Ch, G);
+  const int st0 = upcat_gn_check(a, h, h_dtype, N, H, W, Ca, Ch, G);
   if (st0 != DPA_OK) return st0;
   if (!gamma || !beta || !mean || !rstd || (!out && !q)) return DPA_ERR_NULL;
   if (out && q) return DPA_ERR_SHAPE;  // one output: bf16 or e4m3
@@ -2049,6 +2104,7 @@ extern "C" int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int N, int H,
   g.cat_h = (const uint16_t*)h;
   g.cat_ca = Ca;
   g.cat_w = W;
+  g.cat_hf = h_dtype == DPA_DTYPE_F32;
   g.gamma = gamma;
   g.beta = beta;
   g.out = out;
@@ -2068,17 +2124,21 @@ extern "C" int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int N, int H,
     g.out = q;  // not written: the kernel stores through g.q
   }
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  gn_res_fwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, (hipStream_t)stream>>>(g);
+  hipStream_t s = (hipStream_t)stream;
+  if (H == 32)
+    gn_res_fwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, s>>>(g);
+  else
+    gn_res_fwd_kernel<32, 8, false, true, false, true><<<grid, 8 * 32, 0, s>>>(g);
   return launch_status();
 }
 
-extern "C" int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int N, int H, int W, int Ca,
-                                     int Ch, const void* dout, const float* gamma,
+extern "C" int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int h_dtype, int N, int H,
+                                     int W, int Ca, int Ch, const void* dout, const float* gamma,
                                      const float* beta, const float* mean, const float* rstd,
                                      const void* dx_add, void* ga, void* gh, float* dgamma,
                                      float* dbeta, void* workspace, int64_t workspace_bytes,
                                      int G, void* stream) {
-  const int st0 = upcat_gn_check(a, h, N, H, W, Ca, Ch, G);
+  const int st0 = upcat_gn_check(a, h, h_dtype, N, H, W, Ca, Ch, G);
   if (st0 != DPA_OK) return st0;
   if (!dout || !gamma || !beta || !mean || !rstd || !ga || !gh || !dgamma || !dbeta)
     return DPA_ERR_NULL;
@@ -2093,8 +2153,9 @@ extern "C" int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int N, int H,
   g.cat_h = (const uint16_t*)h;
   g.cat_ca = Ca;
   g.cat_w = W;
+  g.cat_hf = h_dtype == DPA_DTYPE_F32;
   g.cat_ga = (uint16_t*)ga;
-  g.cat_gh = (uint16_t*)gh;
+  g.cat_gh = gh;
   g.dout = (const uint16_t*)dout;
   g.gamma = gamma;
   g.beta = beta;
@@ -2106,7 +2167,10 @@ extern "C" int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int N, int H,
   g.N = N; g.HW = HW; g.C = C; g.G = G; g.cpg = C / G; g.eps = 0.f;
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)(C / kSlab), (unsigned)N);
-  gn_res_bwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, s>>>(g);
+  if (H == 32)
+    gn_res_bwd_kernel<64, 16, false, false, false, true><<<grid, 8 * 64, 0, s>>>(g);
+  else
+    gn_res_bwd_kernel<32, 8, false, true, false, true><<<grid, 8 * 32, 0, s>>>(g);
   int st = launch_status();
   if (st != DPA_OK) return st;
   gn_param_reduce_kernel<<<(unsigned)ceil_div(C, 64), 64 * kPrSlices, 0, s>>>(

@@ -289,24 +289,28 @@ def group_norm_silu_tee(x, gamma, beta, groups: int, eps: float = 1e-5, skip_bf1
 
 def upcat_ok(a: torch.Tensor, h: torch.Tensor, up: bool) -> bool:
     """Whether cat([up2(a), h], 1) can feed the fused upsample-and-concatenate GroupNorm
-    (dpa_upcat_gn_silu_fwd): both bf16 channels-last on the GPU, 1024-pixel images, channel
-    counts multiples of 64."""
+    (dpa_upcat_gn_silu_fwd): channels-last on the GPU, a bf16, 32x32 images with h bf16 or
+    16x16 images with h bf16 or fp32, channel counts multiples of 64."""
     cl = torch.channels_last
     if not (up and a.is_cuda and h.is_cuda and a.dtype == torch.bfloat16
-            and h.dtype == torch.bfloat16 and a.ndim == 4 and h.ndim == 4):
+            and h.dtype in (torch.bfloat16, torch.float32) and a.ndim == 4 and h.ndim == 4):
         return False
     n, ca, ha, wa = a.shape
     nh, ch, hh, wh = h.shape
-    return (n == nh and hh == 2 * ha and wh == 2 * wa and hh * wh == 1024 and ca % 64 == 0
+    size_ok = (hh == wh == 32 and h.dtype == torch.bfloat16) or hh == wh == 16
+    return (n == nh and hh == 2 * ha and wh == 2 * wa and size_ok and ca % 64 == 0
             and ch % 64 == 0 and a.is_contiguous(memory_format=cl)
             and h.is_contiguous(memory_format=cl) and a.data_ptr() % 16 == 0
             and h.data_ptr() % 16 == 0)
 
 
+_DT_H = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+
+
 class UpcatGroupNormSiLUTee(torch.autograd.Function):
     """GroupNormSiLUTee on x = cat([up2(a), h], 1), the fp32 decoder-stage input of
     diffusion/unet.py:379-382, with skip_bf16: (silu(GroupNorm(x)), x.to(bfloat16)). The
-    kernels read a and h (bf16) where x would be read, so the fp32 concatenation is never
+    kernels read a and h where x would be read, so the fp32 concatenation is never
     formed; the backward returns the gradients of a and h that the upsample-and-concatenate's
     backward would form from the GroupNorm's fp32 dx plus the bf16 skip-path gradient. Every
     output and gradient is bit-identical to upsample_concat followed by GroupNormSiLUTee."""
@@ -334,8 +338,8 @@ class UpcatGroupNormSiLUTee(torch.autograd.Function):
             q = torch.empty((n, c, hh, wh), device=a.device, dtype=FP8_DTYPE, memory_format=cl)
             qargs = (hand.scale.data_ptr(), hand.partials.data_ptr(), hand.partials.numel(),
                      hand.count.data_ptr())
-        _lib.call("dpa_upcat_gn_silu_fwd", a.data_ptr(), h.data_ptr(), n, hh, wh, ca, ch,
-                  g32.data_ptr(), b32.data_ptr(), p(out), p(q), *qargs, mean.data_ptr(),
+        _lib.call("dpa_upcat_gn_silu_fwd", a.data_ptr(), h.data_ptr(), _DT_H[h.dtype], n, hh,
+                  wh, ca, ch, g32.data_ptr(), b32.data_ptr(), p(out), p(q), *qargs, mean.data_ptr(),
                   rstd.data_ptr(), x16.data_ptr(), p(xbp), 0 if xbp is None else xbp.numel(),
                   groups, float(eps), _stream(a))
         if xbp is not None:
@@ -365,8 +369,8 @@ class UpcatGroupNormSiLUTee(torch.autograd.Function):
         dbeta = torch.empty(c, device=a.device, dtype=torch.float32)
         ws_bytes = 2 * n * c * 4
         ws = torch.empty(ws_bytes, device=a.device, dtype=torch.uint8)
-        _lib.call("dpa_upcat_gn_silu_bwd", a.data_ptr(), h.data_ptr(), n, hh, wh, ca, ch,
-                  dout.data_ptr(), gamma.float().contiguous().data_ptr(),
+        _lib.call("dpa_upcat_gn_silu_bwd", a.data_ptr(), h.data_ptr(), _DT_H[h.dtype], n, hh,
+                  wh, ca, ch, dout.data_ptr(), gamma.float().contiguous().data_ptr(),
                   beta.float().contiguous().data_ptr(), mean.data_ptr(), rstd.data_ptr(),
                   None if add is None else add.data_ptr(), ga.data_ptr(), gh.data_ptr(),
                   dgamma.data_ptr(), dbeta.data_ptr(), ws.data_ptr(), ws_bytes, ctx.groups,

@@ -644,30 +644,31 @@ int dpa_upsample_concat_bwd_f32(const float* gy, void* ga, int a_dtype, void* gh
 
 /* A decoder stage's first GroupNorm+SiLU with the upsample-and-concatenate before it
  * (diffusion/unet.py:379-382 with :151; no counterpart op in the reference): x =
- * cat([up2(a), h], channels) read from a ([N][H/2][W/2][Ca]) and h ([N][H][W][Ch]), both bf16
- * NHWC, instead of from the fp32 concatenation (which holds those bf16 values exactly), so
- * neither the concatenation nor its gradient is written. Outputs as dpa_gn_silu_fwd_fp8_amax
- * for an fp32 x: out (bf16 [N][H][W][C], C = Ca + Ch) or, instead, the e4m3 hand-off q
- * (q_scale, q_partials, q_count as there); x_bf16 (optional) the bf16 concatenation, with one
- * amax partial per workgroup in xb_partials (optional); mean / rstd [N][G]. H * W = 1024
- * (the resident form), H and W even, Ca and Ch multiples of 64; no FiLM, no dropout.
- * Bit-identical to dpa_upsample_concat_f32 followed by the GroupNorm on its fp32 result. */
-int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int N, int H, int W, int Ca, int Ch,
-                          const float* gamma, const float* beta, void* out, void* q,
-                          const float* q_scale, uint32_t* q_partials, int q_partials_cap,
-                          uint32_t* q_count, float* mean, float* rstd, void* x_bf16,
-                          uint32_t* xb_partials, int xb_partials_cap, int G, float eps,
-                          void* stream);
+ * cat([up2(a), h], channels) read from a ([N][H/2][W/2][Ca], bf16) and h ([N][H][W][Ch],
+ * h_dtype: DPA_DTYPE_BF16, or DPA_DTYPE_F32 at 16x16), NHWC, instead of from the fp32
+ * concatenation (which holds exactly those values), so neither the concatenation nor its
+ * gradient is written. Outputs as dpa_gn_silu_fwd_fp8_amax for an fp32 x: out (bf16
+ * [N][H][W][C], C = Ca + Ch) or, instead, the e4m3 hand-off q (q_scale, q_partials, q_count
+ * as there); x_bf16 (optional) the bf16 concatenation, with one amax partial per workgroup in
+ * xb_partials (optional); mean / rstd [N][G]. H = W = 32 (h bf16) or 16, Ca and Ch multiples
+ * of 64; no FiLM, no dropout. Bit-identical to dpa_upsample_concat_f32 followed by the
+ * GroupNorm on its fp32 result. */
+int dpa_upcat_gn_silu_fwd(const void* a, const void* h, int h_dtype, int N, int H, int W,
+                          int Ca, int Ch, const float* gamma, const float* beta, void* out,
+                          void* q, const float* q_scale, uint32_t* q_partials,
+                          int q_partials_cap, uint32_t* q_count, float* mean, float* rstd,
+                          void* x_bf16, uint32_t* xb_partials, int xb_partials_cap, int G,
+                          float eps, void* stream);
 /* Its backward: the concatenation's gradient (the GroupNorm's fp32 dx plus dx_add, a bf16
  * gradient of the concatenation from its other reader, the 1x1 skip conv, or NULL) goes
  * straight to ga (bf16, a's shape: each 2x2 window summed from zero in row-major order) and
- * gh (bf16, h's shape), as dpa_upsample_concat_bwd_f32 splits it; dgamma, dbeta as
+ * gh (h's dtype and shape), as dpa_upsample_concat_bwd_f32 splits it; dgamma, dbeta as
  * dpa_gn_silu_bwd_ex (workspace of 2 N C floats). */
-int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int N, int H, int W, int Ca, int Ch,
-                          const void* dout, const float* gamma, const float* beta,
-                          const float* mean, const float* rstd, const void* dx_add, void* ga,
-                          void* gh, float* dgamma, float* dbeta, void* workspace,
-                          int64_t workspace_bytes, int G, void* stream);
+int dpa_upcat_gn_silu_bwd(const void* a, const void* h, int h_dtype, int N, int H, int W,
+                          int Ca, int Ch, const void* dout, const float* gamma,
+                          const float* beta, const float* mean, const float* rstd,
+                          const void* dx_add, void* ga, void* gh, float* dgamma, float* dbeta,
+                          void* workspace, int64_t workspace_bytes, int G, void* stream);
 
 /* Encoder downsampling F.interpolate(a, scale_factor=0.5, mode="nearest") under autocast
  * (diffusion/unet.py:370-373): y[n][i][j][c] = a[n][2i][2j][c] as fp32; a [N][H][W][C] bf16

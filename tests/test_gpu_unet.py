@@ -275,8 +275,8 @@ def _fp8_site_active(m, x) -> bool:
 def test_unet_fused_gradient_sums_equal_autograd():
     """The skip-gradient sums fused into kernels (the encoder activations' two gradients
     inside the downsampling's backward, the attention block input's inside the LayerNorm
-    backward) and the 32x32 decoder stage's upsample-and-concatenate read by its first
-    GroupNorm change no bit of the U-Net's gradients: cfg5's model at batch 2 (current
+    backward) and the 32x32 and 16x16 decoder stages' upsample-and-concatenate read by their
+    first GroupNorm change no bit of the U-Net's gradients: cfg5's model at batch 2 (current
     scaling, dropout off), forward + backward under autocast with the fused forms and with
     autograd's own accumulation on the formed concatenation."""
     torch.manual_seed(5)
@@ -300,7 +300,7 @@ def test_unet_fused_gradient_sums_equal_autograd():
         _fused_vs_autograd_grads(model, x, t, gy, grads)
     finally:
         del G.UpcatGroupNormSiLUTee.apply
-    assert len(calls) == 1  # the fused pass took the fused concatenation once (32x32 stage)
+    assert len(calls) == 2  # the fused pass took the fused concatenation at 32x32 and 16x16
     assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 100
     for n in grads[0]:
         assert torch.equal(grads[0][n], grads[1][n]), n

@@ -21,10 +21,13 @@ G = dpa_mod("gn_silu")
 R = dpa_mod("residual")
 
 CASES = [
-    # (n, channels of a (upsampled from 16x16), channels of h (32x32))
-    (3, 256, 256),   # the U-Net's 32x32 decoder stage: 256 + 256
-    (2, 128, 384),
-    (2, 64, 64),     # C = 128: four channels per group
+    # (n, channels of a (upsampled), channels of h, image side, h fp32)
+    (3, 256, 256, 32, False),   # the U-Net's 32x32 decoder stage: 256 + 256, bf16
+    (2, 128, 384, 32, False),
+    (2, 64, 64, 32, False),     # C = 128: four channels per group
+    (3, 256, 256, 16, True),    # the 16x16 stage: a bf16, h fp32
+    (2, 128, 384, 16, True),
+    (2, 128, 128, 16, False),   # h bf16 at 16x16
 ]
 
 
@@ -32,15 +35,16 @@ def cl(t):
     return t.cuda().contiguous(memory_format=torch.channels_last)
 
 
-def inputs(n, ca, ch, seed):
+def inputs(n, ca, ch, seed, side=32, h32=False):
     g = torch.Generator().manual_seed(seed)
-    a = cl((torch.randn((n, ca, 16, 16), generator=g) * 1.5 + 0.3).to(torch.bfloat16))
-    h = cl((torch.randn((n, ch, 32, 32), generator=g) * 0.7 - 0.2).to(torch.bfloat16))
+    a = cl((torch.randn((n, ca, side // 2, side // 2), generator=g) * 1.5 + 0.3).to(torch.bfloat16))
+    h = torch.randn((n, ch, side, side), generator=g) * 0.7 - 0.2
+    h = cl(h if h32 else h.to(torch.bfloat16))
     c = ca + ch
     gamma = (1.0 + 0.2 * torch.randn(c, generator=g)).cuda()
     beta = (0.1 * torch.randn(c, generator=g)).cuda()
-    dout = cl((1e-2 * torch.randn((n, c, 32, 32), generator=g)).to(torch.bfloat16))
-    dskip = cl((1e-2 * torch.randn((n, c, 32, 32), generator=g)).to(torch.bfloat16))
+    dout = cl((1e-2 * torch.randn((n, c, side, side), generator=g)).to(torch.bfloat16))
+    dskip = cl((1e-2 * torch.randn((n, c, side, side), generator=g)).to(torch.bfloat16))
     return a, h, gamma, beta, dout, dskip
 
 
@@ -62,9 +66,9 @@ def run(fused: bool, a, h, gamma, beta, dout, dskip, hand=None):
     return y, x16, parts, a.grad, h.grad, gamma.grad, beta.grad
 
 
-@pytest.mark.parametrize("n,ca,ch", CASES, ids=lambda v: str(v))
-def test_upcat_gn_equals_upsample_concat_then_gn(n, ca, ch):
-    a, h, gamma, beta, dout, dskip = inputs(n, ca, ch, seed=n * 7 + ca + ch)
+@pytest.mark.parametrize("n,ca,ch,side,h32", CASES, ids=lambda v: str(v))
+def test_upcat_gn_equals_upsample_concat_then_gn(n, ca, ch, side, h32):
+    a, h, gamma, beta, dout, dskip = inputs(n, ca, ch, n * 7 + ca + ch + side, side, h32)
     got = run(True, a, h, gamma, beta, dout, dskip)
     ref = run(False, a, h, gamma, beta, dout, dskip)
     names = ["y", "x16", "x16 amax partials", "grad a", "grad h", "dgamma", "dbeta"]
@@ -78,12 +82,13 @@ def test_upcat_gn_equals_upsample_concat_then_gn(n, ca, ch):
     assert not torch.equal(bare[3], got[3]) and not torch.equal(bare[4], got[4])
 
 
-def test_upcat_gn_fp8_handoff_equals_unfused():
+@pytest.mark.parametrize("side,h32", [(32, False), (16, True)], ids=lambda v: str(v))
+def test_upcat_gn_fp8_handoff_equals_unfused(side, h32):
     """With conv_1's delayed-scaling hand-off the forward writes e4m3(y / scale) and the amax
     partials of y instead of y: the same bytes and partials as the unfused GroupNorm's
     hand-off on the fp32 concatenation."""
     n, ca, ch = 2, 256, 256
-    a, h, gamma, beta, dout, dskip = inputs(n, ca, ch, seed=11)
+    a, h, gamma, beta, dout, dskip = inputs(n, ca, ch, 11, side, h32)
 
     def hand(scale):
         return K.Fp8Handoff(torch.tensor(scale, device="cuda", dtype=torch.float32),
@@ -106,15 +111,18 @@ def test_upcat_gn_fp8_handoff_equals_unfused():
 def test_upcat_gn_refuses_other_shapes():
     """Sizes without the fused form: the checker says no, the entry point refuses."""
     L = dpa_mod("_lib")
-    a = cl(torch.zeros((1, 64, 8, 8), dtype=torch.bfloat16))
-    h = cl(torch.zeros((1, 64, 16, 16), dtype=torch.bfloat16))
-    assert not G.upcat_ok(a, h, True)            # 256-pixel images
+    a = cl(torch.zeros((1, 64, 4, 4), dtype=torch.bfloat16))
+    h = cl(torch.zeros((1, 64, 8, 8), dtype=torch.bfloat16))
+    assert not G.upcat_ok(a, h, True)            # 64-pixel images
     assert not G.upcat_ok(cl(torch.zeros((1, 64, 16, 16), dtype=torch.bfloat16)),
                           cl(torch.zeros((1, 64, 32, 32), dtype=torch.float32)), True)
+    assert not G.upcat_ok(cl(torch.zeros((1, 64, 8, 8), dtype=torch.float32)),
+                          cl(torch.zeros((1, 64, 16, 16), dtype=torch.float32)), True)
     assert not G.upcat_ok(a, h, False)
     dummy = torch.zeros(1 << 20, device="cuda", dtype=torch.float32)
     p = dummy.data_ptr()
-    st = L.load().dpa_upcat_gn_silu_fwd(a.data_ptr(), h.data_ptr(), 1, 16, 16, 64, 64, p, p, p,
-                                        None, None, None, 0, None, p, p, None, None, 0, GROUPS,
-                                        1e-5, None)
-    assert st == -4  # DPA_ERR_SHAPE
+    for hd, side in ((0, 8), (1, 32)):  # 8x8 images; an fp32 h at 32x32
+        st = L.load().dpa_upcat_gn_silu_fwd(a.data_ptr(), h.data_ptr(), hd, 1, side, side, 64,
+                                            64, p, p, p, None, None, None, 0, None, p, p, None,
+                                            None, 0, GROUPS, 1e-5, None)
+        assert st == -4  # DPA_ERR_SHAPE
