@@ -103,6 +103,18 @@ __device__ __forceinline__ uint32_t drop_keep8(uint64_t seed, int64_t idx0, uint
   return bits;
 }
 
+// v * scale if bit e of the keep bits is set, else +0: the selection as a mask of the bit
+// (v_bfe_i32 gives 0 or all ones) and'ed into the product, so no per-element lane mask is
+// formed (in the backward, which keeps each pixel's keep bits for both passes, those masks
+// took 2 scalar registers per element and were spilled to vector lanes: ~700 v_readlane /
+// v_writelane per thread in the 1024-pixel form)
+__device__ __forceinline__ float drop_sel(float v, uint32_t keep, int e, float scale) {
+  uint32_t m;
+  // (as an instruction of its own: the compiler would turn the and back into a select)
+  asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(m) : "v"(keep), "i"(e));
+  return __uint_as_float(__float_as_uint(v * scale) & m);
+}
+
 // sigmoid(v) = 1 / (1 + e^-v) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32,
 // about 1 ulp each), e^-v = 2^(-v log2 e). The SiLU and its derivative are rounded to bf16
 // (2^16 fp32 ulps), so this changes an output bit only at rounding ties; the IEEE-exact
@@ -912,7 +924,7 @@ __device__ __forceinline__ void bwd_dout_kb(uint4 v, uint32_t kb, float drop_sca
   unpack8(v, d);
   if (kDrop) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d[e] = (kb >> e) & 1u ? d[e] * drop_scale : 0.0f;
+    for (int e = 0; e < 8; ++e) d[e] = drop_sel(d[e], kb, e, drop_scale);
   }
 }
 
