@@ -341,6 +341,13 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
     for (int kb = 0; kb < KB; ++kb) dvt[hb][kb] = dkt[hb][kb] = v4f{0.f, 0.f, 0.f, 0.f};
   __syncthreads();  // Q, K, dO rows, lse and D complete
 
+  // the K^T operand of this wave's dQ block (dims 16 (wave & 3) ..) over all keys: the same
+  // for every query block, so read once
+  uint4 ktf[LP / 32];
+#pragma unroll
+  for (int kk = 0; kk < LP / 32; ++kk)
+    ktf[kk] = frag_tr(ks, 32 * kk + 8 * fq, 32 * kk + 8 * fq + 4, 16 * (wave & 3), frow);
+
   // A fragments of a query block: rows q0 + 16 sub + frow of Q and dO (read one block ahead,
   // during the previous block's dQ products)
   uint4 qa[2][2], da[2][2];
@@ -357,8 +364,29 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
   if (kact) load_a(0);
 
   us2 am = {0, 0};
+  // dQ^T block (dims 16 hb .., queries 16 sub ..) of the query block at q0 over all keys, from
+  // that block's dS in LDS, in two interleaved accumulators (a shorter dependent chain)
+  auto dq_block = [&](int q0, const uint16_t* ds) __attribute__((always_inline)) {
+    const int hb = wave & 3, sub = wave >> 2;
+    v4f acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kk = 0; kk < LP / 32; ++kk)
+      acc2[kk & 1] = mfma16x16x32_bf16(ktf[kk], ld16(ds + (16 * sub + frow) * TP + 32 * kk + 8 * fq),
+                                       acc2[kk & 1]);
+    const v4f acc = acc2[0] + acc2[1];
+    const int q = q0 + 16 * sub + frow;
+    if (q < L)
+      *reinterpret_cast<uint2*>(dqg + q * S3 + 16 * hb + 4 * fq) =
+          att_pack4(acc[0] * kAttScale, acc[1] * kAttScale, acc[2] * kAttScale,
+                    acc[3] * kAttScale, am);
+  };
+  // Block i's dQ runs in step i + 1, before that step's barrier: every wave has its own
+  // products of the next block to issue instead of waiting at the barrier, and dS(i)'s buffer
+  // is only rewritten (by block i + 2) after barrier i + 1.
+  int q_last = 0;
   for (int q0 = 0, blk = 0; q0 < L; q0 += 32, ++blk) {
     uint16_t* ds = dsb[blk & 1];
+    q_last = q0;
     if (kact) {
       uint4 pb[KB], sb[KB];
 #pragma unroll
@@ -405,26 +433,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs p) {
         }
       }
     }
+    if (blk > 0) dq_block(q0 - 32, dsb[(blk - 1) & 1]);
     __syncthreads();  // this block's dS complete
     if (kact && q0 + 32 < L) load_a(q0 + 32);
-
-    // dQ^T block (dims 16 hb .., queries 16 sub ..) over all keys, in two interleaved
-    // accumulators (a shorter dependent chain), added at the end
-    {
-      const int hb = wave & 3, sub = wave >> 2;
-      v4f acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-      for (int kk = 0; kk < LP / 32; ++kk)
-        acc2[kk & 1] = mfma16x16x32_bf16(frag_tr(ks, 32 * kk + 8 * fq, 32 * kk + 8 * fq + 4, 16 * hb, frow),
-                                         ld16(ds + (16 * sub + frow) * TP + 32 * kk + 8 * fq), acc2[kk & 1]);
-      const v4f acc = acc2[0] + acc2[1];
-      const int q = q0 + 16 * sub + frow;
-      if (q < L)
-        *reinterpret_cast<uint2*>(dqg + q * S3 + 16 * hb + 4 * fq) =
-            att_pack4(acc[0] * kAttScale, acc[1] * kAttScale, acc[2] * kAttScale,
-                      acc[3] * kAttScale, am);
-    }
   }
+  dq_block(q_last, dsb[((L + 31) / 32 - 1) & 1]);
 
   // dK, dV of this wave's keys: lane holds dims 16 hb + 4 fq + t of key kw0 + 16 kb + frow
   if (kact) {
