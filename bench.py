@@ -117,13 +117,18 @@ class ConvWorkload:
         x's amax and cast launches (two launches for x and the weight, in place of
         quantize_fp8's two per tensor and the transpose); for the halo-patch kernel's shapes
         both copies are written in its fragment layouts."""
-        K = self.K
+        self.quantize_xw()
+        self.quantize_dy()
+
+    def quantize_xw(self):
         if self.wprep is None:
             WP = importlib.import_module("diffusion-profiled_amd.weight_prep")
             self.wprep = WP.TensorPrep([self.wt], frag=[self.frag])
         self.xq, self.xs = self.wprep.run_with_quantize(self.x)
         self.wq, self.wq_t, self.ws = self.wprep.q[0], self.wprep.qt[0], self.wprep.scale(0)
-        self.dyq, self.dys = K.quantize_fp8(self.dy)
+
+    def quantize_dy(self):
+        self.dyq, self.dys = self.K.quantize_fp8(self.dy)
 
     @property
     def frag(self):
@@ -147,8 +152,11 @@ class ConvWorkload:
                                                self.stride, self.pad)
 
     def step(self):
-        self.quantize()
+        """In the order of the reference's autograd Function (diffusion/fp8_kernels.py:823-913):
+        x and w quantized, forward; then dy quantized, data and weight gradients."""
+        self.quantize_xw()
         self.fwd()
+        self.quantize_dy()
         self.dgrad()
         self.wgrad()
 
@@ -177,7 +185,7 @@ class ConvWorkload:
             "batch": self.n, "cin": self.cin, "cout": self.cout, "h": self.h, "w": self.w,
             "kernel": self.k, "stride": self.stride, "pad": self.pad,
             "layout": "NHWC activations, OHWI weights, e4m3 per-tensor current scaling",
-            "step": "quantize x,w,dy + conv fwd + dgrad + wgrad",
+            "step": "quantize x,w + conv fwd + quantize dy + dgrad + wgrad",
         }
 
 
